@@ -1,0 +1,181 @@
+/*
+ * ssdq.h — C ABI of libssdq.so, the MI355X (gfx950) quantized compute path
+ * for the ssd-llm inference engine.
+ *
+ * Replaces the kernel-dispatch surface that src/inference calls in place of
+ * src/metal (MetalCompute, src/metal/compute.rs:29-373; MetalGpu,
+ * src/metal/gpu.rs:71-1258) for:
+ *   - GGUF block dequantization (Q4_0, Q8_0, Q4_K, Q6_K) fused into matvec /
+ *     small-batch matmul and the batched prefill GEMM,
+ *   - INT8 per-row KV-cache quantize / dequantize and the paged append,
+ *   - single-query GQA decode attention over f32 or paged INT8 KV.
+ *
+ * Conventions
+ *   - Every function returns an int status: SSDQ_OK (0), a negative
+ *     SSDQ_ERR_* code, or SSDQ_WARN_UNSUPPORTED_ZEROED (1) when the reference
+ *     would have returned zeros for an unsupported dtype (the output is then
+ *     zero-filled, compute.rs:672-675). ssdq_last_error() describes the last
+ *     failure on the calling thread. No C++ exception crosses this boundary.
+ *   - "dev" functions take device pointers and a stream (a hipStream_t, NULL
+ *     for the default stream); they only enqueue work and return at once.
+ *   - "host" functions take host pointers, copy in, compute, copy out and
+ *     return when the result is in place: the synchronous, allocate-per-call
+ *     contract of MetalCompute (gpu.rs:492-535), on a context that is created
+ *     once (not per forward pass, unlike transformer.rs:301-302).
+ *   - dtype uses the GgmlType numeric ids of src/model/gguf.rs:17-48.
+ *   - Sizes are element counts unless named *_bytes.
+ */
+#ifndef SSDQ_H
+#define SSDQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SSDQ_ABI_VERSION 1
+
+/* status codes */
+#define SSDQ_OK 0
+#define SSDQ_WARN_UNSUPPORTED_ZEROED 1
+#define SSDQ_ERR_INVALID_ARG (-1)
+#define SSDQ_ERR_UNSUPPORTED (-2)
+#define SSDQ_ERR_HIP (-3)
+#define SSDQ_ERR_NO_DEVICE (-4)
+#define SSDQ_ERR_OUT_OF_MEMORY (-5)
+
+/* GgmlType ids, src/model/gguf.rs:17-48 */
+#define SSDQ_TYPE_F32 0
+#define SSDQ_TYPE_F16 1
+#define SSDQ_TYPE_Q4_0 2
+#define SSDQ_TYPE_Q8_0 8
+#define SSDQ_TYPE_Q4_K 12
+#define SSDQ_TYPE_Q6_K 14
+#define SSDQ_TYPE_BF16 30
+
+typedef void* ssdq_stream_t; /* a hipStream_t; NULL = default stream */
+typedef struct ssdq_ctx ssdq_ctx;
+
+/* ---------------------------------------------------------------- library */
+int ssdq_abi_version(void);
+/* Message of the last failing call on this thread ("" if none). */
+const char* ssdq_last_error(void);
+/* GgmlType::block_size / type_size, src/model/gguf.rs:87-135 (0 if unknown). */
+size_t ssdq_block_size(int dtype);
+size_t ssdq_type_size(int dtype);
+/* Bytes of one weight row of in_dim elements: (in_dim / block) * type_size,
+ * the row stride matvec_*_cpu uses (compute.rs:683-688). */
+size_t ssdq_row_bytes(int dtype, size_t in_dim);
+
+/* ---------------------------------------------------------------- context */
+/* Replaces MetalCompute::new() -> Option<Self> (compute.rs:47-71): fails with
+ * SSDQ_ERR_NO_DEVICE when no GPU is usable, where the caller keeps its CPU
+ * path. `device` is a HIP device ordinal (-1: the current device). */
+int ssdq_ctx_create(int device, ssdq_ctx** out);
+void ssdq_ctx_destroy(ssdq_ctx* ctx);
+/* MetalCompute::has_gpu (compute.rs:262-264) */
+int ssdq_ctx_device(const ssdq_ctx* ctx);
+
+/* --------------------------------------------------- dequant (bit-exact) */
+/* Device dequantization of n_elements into f32, element values bit-identical
+ * to the reference: dequantize_q4_0 / q8_0 / q6_k (src/ssd/streamer.rs:128-220)
+ * and the Q4_K values of matvec_q4_k_cpu (compute.rs:716-744; the reference's
+ * loader has no Q4_K path and returns zeros, streamer.rs:119-123). Elements past
+ * the last whole block are zero (streamer.rs `output.resize`). Replaces
+ * dequantize_to_f32 (streamer.rs:93-125) for quantized types. */
+int ssdq_dequant_dev(int dtype, const void* w, size_t n_elements, float* out,
+                     ssdq_stream_t stream);
+
+/* ---------------------------------------------------------------- matvec */
+/* y[b, r] = sum_k dequant(W)[r, k] * x[b, k] for b < batch, r < out_dim, over
+ * the (in_dim / block) whole blocks of each row.  W is out_dim rows of
+ * ssdq_row_bytes(dtype, in_dim) bytes in the reference's GGUF block layout;
+ * x is [batch, in_dim] f32, y is [batch, out_dim] f32.
+ * Replaces MetalCompute::matvec_quantized (compute.rs:157-191), MetalGpu::
+ * matvec_q4_0/q4_k/q6_k/q8_0 (gpu.rs:396-428) and matvec_quantized_cpu
+ * (compute.rs:648-677); batch > 1 replaces the per-row loop of
+ * batch_scheduler.rs:242-276. Unsupported dtypes zero-fill y and return
+ * SSDQ_WARN_UNSUPPORTED_ZEROED. */
+int ssdq_matvec_dev(int dtype, const void* w, const float* x, float* y, size_t out_dim,
+                    size_t in_dim, size_t batch, ssdq_stream_t stream);
+/* Host twin with the MetalCompute::matvec_quantized contract
+ * (compute.rs:157-191): w_len bytes of raw blocks, x_len floats, y gets out_dim
+ * floats. Synchronous. */
+int ssdq_matvec_quantized(ssdq_ctx* ctx, const uint8_t* w_raw, size_t w_len, const float* x,
+                          size_t x_len, size_t out_dim, size_t in_dim, int dtype, float* y);
+
+/* ------------------------------------------------------- prefill GEMM */
+/* Y[M, N] f32 = X[M, K] bf16 (row-major) times Q4_K W[N rows, K] (reference
+ * layout), fp32 accumulate.  The reference has no GEMM: prefill is one matvec
+ * per token (src/inference/transformer.rs:166-196 -> matvec_q4_k_cpu,
+ * compute.rs:707-750); this computes the same Y in one pass. K % 256 == 0. */
+int ssdq_gemm_q4k_bf16_dev(const void* w, const uint16_t* x_bf16, float* y, size_t M,
+                           size_t N, size_t K, ssdq_stream_t stream);
+
+/* ------------------------------------------------------ INT8 KV cache */
+/* Per-row absmax INT8 quantization, bit-exact codes and scales:
+ * quantize_vectors_int8 (src/ssd/block_swap.rs:36-60) == QuantizedVec::quantize
+ * (src/inference/quantized_kv_cache.rs:23-41). in [n_rows, row_len] f32 ->
+ * codes [n_rows, row_len] i8, scales [n_rows] f32. */
+int ssdq_kv_quantize_rows_dev(const float* in, int8_t* codes, float* scales, size_t n_rows,
+                              size_t row_len, ssdq_stream_t stream);
+/* code as f32 * scale: dequantize_vectors_int8 (block_swap.rs:63-74) ==
+ * QuantizedVec::dequantize (quantized_kv_cache.rs:44-53). */
+int ssdq_kv_dequantize_rows_dev(const int8_t* codes, const float* scales, float* out,
+                                size_t n_rows, size_t row_len, ssdq_stream_t stream);
+/* Quantize-on-append into the paged INT8 pool: token t's K and V rows
+ * (kv_dim floats each) are quantized like ssdq_kv_quantize_rows_dev and stored
+ * at pool row slot_mapping[t] (= physical_block * block_size + slot, see
+ * physical_block_for_position, src/inference/paged_attention.rs:113-123);
+ * slot_mapping[t] < 0 skips the token. Pool layout: codes
+ * [n_blocks * block_size, kv_dim] i8 (PhysicalBlock [block_size, kv_dim],
+ * paged_attention.rs:34-35), scales [n_blocks * block_size] f32.
+ * Replaces PagedKvCache::append (paged_attention.rs:351-409) composed with
+ * QuantizedLayerKvCache::append (quantized_kv_cache.rs:107-110). */
+int ssdq_paged_kv_append_dev(const float* k, const float* v, const int32_t* slot_mapping,
+                             int8_t* k_codes, float* k_scales, int8_t* v_codes, float* v_scales,
+                             size_t n_tokens, size_t kv_dim, ssdq_stream_t stream);
+
+/* ------------------------------------------------------------ attention */
+/* GQA decode attention over the paged INT8 cache, one query token per
+ * sequence: for each sequence s and head h, online softmax over positions
+ * [0, ctx_lens[s]) of K/V = code * row scale, kv head h / (n_head/n_head_kv),
+ * scale 1/sqrt(head_dim) (src/inference/flash_attention.rs:70-139), the block
+ * table addressing of paged_attention.rs:113-123, zeros when the context is
+ * empty. q, out: [n_seq, n_head, head_dim] f32; block_tables
+ * [n_seq, max_blocks_per_seq] i32; ctx_lens [n_seq] i32 with
+ * ctx_lens[s] <= max_ctx <= max_blocks_per_seq * block_size.
+ * head_dim in {64, 128, 256}. The library keeps a per-device workspace. */
+int ssdq_paged_attention_int8_dev(const float* q, const int8_t* k_codes, const float* k_scales,
+                                  const int8_t* v_codes, const float* v_scales,
+                                  const int32_t* block_tables, const int32_t* ctx_lens,
+                                  float* out, size_t n_seq, size_t n_head, size_t n_head_kv,
+                                  size_t head_dim, size_t block_size, size_t max_blocks_per_seq,
+                                  size_t max_ctx, ssdq_stream_t stream);
+/* MetalCompute::flash_attention_f32 (compute.rs:217-258) / MetalGpu::
+ * flash_attention_f32 (gpu.rs:547-599): q [n_head, head_dim], k/v flattened
+ * [seq_len, n_head_kv, head_dim] f32, positions [window_start,
+ * min(window_end, seq_len)), out [n_head, head_dim]. head_dim in {64,128,256}. */
+int ssdq_flash_attention_f32_dev(const float* q, const float* k, const float* v, float* out,
+                                 size_t n_head, size_t n_head_kv, size_t head_dim,
+                                 size_t seq_len, size_t window_start, size_t window_end,
+                                 ssdq_stream_t stream);
+/* Host twin (synchronous, copies in/out). Unlike MetalCompute, it never returns
+ * "None": the seq_len >= 4 dispatch heuristic of compute.rs:232 is the
+ * caller's choice. */
+int ssdq_flash_attention_f32(ssdq_ctx* ctx, const float* q, const float* k, const float* v,
+                             size_t n_head, size_t n_head_kv, size_t head_dim, size_t seq_len,
+                             size_t window_start, size_t window_end, float* out);
+
+/* -------------------------------------------------------------- testing */
+/* Forces the byte-addressed matvec kernel that unaligned weights take, so the
+ * fallback can be checked on aligned inputs. Same contract as ssdq_matvec_dev. */
+int ssdq_matvec_generic_dev(int dtype, const void* w, const float* x, float* y, size_t out_dim,
+                            size_t in_dim, size_t batch, ssdq_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SSDQ_H */

@@ -1,0 +1,660 @@
+/*
+ * ssdq_oracle.c — CPU oracle for the ssd-llm quantized compute path.
+ *
+ * TEST INFRASTRUCTURE ONLY (see ssdq_oracle.h). Restates the reference's Rust
+ * CPU functions op for op. Build with -ffp-contract=off and without
+ * -ffast-math: Rust never fuses a*b+c, so neither may this file.
+ *
+ * Checks that pin this restatement (reference known-answer tests, closed
+ * forms, an independent encoder round trip, exhaustive f16 widening, double
+ * brute force) live in tests/test_oracle.py.
+ */
+#include "ssdq_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+size_t ssdo_block_size(int dtype) {
+    /* src/model/gguf.rs:87-105 */
+    switch (dtype) {
+        case SSDO_F32: case SSDO_F16: case SSDO_BF16: return 1;
+        case SSDO_Q4_0: case SSDO_Q8_0: return 32;
+        case SSDO_Q4_K: case SSDO_Q6_K: return 256;
+        default: return 0;
+    }
+}
+
+size_t ssdo_type_size(int dtype) {
+    /* src/model/gguf.rs:108-135 */
+    switch (dtype) {
+        case SSDO_F32: return 4;
+        case SSDO_F16: case SSDO_BF16: return 2;
+        case SSDO_Q4_0: return 18;                      /* 2 + 32/2 */
+        case SSDO_Q8_0: return 34;                      /* 2 + 32 */
+        case SSDO_Q4_K: return 2 + 2 + 12 + 256 / 2;    /* 144 */
+        case SSDO_Q6_K: return 256 / 2 + 256 / 4 + 256 / 16 + 2; /* 210 */
+        default: return 0;
+    }
+}
+
+/* IEEE-754 binary16 -> binary32 widening (exact). This is what
+ * half::f16::to_f32 computes for f16_to_f32, src/metal/compute.rs:2243-2246:
+ * subnormals are normalised, infinities kept, NaNs quieted with the payload
+ * shifted into the top of the f32 mantissa. */
+float ssdo_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1Fu;
+    uint32_t m = h & 0x3FFu;
+    uint32_t bits;
+    if (e == 0x1Fu) {
+        bits = sign | 0x7F800000u | (m << 13);
+        if (m) bits |= 0x00400000u;
+    } else if (e == 0) {
+        if (m == 0) {
+            bits = sign;
+        } else {
+            int p = 31 - __builtin_clz(m); /* leading one: value = 2^(p-24) * 1.f */
+            bits = sign | ((uint32_t)(p + 103) << 23) | ((m << (23 - p)) & 0x7FFFFFu);
+        }
+    } else {
+        bits = sign | ((e + 112u) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+void ssdo_f16_to_f32_array(const uint16_t* h, size_t n, float* out) {
+    for (size_t i = 0; i < n; i++) out[i] = ssdo_f16_to_f32(h[i]);
+}
+
+float ssdo_bf16_to_f32(uint16_t h) {
+    /* f32::from_bits((h as u32) << 16), src/ssd/streamer.rs:108-114 */
+    uint32_t bits = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+static inline float le_f16(const uint8_t* p) {
+    return ssdo_f16_to_f32((uint16_t)(p[0] | ((uint16_t)p[1] << 8)));
+}
+
+/* ---------------------------------------------------------------- dequant */
+
+void ssdo_dequant_q8_0(const uint8_t* data, size_t data_len, size_t n_elements, float* out) {
+    /* src/ssd/streamer.rs:128-150: element = (i8 as f32) * scale */
+    const size_t bs = 32, bb = 34;
+    size_t n_blocks = n_elements / bs, written = 0;
+    for (size_t i = 0; i < n_blocks; i++) {
+        size_t s = i * bb;
+        if (s + bb > data_len) break;
+        float scale = le_f16(data + s);
+        for (size_t j = 0; j < bs; j++) out[written++] = (float)(int8_t)data[s + 2 + j] * scale;
+    }
+    for (; written < n_elements; written++) out[written] = 0.0f; /* output.resize(n, 0.0) */
+}
+
+void ssdo_dequant_q4_0(const uint8_t* data, size_t data_len, size_t n_elements, float* out) {
+    /* src/ssd/streamer.rs:153-178: element 2j from the low nibble of qs[j],
+     * 2j+1 from the high nibble, both minus 8, times scale */
+    const size_t bs = 32, bb = 18;
+    size_t n_blocks = n_elements / bs, written = 0;
+    for (size_t i = 0; i < n_blocks; i++) {
+        size_t s = i * bb;
+        if (s + bb > data_len) break;
+        float scale = le_f16(data + s);
+        for (size_t j = 0; j < 16; j++) {
+            uint8_t byte = data[s + 2 + j];
+            int lo = (int)(byte & 0x0F) - 8;
+            int hi = (int)((byte >> 4) & 0x0F) - 8;
+            out[written++] = (float)lo * scale;
+            out[written++] = (float)hi * scale;
+        }
+    }
+    for (; written < n_elements; written++) out[written] = 0.0f;
+}
+
+void ssdo_dequant_q6_k(const uint8_t* data, size_t data_len, size_t n_elements, float* out) {
+    /* src/ssd/streamer.rs:182-220: ql[128] @0, qh[64] @128, scales i8[16] @192,
+     * d f16 @208; element = (d * scale) * q, q = (hi2<<4 | lo4) - 32 */
+    const size_t bs = 256, bb = 210;
+    size_t n_blocks = n_elements / bs, written = 0;
+    for (size_t i = 0; i < n_blocks; i++) {
+        size_t s = i * bb;
+        if (s + bb > data_len) break;
+        const uint8_t* ql = data + s;
+        const uint8_t* qh = data + s + 128;
+        const uint8_t* sc = data + s + 192;
+        float d = le_f16(data + s + 208);
+        for (size_t j = 0; j < 256; j++) {
+            uint8_t qlb = ql[j / 2];
+            unsigned lo4 = (j % 2 == 0) ? (qlb & 0x0Fu) : (unsigned)(qlb >> 4);
+            unsigned hi2 = (qh[j / 4] >> ((j % 4) * 2)) & 0x03u;
+            int q = (int)(lo4 | (hi2 << 4)) - 32;
+            float scale = (float)(int8_t)sc[j / 16];
+            out[written++] = d * scale * (float)q;
+        }
+    }
+    for (; written < n_elements; written++) out[written] = 0.0f;
+}
+
+/* The 6-bit scale/min of sub-block sb as matvec_q4_k_cpu unpacks them,
+ * src/metal/compute.rs:724-731 (note: for sb>=4 the bits taken from sc[sb-4]
+ * and sc[sb] land in the LOW two bits). */
+static inline void q4k_scale_min(const uint8_t* sc, unsigned sb, unsigned* s, unsigned* m) {
+    if (sb < 4) {
+        *s = sc[sb] & 0x3Fu;
+        *m = sc[sb + 4] & 0x3Fu;
+    } else {
+        unsigned si = sb - 4;
+        *s = (unsigned)(sc[si] >> 6) | ((unsigned)(sc[sb + 4] & 0x0F) << 2);
+        *m = (unsigned)(sc[sb] >> 6) | ((unsigned)(sc[sb + 4] >> 4) << 2);
+    }
+}
+
+void ssdo_dequant_q4_k(const uint8_t* data, size_t data_len, size_t n_elements, float* out) {
+    /* Element values of matvec_q4_k_cpu, src/metal/compute.rs:716-744:
+     * d f16 @0, dmin f16 @2, sc[12] @4, qs[128] @16;
+     * v = (d*s)*q - dmin*m, with q the low/high nibble of qs[sb*16+j]
+     * for elements sb*32+2j / sb*32+2j+1. */
+    const size_t bs = 256, bb = 144;
+    size_t n_blocks = n_elements / bs, written = 0;
+    for (size_t i = 0; i < n_blocks; i++) {
+        size_t s0 = i * bb;
+        if (s0 + bb > data_len) break;
+        float d = le_f16(data + s0);
+        float dmin = le_f16(data + s0 + 2);
+        const uint8_t* sc = data + s0 + 4;
+        const uint8_t* qs = data + s0 + 16;
+        for (unsigned sb = 0; sb < 8; sb++) {
+            unsigned s, m;
+            q4k_scale_min(sc, sb, &s, &m);
+            float scale = d * (float)s;
+            float min_val = dmin * (float)m;
+            for (unsigned j = 0; j < 16; j++) {
+                uint8_t b = qs[sb * 16 + j];
+                out[written++] = scale * (float)(b & 0x0F) - min_val;
+                out[written++] = scale * (float)((b >> 4) & 0x0F) - min_val;
+            }
+        }
+    }
+    for (; written < n_elements; written++) out[written] = 0.0f;
+}
+
+int ssdo_dequantize_to_f32(int dtype, const uint8_t* data, size_t data_len, size_t n_elements,
+                           float* out) {
+    /* src/ssd/streamer.rs:93-125 (Q4_K added: its values per compute.rs:716-744) */
+    switch (dtype) {
+        case SSDO_F32:
+            memcpy(out, data, n_elements * 4);
+            return 0;
+        case SSDO_F16:
+            for (size_t i = 0; i < n_elements; i++) out[i] = le_f16(data + 2 * i);
+            return 0;
+        case SSDO_BF16:
+            for (size_t i = 0; i < n_elements; i++)
+                out[i] = ssdo_bf16_to_f32((uint16_t)(data[2 * i] | (data[2 * i + 1] << 8)));
+            return 0;
+        case SSDO_Q8_0: ssdo_dequant_q8_0(data, data_len, n_elements, out); return 0;
+        case SSDO_Q4_0: ssdo_dequant_q4_0(data, data_len, n_elements, out); return 0;
+        case SSDO_Q6_K: ssdo_dequant_q6_k(data, data_len, n_elements, out); return 0;
+        case SSDO_Q4_K: ssdo_dequant_q4_k(data, data_len, n_elements, out); return 0;
+        default:
+            for (size_t i = 0; i < n_elements; i++) out[i] = 0.0f;
+            return 1;
+    }
+}
+
+/* ----------------------------------------------------------------- matvec */
+
+static void mv_q4_0(const uint8_t* w, const float* x, size_t r0, size_t r1, size_t in_dim,
+                    float* y) {
+    /* src/metal/compute.rs:680-704 */
+    const size_t bs = 32, bb = 18, bpr = in_dim / bs;
+    for (size_t row = r0; row < r1; row++) {
+        size_t row_off = row * bpr * bb;
+        float sum = 0.0f;
+        for (size_t b = 0; b < bpr; b++) {
+            size_t boff = row_off + b * bb;
+            float scale = le_f16(w + boff);
+            size_t xb = b * bs;
+            for (size_t j = 0; j < 16; j++) {
+                uint8_t byte = w[boff + 2 + j];
+                int lo = (int)(byte & 0x0F) - 8;
+                int hi = (int)((byte >> 4) & 0x0F) - 8;
+                sum += scale * (float)lo * x[xb + j * 2];
+                sum += scale * (float)hi * x[xb + j * 2 + 1];
+            }
+        }
+        y[row] = sum;
+    }
+}
+
+static void mv_q4_k(const uint8_t* w, const float* x, size_t r0, size_t r1, size_t in_dim,
+                    float* y) {
+    /* src/metal/compute.rs:707-750 */
+    const size_t bs = 256, bb = 144, bpr = in_dim / bs;
+    for (size_t row = r0; row < r1; row++) {
+        size_t row_off = row * bpr * bb;
+        float sum = 0.0f;
+        for (size_t b = 0; b < bpr; b++) {
+            size_t boff = row_off + b * bb;
+            float d = le_f16(w + boff);
+            float dmin = le_f16(w + boff + 2);
+            const uint8_t* sc = w + boff + 4;
+            const uint8_t* qs = w + boff + 16;
+            size_t xb = b * bs;
+            for (unsigned sb = 0; sb < 8; sb++) {
+                unsigned s, m;
+                q4k_scale_min(sc, sb, &s, &m);
+                float scale = d * (float)s;
+                float min_val = dmin * (float)m;
+                size_t qo = sb * 16;
+                for (size_t j = 0; j < 16; j++) {
+                    uint8_t bv = qs[qo + j];
+                    float v0 = scale * (float)(bv & 0x0F) - min_val;
+                    float v1 = scale * (float)((bv >> 4) & 0x0F) - min_val;
+                    size_t xi = xb + sb * 32 + j * 2;
+                    sum += v0 * x[xi] + v1 * x[xi + 1];
+                }
+            }
+        }
+        y[row] = sum;
+    }
+}
+
+static void mv_q6_k(const uint8_t* w, const float* x, size_t r0, size_t r1, size_t in_dim,
+                    float* y) {
+    /* src/metal/compute.rs:753-791 */
+    const size_t bs = 256, bb = 210, bpr = in_dim / bs;
+    for (size_t row = r0; row < r1; row++) {
+        size_t row_off = row * bpr * bb;
+        float sum = 0.0f;
+        for (size_t b = 0; b < bpr; b++) {
+            size_t boff = row_off + b * bb;
+            const uint8_t* ql = w + boff;
+            const uint8_t* qh = w + boff + 128;
+            const uint8_t* scales = w + boff + 192;
+            float d = le_f16(w + boff + 208);
+            size_t xb = b * bs;
+            for (size_t sb = 0; sb < 16; sb++) {
+                float sc = d * (float)(int8_t)scales[sb];
+                for (size_t j = 0; j < 16; j++) {
+                    size_t idx = sb * 16 + j;
+                    uint8_t qlb = ql[idx / 2];
+                    unsigned low4 = (idx & 1) ? ((qlb >> 4) & 0x0Fu) : (qlb & 0x0Fu);
+                    unsigned high2 = (qh[idx / 4] >> ((idx % 4) * 2)) & 0x03u;
+                    int q = (int)((high2 << 4) | low4) - 32;
+                    sum += sc * (float)q * x[xb + idx];
+                }
+            }
+        }
+        y[row] = sum;
+    }
+}
+
+static void mv_q8_0(const uint8_t* w, const float* x, size_t r0, size_t r1, size_t in_dim,
+                    float* y) {
+    /* src/metal/compute.rs:904-925 */
+    const size_t bs = 32, bb = 34, bpr = in_dim / bs;
+    for (size_t row = r0; row < r1; row++) {
+        size_t row_off = row * bpr * bb;
+        float sum = 0.0f;
+        for (size_t b = 0; b < bpr; b++) {
+            size_t boff = row_off + b * bb;
+            float scale = le_f16(w + boff);
+            size_t xb = b * bs;
+            for (size_t j = 0; j < 32; j++) {
+                int8_t val = (int8_t)w[boff + 2 + j];
+                sum += scale * (float)val * x[xb + j];
+            }
+        }
+        y[row] = sum;
+    }
+}
+
+typedef void (*mv_fn)(const uint8_t*, const float*, size_t, size_t, size_t, float*);
+
+static mv_fn pick_mv(int dtype) {
+    /* matvec_quantized_cpu dispatch, src/metal/compute.rs:648-677 */
+    switch (dtype) {
+        case SSDO_Q4_0: return mv_q4_0;
+        case SSDO_Q4_K: return mv_q4_k;
+        case SSDO_Q6_K: return mv_q6_k;
+        case SSDO_Q8_0: return mv_q8_0;
+        default: return NULL;
+    }
+}
+
+int ssdo_matvec_quantized(const uint8_t* w, const float* x, size_t out_dim, size_t in_dim,
+                          int dtype, float* y) {
+    mv_fn f = pick_mv(dtype);
+    if (!f) {
+        for (size_t i = 0; i < out_dim; i++) y[i] = 0.0f; /* compute.rs:672-675 */
+        return 1;
+    }
+    f(w, x, 0, out_dim, in_dim, y);
+    return 0;
+}
+
+typedef struct {
+    mv_fn f;
+    const uint8_t* w;
+    const float* x;
+    size_t r0, r1, in_dim;
+    float* y;
+} mv_job;
+
+static void* mv_worker(void* p) {
+    mv_job* j = (mv_job*)p;
+    j->f(j->w, j->x, j->r0, j->r1, j->in_dim, j->y);
+    return NULL;
+}
+
+int ssdo_matvec_quantized_mt(const uint8_t* w, const float* x, size_t out_dim, size_t in_dim,
+                             int dtype, float* y, int nthreads) {
+    /* Row shards like src/inference/tensor_parallel.rs:45-96 */
+    mv_fn f = pick_mv(dtype);
+    if (!f) return ssdo_matvec_quantized(w, x, out_dim, in_dim, dtype, y);
+    if (nthreads < 1) nthreads = 1;
+    if ((size_t)nthreads > out_dim) nthreads = (int)(out_dim ? out_dim : 1);
+    pthread_t* th = (pthread_t*)calloc((size_t)nthreads, sizeof(pthread_t));
+    mv_job* jobs = (mv_job*)calloc((size_t)nthreads, sizeof(mv_job));
+    size_t chunk = (out_dim + (size_t)nthreads - 1) / (size_t)nthreads;
+    for (int t = 0; t < nthreads; t++) {
+        size_t r0 = (size_t)t * chunk, r1 = r0 + chunk;
+        if (r0 > out_dim) r0 = out_dim;
+        if (r1 > out_dim) r1 = out_dim;
+        jobs[t] = (mv_job){f, w, x, r0, r1, in_dim, y};
+        pthread_create(&th[t], NULL, mv_worker, &jobs[t]);
+    }
+    for (int t = 0; t < nthreads; t++) pthread_join(th[t], NULL);
+    free(th);
+    free(jobs);
+    return 0;
+}
+
+int ssdo_matvec_exact(const uint8_t* w, const float* x, size_t out_dim, size_t in_dim, int dtype,
+                      double* y) {
+    size_t bs = ssdo_block_size(dtype), tb = ssdo_type_size(dtype);
+    if (!pick_mv(dtype)) {
+        for (size_t i = 0; i < out_dim; i++) y[i] = 0.0;
+        return 1;
+    }
+    size_t bpr = in_dim / bs, k = bpr * bs, row_bytes = bpr * tb;
+    float* e = (float*)malloc(k * sizeof(float));
+    for (size_t r = 0; r < out_dim; r++) {
+        ssdo_dequantize_to_f32(dtype, w + r * row_bytes, row_bytes, k, e);
+        double s = 0.0;
+        for (size_t i = 0; i < k; i++) s += (double)e[i] * (double)x[i];
+        y[r] = s;
+    }
+    free(e);
+    return 0;
+}
+
+/* ---------------------------------------------------------------- INT8 KV */
+
+void ssdo_quantize_rows_int8(const float* data, size_t n_rows, size_t dim, int8_t* codes,
+                             float* scales) {
+    /* src/ssd/block_swap.rs:36-60 (== quantized_kv_cache.rs:23-41) */
+    for (size_t row = 0; row < n_rows; row++) {
+        const float* r = data + row * dim;
+        int8_t* c = codes + row * dim;
+        float absmax = 0.0f;
+        for (size_t i = 0; i < dim; i++) absmax = fmaxf(absmax, fabsf(r[i])); /* f32::max ignores NaN */
+        if (absmax == 0.0f) {
+            scales[row] = 0.0f;
+            memset(c, 0, dim);
+            continue;
+        }
+        float inv_scale = 127.0f / absmax;
+        scales[row] = absmax / 127.0f;
+        for (size_t i = 0; i < dim; i++) {
+            float t = roundf(r[i] * inv_scale); /* f32::round: half away from zero */
+            if (isnan(t)) {
+                c[i] = 0; /* `as i8` saturates, NaN -> 0 */
+            } else {
+                if (t < -127.0f) t = -127.0f;
+                if (t > 127.0f) t = 127.0f;
+                c[i] = (int8_t)t;
+            }
+        }
+    }
+}
+
+void ssdo_dequantize_rows_int8(const int8_t* codes, const float* scales, size_t n_rows,
+                               size_t dim, float* out) {
+    /* src/ssd/block_swap.rs:63-74 */
+    for (size_t row = 0; row < n_rows; row++)
+        for (size_t i = 0; i < dim; i++)
+            out[row * dim + i] = (float)codes[row * dim + i] * scales[row];
+}
+
+/* -------------------------------------------------------------- attention */
+
+/* One head of the online-softmax loop, src/inference/flash_attention.rs:76-139.
+ * k_at / v_at produce the f32 key/value head vectors for a position. */
+typedef struct {
+    /* flattened f32 KV */
+    const float* k;
+    const float* v;
+    size_t stride; /* n_head_kv*head_dim */
+    /* paged int8 KV */
+    const int8_t* kc;
+    const float* ks;
+    const int8_t* vc;
+    const float* vs;
+    const int32_t* table;
+    size_t block_size;
+    int paged;
+} kv_src;
+
+static void kv_fetch(const kv_src* s, size_t pos, size_t kv_h, size_t head_dim, float* kh,
+                     float* vh) {
+    if (!s->paged) {
+        const float* kp = s->k + pos * s->stride + kv_h * head_dim;
+        const float* vp = s->v + pos * s->stride + kv_h * head_dim;
+        memcpy(kh, kp, head_dim * 4);
+        memcpy(vh, vp, head_dim * 4);
+        return;
+    }
+    /* physical_block_for_position, src/inference/paged_attention.rs:113-123 */
+    size_t logical = pos / s->block_size, slot = pos % s->block_size;
+    size_t phys = (size_t)s->table[logical];
+    size_t row = phys * s->block_size + slot;
+    /* PhysicalBlock layout [block_size, kv_dim], key_at offset
+     * slot*kv_dim + kv_head*head_dim (paged_attention.rs:34-35, 72-76) */
+    const int8_t* kc = s->kc + row * s->stride + kv_h * head_dim;
+    const int8_t* vc = s->vc + row * s->stride + kv_h * head_dim;
+    float ksc = s->ks[row], vsc = s->vs[row];
+    /* QuantizedVec::dequantize_into, quantized_kv_cache.rs:49-53 */
+    for (size_t d = 0; d < head_dim; d++) {
+        kh[d] = (float)kc[d] * ksc;
+        vh[d] = (float)vc[d] * vsc;
+    }
+}
+
+static void attend_head(const float* qh, const kv_src* src, size_t kv_h, size_t head_dim,
+                        size_t p0, size_t p1, float* out, float* kh, float* vh, float* acc) {
+    float scale = 1.0f / sqrtf((float)head_dim); /* flash_attention.rs:70 */
+    float running_max = -INFINITY, running_sum = 0.0f;
+    for (size_t d = 0; d < head_dim; d++) acc[d] = 0.0f;
+    size_t chunks = head_dim / 4, rem = head_dim % 4;
+    for (size_t pos = p0; pos < p1; pos++) {
+        kv_fetch(src, pos, kv_h, head_dim, kh, vh);
+        float dot = 0.0f;
+        for (size_t c = 0; c < chunks; c++) { /* 4-wide partial dot, flash_attention.rs:93-104 */
+            size_t b = c * 4;
+            dot += qh[b] * kh[b] + qh[b + 1] * kh[b + 1] + qh[b + 2] * kh[b + 2] +
+                   qh[b + 3] * kh[b + 3];
+        }
+        for (size_t i = chunks * 4; i < chunks * 4 + rem; i++) dot += qh[i] * kh[i];
+        float score = dot * scale;
+        if (score > running_max) { /* flash_attention.rs:110-118 */
+            float correction = expf(running_max - score);
+            running_sum *= correction;
+            for (size_t d = 0; d < head_dim; d++) acc[d] *= correction;
+            running_max = score;
+        }
+        float weight = expf(score - running_max);
+        running_sum += weight;
+        for (size_t d = 0; d < head_dim; d++) acc[d] += weight * vh[d];
+    }
+    if (running_sum > 0.0f) { /* flash_attention.rs:128-137 */
+        float inv_sum = 1.0f / running_sum;
+        for (size_t d = 0; d < head_dim; d++) out[d] = acc[d] * inv_sum;
+    } else {
+        for (size_t d = 0; d < head_dim; d++) out[d] = 0.0f;
+    }
+}
+
+void ssdo_flash_attention_f32(const float* q, const float* k, const float* v, size_t n_head,
+                              size_t n_head_kv, size_t head_dim, size_t seq_len,
+                              size_t window_start, size_t window_end, float* out) {
+    kv_src src;
+    memset(&src, 0, sizeof src);
+    src.k = k;
+    src.v = v;
+    src.stride = n_head_kv * head_dim;
+    size_t group = n_head_kv ? n_head / n_head_kv : 0;
+    if (group < 1) group = 1; /* (n_head / n_head_kv).max(1), flash_attention.rs:71 */
+    size_t end = window_end < seq_len ? window_end : seq_len;
+    float* scratch = (float*)malloc(3 * head_dim * sizeof(float));
+    for (size_t h = 0; h < n_head; h++)
+        attend_head(q + h * head_dim, &src, h / group, head_dim, window_start, end,
+                    out + h * head_dim, scratch, scratch + head_dim, scratch + 2 * head_dim);
+    free(scratch);
+}
+
+typedef struct {
+    const float* q;
+    kv_src base;
+    const int32_t* block_tables;
+    const int32_t* ctx_lens;
+    size_t n_head, group, head_dim, max_blocks;
+    size_t u0, u1; /* units = seq*n_head + h */
+    float* out;
+} attn_job;
+
+static void* attn_worker(void* p) {
+    attn_job* j = (attn_job*)p;
+    float* scratch = (float*)malloc(3 * j->head_dim * sizeof(float));
+    for (size_t u = j->u0; u < j->u1; u++) {
+        size_t s = u / j->n_head, h = u % j->n_head;
+        kv_src src = j->base;
+        src.table = j->block_tables + s * j->max_blocks;
+        size_t ctx = j->ctx_lens[s] > 0 ? (size_t)j->ctx_lens[s] : 0;
+        attend_head(j->q + u * j->head_dim, &src, h / j->group, j->head_dim, 0, ctx,
+                    j->out + u * j->head_dim, scratch, scratch + j->head_dim,
+                    scratch + 2 * j->head_dim);
+    }
+    free(scratch);
+    return NULL;
+}
+
+void ssdo_paged_attention_int8_mt(const float* q, const int8_t* k_codes, const float* k_scales,
+                                  const int8_t* v_codes, const float* v_scales,
+                                  const int32_t* block_tables, const int32_t* ctx_lens,
+                                  size_t n_seq, size_t n_head, size_t n_head_kv, size_t head_dim,
+                                  size_t block_size, size_t max_blocks_per_seq, float* out,
+                                  int nthreads) {
+    kv_src base;
+    memset(&base, 0, sizeof base);
+    base.paged = 1;
+    base.kc = k_codes;
+    base.ks = k_scales;
+    base.vc = v_codes;
+    base.vs = v_scales;
+    base.stride = n_head_kv * head_dim;
+    base.block_size = block_size;
+    size_t group = n_head_kv ? n_head / n_head_kv : 0;
+    if (group < 1) group = 1;
+    size_t units = n_seq * n_head;
+    if (nthreads < 1) nthreads = 1;
+    if ((size_t)nthreads > units) nthreads = (int)(units ? units : 1);
+    pthread_t* th = (pthread_t*)calloc((size_t)nthreads, sizeof(pthread_t));
+    attn_job* jobs = (attn_job*)calloc((size_t)nthreads, sizeof(attn_job));
+    size_t chunk = (units + (size_t)nthreads - 1) / (size_t)nthreads;
+    for (int t = 0; t < nthreads; t++) {
+        size_t u0 = (size_t)t * chunk, u1 = u0 + chunk;
+        if (u0 > units) u0 = units;
+        if (u1 > units) u1 = units;
+        jobs[t] = (attn_job){q, base, block_tables, ctx_lens, n_head, group, head_dim,
+                             max_blocks_per_seq, u0, u1, out};
+        if (nthreads == 1)
+            attn_worker(&jobs[t]);
+        else
+            pthread_create(&th[t], NULL, attn_worker, &jobs[t]);
+    }
+    if (nthreads > 1)
+        for (int t = 0; t < nthreads; t++) pthread_join(th[t], NULL);
+    free(th);
+    free(jobs);
+}
+
+void ssdo_paged_attention_int8(const float* q, const int8_t* k_codes, const float* k_scales,
+                               const int8_t* v_codes, const float* v_scales,
+                               const int32_t* block_tables, const int32_t* ctx_lens,
+                               size_t n_seq, size_t n_head, size_t n_head_kv, size_t head_dim,
+                               size_t block_size, size_t max_blocks_per_seq, float* out) {
+    ssdo_paged_attention_int8_mt(q, k_codes, k_scales, v_codes, v_scales, block_tables, ctx_lens,
+                                 n_seq, n_head, n_head_kv, head_dim, block_size,
+                                 max_blocks_per_seq, out, 1);
+}
+
+/* -------------------------------------------------------------------- GEMM */
+
+typedef struct {
+    const uint8_t* w;
+    const uint16_t* x;
+    size_t N, K, t0, t1;
+    float* y;
+    double* yd;
+} gemm_job;
+
+static void* gemm_worker(void* p) {
+    gemm_job* j = (gemm_job*)p;
+    float* xf = (float*)malloc(j->K * sizeof(float));
+    for (size_t t = j->t0; t < j->t1; t++) {
+        for (size_t i = 0; i < j->K; i++) xf[i] = ssdo_bf16_to_f32(j->x[t * j->K + i]);
+        if (j->y)
+            mv_q4_k(j->w, xf, 0, j->N, j->K, j->y + t * j->N);
+        else
+            ssdo_matvec_exact(j->w, xf, j->N, j->K, SSDO_Q4_K, j->yd + t * j->N);
+    }
+    free(xf);
+    return NULL;
+}
+
+static void gemm_run(const uint8_t* w, const uint16_t* x, size_t M, size_t N, size_t K, float* y,
+                     double* yd, int nthreads) {
+    if (nthreads < 1) nthreads = 1;
+    if ((size_t)nthreads > M) nthreads = (int)(M ? M : 1);
+    pthread_t* th = (pthread_t*)calloc((size_t)nthreads, sizeof(pthread_t));
+    gemm_job* jobs = (gemm_job*)calloc((size_t)nthreads, sizeof(gemm_job));
+    size_t chunk = (M + (size_t)nthreads - 1) / (size_t)nthreads;
+    for (int t = 0; t < nthreads; t++) {
+        size_t t0 = (size_t)t * chunk, t1 = t0 + chunk;
+        if (t0 > M) t0 = M;
+        if (t1 > M) t1 = M;
+        jobs[t] = (gemm_job){w, x, N, K, t0, t1, y, yd};
+        pthread_create(&th[t], NULL, gemm_worker, &jobs[t]);
+    }
+    for (int t = 0; t < nthreads; t++) pthread_join(th[t], NULL);
+    free(th);
+    free(jobs);
+}
+
+void ssdo_gemm_q4k_bf16(const uint8_t* w, const uint16_t* x, size_t M, size_t N, size_t K,
+                        float* y, int nthreads) {
+    gemm_run(w, x, M, N, K, y, NULL, nthreads);
+}
+
+void ssdo_gemm_q4k_bf16_exact(const uint8_t* w, const uint16_t* x, size_t M, size_t N, size_t K,
+                              double* y, int nthreads) {
+    gemm_run(w, x, M, N, K, NULL, y, nthreads);
+}

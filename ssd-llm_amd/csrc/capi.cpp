@@ -1,0 +1,433 @@
+// extern "C" boundary of libssdq.so: argument checking, status codes,
+// per-device workspaces and the synchronous host-pointer twins.
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <utility>
+
+#include "../../include/ssdq.h"
+#include "launch.hpp"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation)
+    return fail(SSDQ_ERR_OUT_OF_MEMORY, "%s: %s", what, hipGetErrorString(e));
+  return fail(SSDQ_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+int ok() {
+  g_err[0] = '\0';
+  return SSDQ_OK;
+}
+
+bool supported_quant(int dtype) {
+  return dtype == SSDQ_TYPE_Q4_0 || dtype == SSDQ_TYPE_Q8_0 || dtype == SSDQ_TYPE_Q4_K ||
+         dtype == SSDQ_TYPE_Q6_K;
+}
+
+bool fits_int(size_t v) { return v <= (size_t)INT_MAX; }
+
+// Grow-only device buffers keyed by (device, stream), so calls on different
+// streams never share scratch memory.
+struct Workspace {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+};
+std::mutex g_ws_mu;
+std::map<std::pair<int, void*>, Workspace> g_ws;
+
+hipError_t workspace_get(size_t bytes, hipStream_t stream, void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  Workspace& w = g_ws[{dev, (void*)stream}];
+  if (w.bytes < bytes) {
+    if (w.ptr) {
+      e = hipStreamSynchronize(stream);
+      if (e != hipSuccess) return e;
+      (void)hipFree(w.ptr);
+      w.ptr = nullptr;
+      w.bytes = 0;
+    }
+    e = hipMalloc(&w.ptr, bytes);
+    if (e != hipSuccess) return e;
+    w.bytes = bytes;
+  }
+  *out = w.ptr;
+  return hipSuccess;
+}
+
+}  // namespace
+
+namespace ssdq {
+
+int device_cu_count() {
+  static std::mutex mu;
+  static std::map<int, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  std::lock_guard<std::mutex> lk(mu);
+  auto it = cache.find(dev);
+  if (it != cache.end()) return it->second;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  cache[dev] = cus;
+  return cus;
+}
+
+}  // namespace ssdq
+
+struct ssdq_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  void* buf[4] = {nullptr, nullptr, nullptr, nullptr};
+  size_t cap[4] = {0, 0, 0, 0};
+};
+
+namespace {
+
+hipError_t ctx_buf(ssdq_ctx* c, int i, size_t bytes, void** out) {
+  if (c->cap[i] < bytes) {
+    if (c->buf[i]) (void)hipFree(c->buf[i]);
+    c->buf[i] = nullptr;
+    c->cap[i] = 0;
+    hipError_t e = hipMalloc(&c->buf[i], bytes ? bytes : 4);
+    if (e != hipSuccess) return e;
+    c->cap[i] = bytes;
+  }
+  *out = c->buf[i];
+  return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ssdq_abi_version(void) { return SSDQ_ABI_VERSION; }
+
+const char* ssdq_last_error(void) { return g_err; }
+
+size_t ssdq_block_size(int dtype) {
+  switch (dtype) {
+    case SSDQ_TYPE_F32: case SSDQ_TYPE_F16: case SSDQ_TYPE_BF16: return 1;
+    case SSDQ_TYPE_Q4_0: case SSDQ_TYPE_Q8_0: return 32;
+    case SSDQ_TYPE_Q4_K: case SSDQ_TYPE_Q6_K: return 256;
+    default: return 0;
+  }
+}
+
+size_t ssdq_type_size(int dtype) {
+  switch (dtype) {
+    case SSDQ_TYPE_F32: return 4;
+    case SSDQ_TYPE_F16: case SSDQ_TYPE_BF16: return 2;
+    case SSDQ_TYPE_Q4_0: return 18;
+    case SSDQ_TYPE_Q8_0: return 34;
+    case SSDQ_TYPE_Q4_K: return 144;
+    case SSDQ_TYPE_Q6_K: return 210;
+    default: return 0;
+  }
+}
+
+size_t ssdq_row_bytes(int dtype, size_t in_dim) {
+  const size_t bs = ssdq_block_size(dtype);
+  return bs ? (in_dim / bs) * ssdq_type_size(dtype) : 0;
+}
+
+int ssdq_ctx_create(int device, ssdq_ctx** out) {
+  if (!out) return fail(SSDQ_ERR_INVALID_ARG, "ssdq_ctx_create: out is NULL");
+  *out = nullptr;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0)
+    return fail(SSDQ_ERR_NO_DEVICE, "ssdq_ctx_create: no HIP device");
+  if (device < 0) {
+    if (hipGetDevice(&device) != hipSuccess) device = 0;
+  }
+  if (device >= n) return fail(SSDQ_ERR_NO_DEVICE, "ssdq_ctx_create: device %d of %d", device, n);
+  hipError_t e = hipSetDevice(device);
+  if (e != hipSuccess) return hip_fail(e, "ssdq_ctx_create: hipSetDevice");
+  ssdq_ctx* c = new (std::nothrow) ssdq_ctx();
+  if (!c) return fail(SSDQ_ERR_OUT_OF_MEMORY, "ssdq_ctx_create: host allocation");
+  c->device = device;
+  e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete c;
+    return hip_fail(e, "ssdq_ctx_create: hipStreamCreate");
+  }
+  *out = c;
+  return ok();
+}
+
+void ssdq_ctx_destroy(ssdq_ctx* c) {
+  if (!c) return;
+  (void)hipSetDevice(c->device);
+  (void)hipStreamSynchronize(c->stream);
+  for (int i = 0; i < 4; i++)
+    if (c->buf[i]) (void)hipFree(c->buf[i]);
+  (void)hipStreamDestroy(c->stream);
+  delete c;
+}
+
+int ssdq_ctx_device(const ssdq_ctx* c) { return c ? c->device : -1; }
+
+int ssdq_dequant_dev(int dtype, const void* w, size_t n_elements, float* out,
+                     ssdq_stream_t stream) {
+  if (n_elements == 0) return ok();
+  if (!out) return fail(SSDQ_ERR_INVALID_ARG, "ssdq_dequant_dev: out is NULL");
+  hipStream_t s = (hipStream_t)stream;
+  if (!supported_quant(dtype)) {
+    hipError_t e = ssdq::launch_fill_zero(out, n_elements, s);
+    if (e != hipSuccess) return hip_fail(e, "ssdq_dequant_dev: fill");
+    fail(SSDQ_WARN_UNSUPPORTED_ZEROED, "ssdq_dequant_dev: dtype %d unsupported, zero-filled", dtype);
+    return SSDQ_WARN_UNSUPPORTED_ZEROED;
+  }
+  if (!w) return fail(SSDQ_ERR_INVALID_ARG, "ssdq_dequant_dev: w is NULL");
+  const size_t bs = ssdq_block_size(dtype);
+  const size_t n_blocks = n_elements / bs;
+  hipError_t e = ssdq::launch_dequant(dtype, (const uint8_t*)w, n_blocks, out, s);
+  if (e != hipSuccess) return hip_fail(e, "ssdq_dequant_dev");
+  if (n_blocks * bs < n_elements) {
+    e = ssdq::launch_fill_zero(out + n_blocks * bs, n_elements - n_blocks * bs, s);
+    if (e != hipSuccess) return hip_fail(e, "ssdq_dequant_dev: tail");
+  }
+  return ok();
+}
+
+static int matvec_common(int dtype, const void* w, const float* x, float* y, size_t out_dim,
+                         size_t in_dim, size_t batch, ssdq_stream_t stream, bool generic) {
+  const char* fn = generic ? "ssdq_matvec_generic_dev" : "ssdq_matvec_dev";
+  if (out_dim == 0 || batch == 0) return ok();
+  if (!y) return fail(SSDQ_ERR_INVALID_ARG, "%s: y is NULL", fn);
+  if (!fits_int(out_dim) || !fits_int(in_dim) || !fits_int(batch) ||
+      !fits_int(out_dim * batch) || !fits_int(in_dim * batch))
+    return fail(SSDQ_ERR_INVALID_ARG, "%s: dimensions exceed 2^31", fn);
+  hipStream_t s = (hipStream_t)stream;
+  if (!supported_quant(dtype)) {
+    hipError_t e = ssdq::launch_fill_zero(y, out_dim * batch, s);
+    if (e != hipSuccess) return hip_fail(e, fn);
+    fail(SSDQ_WARN_UNSUPPORTED_ZEROED, "%s: dtype %d unsupported, zero-filled", fn, dtype);
+    return SSDQ_WARN_UNSUPPORTED_ZEROED;
+  }
+  const size_t keff = (in_dim / ssdq_block_size(dtype)) * ssdq_block_size(dtype);
+  if (keff > 0 && (!w || !x)) return fail(SSDQ_ERR_INVALID_ARG, "%s: w or x is NULL", fn);
+  if (((uintptr_t)x & 3) || ((uintptr_t)y & 3))
+    return fail(SSDQ_ERR_INVALID_ARG, "%s: x and y must be 4-byte aligned", fn);
+  hipError_t e = generic ? ssdq::launch_matvec_generic(dtype, (const uint8_t*)w, x, y, out_dim,
+                                                       in_dim, batch, s)
+                         : ssdq::launch_matvec(dtype, (const uint8_t*)w, x, y, out_dim, in_dim,
+                                               batch, s);
+  if (e != hipSuccess) return hip_fail(e, fn);
+  return ok();
+}
+
+int ssdq_matvec_dev(int dtype, const void* w, const float* x, float* y, size_t out_dim,
+                    size_t in_dim, size_t batch, ssdq_stream_t stream) {
+  return matvec_common(dtype, w, x, y, out_dim, in_dim, batch, stream, false);
+}
+
+int ssdq_matvec_generic_dev(int dtype, const void* w, const float* x, float* y, size_t out_dim,
+                            size_t in_dim, size_t batch, ssdq_stream_t stream) {
+  return matvec_common(dtype, w, x, y, out_dim, in_dim, batch, stream, true);
+}
+
+int ssdq_matvec_quantized(ssdq_ctx* c, const uint8_t* w_raw, size_t w_len, const float* x,
+                          size_t x_len, size_t out_dim, size_t in_dim, int dtype, float* y) {
+  if (!c) return fail(SSDQ_ERR_INVALID_ARG, "ssdq_matvec_quantized: ctx is NULL");
+  if (out_dim == 0) return ok();
+  if (!y) return fail(SSDQ_ERR_INVALID_ARG, "ssdq_matvec_quantized: y is NULL");
+  if (!supported_quant(dtype)) {
+    memset(y, 0, out_dim * sizeof(float));
+    fail(SSDQ_WARN_UNSUPPORTED_ZEROED, "ssdq_matvec_quantized: dtype %d unsupported, zeros", dtype);
+    return SSDQ_WARN_UNSUPPORTED_ZEROED;
+  }
+  const size_t rb = ssdq_row_bytes(dtype, in_dim);
+  const size_t keff = (in_dim / ssdq_block_size(dtype)) * ssdq_block_size(dtype);
+  // The reference indexes w[row*row_bytes + ...] and x[..keff) and panics when
+  // they are short; this reports an error instead.
+  if (w_len < out_dim * rb)
+    return fail(SSDQ_ERR_INVALID_ARG, "ssdq_matvec_quantized: w has %zu bytes, need %zu", w_len,
+                out_dim * rb);
+  if (x_len < keff)
+    return fail(SSDQ_ERR_INVALID_ARG, "ssdq_matvec_quantized: x has %zu floats, need %zu", x_len, keff);
+  if ((rb && !w_raw) || (keff && !x)) return fail(SSDQ_ERR_INVALID_ARG, "ssdq_matvec_quantized: NULL input");
+  hipError_t e = hipSetDevice(c->device);
+  if (e != hipSuccess) return hip_fail(e, "ssdq_matvec_quantized: hipSetDevice");
+  void *dw, *dx, *dy;
+  if ((e = ctx_buf(c, 0, out_dim * rb, &dw)) != hipSuccess ||
+      (e = ctx_buf(c, 1, (keff ? keff : 1) * sizeof(float), &dx)) != hipSuccess ||
+      (e = ctx_buf(c, 2, out_dim * sizeof(float), &dy)) != hipSuccess)
+    return hip_fail(e, "ssdq_matvec_quantized: staging allocation");
+  if (rb && (e = hipMemcpyAsync(dw, w_raw, out_dim * rb, hipMemcpyHostToDevice, c->stream)) != hipSuccess)
+    return hip_fail(e, "ssdq_matvec_quantized: copy w");
+  if (keff && (e = hipMemcpyAsync(dx, x, keff * sizeof(float), hipMemcpyHostToDevice, c->stream)) != hipSuccess)
+    return hip_fail(e, "ssdq_matvec_quantized: copy x");
+  int rc = ssdq_matvec_dev(dtype, dw, (const float*)dx, (float*)dy, out_dim, keff ? keff : in_dim,
+                           1, c->stream);
+  if (rc < 0) return rc;
+  if ((e = hipMemcpyAsync(y, dy, out_dim * sizeof(float), hipMemcpyDeviceToHost, c->stream)) != hipSuccess)
+    return hip_fail(e, "ssdq_matvec_quantized: copy y");
+  if ((e = hipStreamSynchronize(c->stream)) != hipSuccess)
+    return hip_fail(e, "ssdq_matvec_quantized: sync");
+  return ok();
+}
+
+int ssdq_gemm_q4k_bf16_dev(const void* w, const uint16_t* x, float* y, size_t M, size_t N,
+                           size_t K, ssdq_stream_t stream) {
+  if (M == 0 || N == 0) return ok();
+  if (!w || !x || !y) return fail(SSDQ_ERR_INVALID_ARG, "ssdq_gemm_q4k_bf16_dev: NULL pointer");
+  if (K == 0 || K % 256) return fail(SSDQ_ERR_INVALID_ARG, "ssdq_gemm_q4k_bf16_dev: K must be a positive multiple of 256");
+  if (!fits_int(M) || !fits_int(N) || !fits_int(K) || !fits_int(M * K) || !fits_int(M * N))
+    return fail(SSDQ_ERR_INVALID_ARG, "ssdq_gemm_q4k_bf16_dev: dimensions exceed 2^31");
+  hipStream_t s = (hipStream_t)stream;
+  const size_t wsb = ssdq::gemm_q4k_workspace_bytes(M, N, K);
+  void* ws = nullptr;
+  hipError_t e = hipSuccess;
+  if (wsb && (e = workspace_get(wsb, s, &ws)) != hipSuccess)
+    return hip_fail(e, "ssdq_gemm_q4k_bf16_dev: workspace");
+  e = ssdq::launch_gemm_q4k((const uint8_t*)w, x, y, M, N, K, ws, wsb, s);
+  if (e != hipSuccess) return hip_fail(e, "ssdq_gemm_q4k_bf16_dev");
+  return ok();
+}
+
+int ssdq_kv_quantize_rows_dev(const float* in, int8_t* codes, float* scales, size_t n_rows,
+                              size_t row_len, ssdq_stream_t stream) {
+  if (n_rows == 0) return ok();
+  if (!scales || (row_len && (!in || !codes)))
+    return fail(SSDQ_ERR_INVALID_ARG, "ssdq_kv_quantize_rows_dev: NULL pointer");
+  if (!fits_int(row_len)) return fail(SSDQ_ERR_INVALID_ARG, "ssdq_kv_quantize_rows_dev: row_len too large");
+  hipError_t e = ssdq::launch_kv_quantize(in, codes, scales, n_rows, row_len, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "ssdq_kv_quantize_rows_dev");
+  return ok();
+}
+
+int ssdq_kv_dequantize_rows_dev(const int8_t* codes, const float* scales, float* out,
+                                size_t n_rows, size_t row_len, ssdq_stream_t stream) {
+  if (n_rows == 0 || row_len == 0) return ok();
+  if (!codes || !scales || !out) return fail(SSDQ_ERR_INVALID_ARG, "ssdq_kv_dequantize_rows_dev: NULL pointer");
+  if (!fits_int(row_len)) return fail(SSDQ_ERR_INVALID_ARG, "ssdq_kv_dequantize_rows_dev: row_len too large");
+  hipError_t e = ssdq::launch_kv_dequantize(codes, scales, out, n_rows, row_len, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "ssdq_kv_dequantize_rows_dev");
+  return ok();
+}
+
+int ssdq_paged_kv_append_dev(const float* k, const float* v, const int32_t* slot_mapping,
+                             int8_t* k_codes, float* k_scales, int8_t* v_codes, float* v_scales,
+                             size_t n_tokens, size_t kv_dim, ssdq_stream_t stream) {
+  if (n_tokens == 0) return ok();
+  if (!k || !v || !slot_mapping || !k_codes || !k_scales || !v_codes || !v_scales)
+    return fail(SSDQ_ERR_INVALID_ARG, "ssdq_paged_kv_append_dev: NULL pointer");
+  if (kv_dim == 0 || !fits_int(kv_dim)) return fail(SSDQ_ERR_INVALID_ARG, "ssdq_paged_kv_append_dev: bad kv_dim");
+  hipError_t e = ssdq::launch_paged_kv_append(k, v, slot_mapping, k_codes, k_scales, v_codes,
+                                              v_scales, n_tokens, kv_dim, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "ssdq_paged_kv_append_dev");
+  return ok();
+}
+
+static bool head_dim_ok(size_t hd) { return hd == 64 || hd == 128 || hd == 256; }
+
+int ssdq_paged_attention_int8_dev(const float* q, const int8_t* k_codes, const float* k_scales,
+                                  const int8_t* v_codes, const float* v_scales,
+                                  const int32_t* block_tables, const int32_t* ctx_lens,
+                                  float* out, size_t n_seq, size_t n_head, size_t n_head_kv,
+                                  size_t head_dim, size_t block_size, size_t max_blocks_per_seq,
+                                  size_t max_ctx, ssdq_stream_t stream) {
+  const char* fn = "ssdq_paged_attention_int8_dev";
+  if (n_seq == 0 || n_head == 0) return ok();
+  if (!q || !k_codes || !k_scales || !v_codes || !v_scales || !block_tables || !ctx_lens || !out)
+    return fail(SSDQ_ERR_INVALID_ARG, "%s: NULL pointer", fn);
+  if (!head_dim_ok(head_dim)) return fail(SSDQ_ERR_UNSUPPORTED, "%s: head_dim %zu not in {64,128,256}", fn, head_dim);
+  if (n_head_kv == 0 || n_head % n_head_kv) return fail(SSDQ_ERR_INVALID_ARG, "%s: n_head must be a multiple of n_head_kv", fn);
+  if (((uintptr_t)k_codes & 3) || ((uintptr_t)v_codes & 3) || ((uintptr_t)q & 3) || ((uintptr_t)out & 3))
+    return fail(SSDQ_ERR_INVALID_ARG, "%s: q, out and the code pools must be 4-byte aligned", fn);
+  if (block_size == 0 || max_blocks_per_seq == 0) return fail(SSDQ_ERR_INVALID_ARG, "%s: empty block geometry", fn);
+  if (max_ctx > max_blocks_per_seq * block_size)
+    return fail(SSDQ_ERR_INVALID_ARG, "%s: max_ctx exceeds the block tables", fn);
+  if (!fits_int(n_seq) || n_seq > 65535 || n_head_kv > 65535 || !fits_int(max_ctx) ||
+      !fits_int(n_seq * max_blocks_per_seq))
+    return fail(SSDQ_ERR_INVALID_ARG, "%s: dimensions too large", fn);
+  ssdq::PagedAttnArgs a{q, k_codes, k_scales, v_codes, v_scales, block_tables, ctx_lens, out,
+                        (int)n_seq, (int)n_head, (int)n_head_kv, (int)head_dim, (int)block_size,
+                        (int)max_blocks_per_seq, (int)(max_ctx ? max_ctx : 1)};
+  hipStream_t s = (hipStream_t)stream;
+  const size_t wsb = ssdq::paged_attn_workspace_bytes(a, nullptr);
+  void* ws = nullptr;
+  hipError_t e = workspace_get(wsb, s, &ws);
+  if (e != hipSuccess) return hip_fail(e, "ssdq_paged_attention_int8_dev: workspace");
+  e = ssdq::launch_paged_attn(a, ws, s);
+  if (e != hipSuccess) return hip_fail(e, fn);
+  return ok();
+}
+
+int ssdq_flash_attention_f32_dev(const float* q, const float* k, const float* v, float* out,
+                                 size_t n_head, size_t n_head_kv, size_t head_dim,
+                                 size_t seq_len, size_t window_start, size_t window_end,
+                                 ssdq_stream_t stream) {
+  const char* fn = "ssdq_flash_attention_f32_dev";
+  if (n_head == 0) return ok();
+  if (!q || !out || (seq_len && (!k || !v))) return fail(SSDQ_ERR_INVALID_ARG, "%s: NULL pointer", fn);
+  if (!head_dim_ok(head_dim)) return fail(SSDQ_ERR_UNSUPPORTED, "%s: head_dim %zu not in {64,128,256}", fn, head_dim);
+  if (n_head_kv == 0 || n_head % n_head_kv) return fail(SSDQ_ERR_INVALID_ARG, "%s: n_head must be a multiple of n_head_kv", fn);
+  if (!fits_int(seq_len) || !fits_int(n_head) || n_head_kv > 65535)
+    return fail(SSDQ_ERR_INVALID_ARG, "%s: dimensions too large", fn);
+  if (((uintptr_t)k & 15) || ((uintptr_t)v & 15))
+    return fail(SSDQ_ERR_INVALID_ARG, "%s: k and v must be 16-byte aligned", fn);
+  const size_t we = window_end < seq_len ? window_end : seq_len;
+  const size_t ws = window_start < we ? window_start : we;
+  hipStream_t s = (hipStream_t)stream;
+  const size_t wsb = ssdq::flash_attn_f32_workspace_bytes((int)n_head, (int)n_head_kv,
+                                                          (int)head_dim, (int)(we - ws), nullptr);
+  void* wsp = nullptr;
+  hipError_t e = workspace_get(wsb, s, &wsp);
+  if (e != hipSuccess) return hip_fail(e, "ssdq_flash_attention_f32_dev: workspace");
+  e = ssdq::launch_flash_attn_f32(q, k, v, out, (int)n_head, (int)n_head_kv, (int)head_dim,
+                                  (int)seq_len, (int)ws, (int)we, wsp, s);
+  if (e != hipSuccess) return hip_fail(e, fn);
+  return ok();
+}
+
+int ssdq_flash_attention_f32(ssdq_ctx* c, const float* q, const float* k, const float* v,
+                             size_t n_head, size_t n_head_kv, size_t head_dim, size_t seq_len,
+                             size_t window_start, size_t window_end, float* out) {
+  if (!c) return fail(SSDQ_ERR_INVALID_ARG, "ssdq_flash_attention_f32: ctx is NULL");
+  if (n_head == 0) return ok();
+  if (!q || !out || (seq_len && (!k || !v))) return fail(SSDQ_ERR_INVALID_ARG, "ssdq_flash_attention_f32: NULL pointer");
+  hipError_t e = hipSetDevice(c->device);
+  if (e != hipSuccess) return hip_fail(e, "ssdq_flash_attention_f32: hipSetDevice");
+  const size_t qn = n_head * head_dim, kvn = seq_len * n_head_kv * head_dim;
+  void *dq, *dk, *dv, *dout;
+  if ((e = ctx_buf(c, 0, qn * 4, &dq)) != hipSuccess || (e = ctx_buf(c, 1, kvn * 4, &dk)) != hipSuccess ||
+      (e = ctx_buf(c, 2, kvn * 4, &dv)) != hipSuccess || (e = ctx_buf(c, 3, qn * 4, &dout)) != hipSuccess)
+    return hip_fail(e, "ssdq_flash_attention_f32: staging allocation");
+  if ((e = hipMemcpyAsync(dq, q, qn * 4, hipMemcpyHostToDevice, c->stream)) != hipSuccess ||
+      (kvn && (e = hipMemcpyAsync(dk, k, kvn * 4, hipMemcpyHostToDevice, c->stream)) != hipSuccess) ||
+      (kvn && (e = hipMemcpyAsync(dv, v, kvn * 4, hipMemcpyHostToDevice, c->stream)) != hipSuccess))
+    return hip_fail(e, "ssdq_flash_attention_f32: copy in");
+  int rc = ssdq_flash_attention_f32_dev((const float*)dq, (const float*)dk, (const float*)dv,
+                                        (float*)dout, n_head, n_head_kv, head_dim, seq_len,
+                                        window_start, window_end, c->stream);
+  if (rc < 0) return rc;
+  if ((e = hipMemcpyAsync(out, dout, qn * 4, hipMemcpyDeviceToHost, c->stream)) != hipSuccess)
+    return hip_fail(e, "ssdq_flash_attention_f32: copy out");
+  if ((e = hipStreamSynchronize(c->stream)) != hipSuccess)
+    return hip_fail(e, "ssdq_flash_attention_f32: sync");
+  return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,65 @@
+// Shared device helpers for the ssdq gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ssdq {
+
+constexpr int kWave = 64;  // CDNA wavefront width
+
+// GgmlType ids (src/model/gguf.rs:17-48) and block geometry (gguf.rs:87-135).
+enum : int { kQ4_0 = 2, kQ8_0 = 8, kQ4_K = 12, kQ6_K = 14 };
+
+template <int F> struct Geom;
+template <> struct Geom<kQ4_0> { static constexpr int bs = 32, bb = 18; };
+template <> struct Geom<kQ8_0> { static constexpr int bs = 32, bb = 34; };
+template <> struct Geom<kQ4_K> { static constexpr int bs = 256, bb = 144; };
+template <> struct Geom<kQ6_K> { static constexpr int bs = 256, bb = 210; };
+
+// IEEE binary16 -> binary32 (exact widening, v_cvt_f32_f16).
+__device__ __forceinline__ float f16_to_f32(uint32_t bits16) {
+  _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)bits16);
+  return (float)h;
+}
+
+__device__ __forceinline__ uint32_t ld_u8(const uint8_t* p) { return *p; }
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) {
+  // p may be only 1-byte aligned in the generic paths
+  return (uint32_t)p[0] | ((uint32_t)p[1] << 8);
+}
+
+// Byte k (0..3) of a dword.
+__device__ __forceinline__ uint32_t byte_of(uint32_t v, int k) { return (v >> (8 * k)) & 0xFFu; }
+
+// Sum across the 64 lanes of a wavefront (result valid in every lane).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+
+// 6-bit scale s and min m of Q4_K sub-block sb from the 12 packed bytes, in the
+// reference's bit order (src/metal/compute.rs:724-731): for sb >= 4 the two bits
+// taken from sc[sb-4] / sc[sb] are the LOW bits.  sc1/sc2/sc3 are bytes 0-3,
+// 4-7 and 8-11 of the packed area as little-endian dwords.
+__device__ __forceinline__ void q4k_scale_min(uint32_t sc1, uint32_t sc2, uint32_t sc3, int sb,
+                                              uint32_t& s, uint32_t& m) {
+  if (sb < 4) {
+    s = byte_of(sc1, sb) & 63u;
+    m = byte_of(sc2, sb) & 63u;
+  } else {
+    const int i = sb - 4;
+    const uint32_t hi = byte_of(sc3, i);
+    s = (byte_of(sc1, i) >> 6) | ((hi & 0x0Fu) << 2);
+    m = (byte_of(sc2, i) >> 6) | ((hi >> 4) << 2);
+  }
+}
+
+}  // namespace ssdq

@@ -1,0 +1,162 @@
+// INT8 per-row KV quantization (bit-exact with the reference) and the paged
+// append that writes quantized rows into the block pool.
+//
+// Reference: quantize_vectors_int8, src/ssd/block_swap.rs:36-60
+//   == QuantizedVec::quantize, src/inference/quantized_kv_cache.rs:23-41:
+//   absmax = fold(0.0, f32::max) of |v|      (NaN ignored, as fmaxf)
+//   absmax == 0  ->  scale 0, codes 0
+//   inv = 127 / absmax, scale = absmax / 127 (two correctly rounded divisions)
+//   code = clamp(round_half_away(v * inv), -127, 127) as i8   (NaN -> 0)
+// Dequant: code as f32 * scale (block_swap.rs:63-74, quantized_kv_cache.rs:44-53).
+// A row is one token's K (or V) vector over kv_dim = n_kv_heads * head_dim
+// (quantized_kv_cache.rs:107-110, block_swap.rs:232-233).
+//
+// One wavefront per row; a row is read once from HBM (kept in registers for
+// rows up to 64*32 floats, re-read from L2 otherwise) and its codes are written
+// as packed dwords.
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace ssdq {
+namespace {
+
+__device__ __forceinline__ uint32_t code_of(float v, float inv) {
+#pragma clang fp contract(off)
+  const float t = roundf(v * inv);  // round half away from zero
+  int c;
+  if (t != t) {
+    c = 0;  // Rust `as i8` maps NaN to 0
+  } else {
+    c = (int)fminf(fmaxf(t, -127.0f), 127.0f);
+  }
+  return (uint32_t)(c & 0xFF);
+}
+
+__device__ __forceinline__ uint32_t pack4(float a, float b, float c, float d, float inv) {
+  return code_of(a, inv) | (code_of(b, inv) << 8) | (code_of(c, inv) << 16) | (code_of(d, inv) << 24);
+}
+
+// Quantizes the row `in` (len floats, 16-byte aligned when len % 4 == 0) into
+// codes/scale.  Executed by one full wavefront.
+template <int NV>  // float4 registers per lane kept resident (0: stream twice)
+__device__ __forceinline__ void quantize_row(const float* __restrict__ in, int len,
+                                             int8_t* __restrict__ codes, float* __restrict__ scale) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  float amax = 0.0f;
+  const bool vec = (len & 3) == 0 && (((uintptr_t)in) & 15) == 0 && (((uintptr_t)codes) & 3) == 0;
+  if (vec && NV > 0 && len <= NV * 4 * 64) {
+    float4 r[NV > 0 ? NV : 1];
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+      const int e = (i * 64 + lane) * 4;
+      r[i] = e < len ? *reinterpret_cast<const float4*>(in + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(r[i].x), fabsf(r[i].y)), fmaxf(fabsf(r[i].z), fabsf(r[i].w))));
+    }
+    amax = wave_max(amax);
+    float inv = 0.0f;
+    if (amax != 0.0f) inv = 127.0f / amax;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+      const int e = (i * 64 + lane) * 4;
+      if (e < len) {
+        const uint32_t p = amax == 0.0f ? 0u : pack4(r[i].x, r[i].y, r[i].z, r[i].w, inv);
+        *reinterpret_cast<uint32_t*>(codes + e) = p;
+      }
+    }
+    if (lane == 0) *scale = amax == 0.0f ? 0.0f : amax / 127.0f;
+    return;
+  }
+  // general path: element-wise, two passes
+  for (int e = lane; e < len; e += 64) amax = fmaxf(amax, fabsf(in[e]));
+  amax = wave_max(amax);
+  const float inv = amax != 0.0f ? 127.0f / amax : 0.0f;
+  for (int e = lane; e < len; e += 64) codes[e] = amax == 0.0f ? (int8_t)0 : (int8_t)code_of(in[e], inv);
+  if (lane == 0) *scale = amax == 0.0f ? 0.0f : amax / 127.0f;
+}
+
+template <int NV>
+__global__ __launch_bounds__(256) void kv_quantize_kernel(const float* __restrict__ in,
+                                                          int8_t* __restrict__ codes,
+                                                          float* __restrict__ scales,
+                                                          size_t n_rows, int row_len) {
+  const size_t waves = (size_t)gridDim.x * (blockDim.x >> 6);
+  for (size_t r = (size_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); r < n_rows; r += waves)
+    quantize_row<NV>(in + r * row_len, row_len, codes + r * row_len, scales + r);
+}
+
+// slot_mapping[t] = physical row (block * block_size + slot) of token t, or < 0 to skip.
+template <int NV>
+__global__ __launch_bounds__(256) void paged_append_kernel(
+    const float* __restrict__ k, const float* __restrict__ v, const int32_t* __restrict__ slots,
+    int8_t* __restrict__ kc, float* __restrict__ ks, int8_t* __restrict__ vc,
+    float* __restrict__ vs, size_t n_tokens, int kv_dim) {
+  const size_t waves = (size_t)gridDim.x * (blockDim.x >> 6);
+  for (size_t i = (size_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); i < 2 * n_tokens; i += waves) {
+    const size_t t = i >> 1;
+    const int32_t slot = slots[t];
+    if (slot < 0) continue;
+    const bool is_v = (i & 1) != 0;
+    const float* src = (is_v ? v : k) + t * kv_dim;
+    int8_t* dst = (is_v ? vc : kc) + (size_t)slot * kv_dim;
+    float* sc = (is_v ? vs : ks) + slot;
+    quantize_row<NV>(src, kv_dim, dst, sc);
+  }
+}
+
+__global__ __launch_bounds__(256) void kv_dequantize_kernel(const int8_t* __restrict__ codes,
+                                                            const float* __restrict__ scales,
+                                                            float* __restrict__ out, size_t n_rows,
+                                                            int row_len) {
+  const size_t total = n_rows * (size_t)row_len;
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride)
+    out[i] = (float)codes[i] * scales[i / row_len];
+}
+
+unsigned grid_waves(size_t rows) {
+  size_t g = (rows + 3) / 4;
+  const size_t cap = (size_t)device_cu_count() * 16;
+  if (g > cap) g = cap;
+  return (unsigned)(g ? g : 1);
+}
+
+}  // namespace
+
+hipError_t launch_kv_quantize(const float* in, int8_t* codes, float* scales, size_t n_rows,
+                              size_t row_len, hipStream_t s) {
+  if (n_rows == 0) return hipSuccess;
+  if (row_len <= 64 * 4 * 4)
+    hipLaunchKernelGGL(kv_quantize_kernel<4>, dim3(grid_waves(n_rows)), dim3(256), 0, s, in, codes,
+                       scales, n_rows, (int)row_len);
+  else
+    hipLaunchKernelGGL(kv_quantize_kernel<8>, dim3(grid_waves(n_rows)), dim3(256), 0, s, in, codes,
+                       scales, n_rows, (int)row_len);
+  return hipGetLastError();
+}
+
+hipError_t launch_paged_kv_append(const float* k, const float* v, const int32_t* slot_mapping,
+                                  int8_t* k_codes, float* k_scales, int8_t* v_codes,
+                                  float* v_scales, size_t n_tokens, size_t kv_dim, hipStream_t s) {
+  if (n_tokens == 0) return hipSuccess;
+  if (kv_dim <= 64 * 4 * 4)
+    hipLaunchKernelGGL(paged_append_kernel<4>, dim3(grid_waves(2 * n_tokens)), dim3(256), 0, s, k,
+                       v, slot_mapping, k_codes, k_scales, v_codes, v_scales, n_tokens, (int)kv_dim);
+  else
+    hipLaunchKernelGGL(paged_append_kernel<8>, dim3(grid_waves(2 * n_tokens)), dim3(256), 0, s, k,
+                       v, slot_mapping, k_codes, k_scales, v_codes, v_scales, n_tokens, (int)kv_dim);
+  return hipGetLastError();
+}
+
+hipError_t launch_kv_dequantize(const int8_t* codes, const float* scales, float* out,
+                                size_t n_rows, size_t row_len, hipStream_t s) {
+  const size_t total = n_rows * row_len;
+  if (total == 0) return hipSuccess;
+  size_t g = (total + 255) / 256;
+  if (g > 65536) g = 65536;
+  hipLaunchKernelGGL(kv_dequantize_kernel, dim3((unsigned)g), dim3(256), 0, s, codes, scales, out,
+                     n_rows, (int)row_len);
+  return hipGetLastError();
+}
+
+}  // namespace ssdq

@@ -1,0 +1,61 @@
+// Internal launchers shared between the kernel translation units and the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace ssdq {
+
+hipError_t launch_fill_zero(float* out, size_t n, hipStream_t stream);
+hipError_t launch_dequant(int dtype, const uint8_t* w, size_t n_blocks, float* out,
+                          hipStream_t stream);
+
+// y[b*out_dim + r] = sum_k W[r,k] * x[b*in_dim + k], b < batch, over the
+// whole blocks of each row (k < (in_dim / block) * block).
+hipError_t launch_matvec(int dtype, const uint8_t* w, const float* x, float* y, size_t out_dim,
+                         size_t in_dim, size_t batch, hipStream_t stream);
+// Same, forcing the byte-addressed fallback kernel (used by tests to cover it).
+hipError_t launch_matvec_generic(int dtype, const uint8_t* w, const float* x, float* y,
+                                 size_t out_dim, size_t in_dim, size_t batch, hipStream_t stream);
+
+hipError_t launch_kv_quantize(const float* in, int8_t* codes, float* scales, size_t n_rows,
+                              size_t row_len, hipStream_t stream);
+hipError_t launch_kv_dequantize(const int8_t* codes, const float* scales, float* out,
+                                size_t n_rows, size_t row_len, hipStream_t stream);
+hipError_t launch_paged_kv_append(const float* k, const float* v, const int32_t* slot_mapping,
+                                  int8_t* k_codes, float* k_scales, int8_t* v_codes,
+                                  float* v_scales, size_t n_tokens, size_t kv_dim,
+                                  hipStream_t stream);
+
+struct PagedAttnArgs {
+  const float* q;
+  const int8_t* k_codes;
+  const float* k_scales;
+  const int8_t* v_codes;
+  const float* v_scales;
+  const int32_t* block_tables;
+  const int32_t* ctx_lens;
+  float* out;
+  int n_seq, n_head, n_head_kv, head_dim, block_size, max_blocks_per_seq;
+  int max_ctx;  // upper bound on ctx_lens (sizes the split-KV grid)
+};
+// Bytes of device workspace the split-KV attention needs for these shapes.
+size_t paged_attn_workspace_bytes(const PagedAttnArgs& a, int* n_splits_out);
+hipError_t launch_paged_attn(const PagedAttnArgs& a, void* workspace, hipStream_t stream);
+
+size_t flash_attn_f32_workspace_bytes(int n_head, int n_head_kv, int head_dim, int len,
+                                      int* n_splits_out);
+hipError_t launch_flash_attn_f32(const float* q, const float* k, const float* v, float* out,
+                                 int n_head, int n_head_kv, int head_dim, int seq_len,
+                                 int window_start, int window_end, void* workspace,
+                                 hipStream_t stream);
+
+// Prefill GEMM: Y[M,N] f32 = X[M,K] bf16 x W[N,K] Q4_K (reference layout).
+hipError_t launch_gemm_q4k(const uint8_t* w, const uint16_t* x, float* y, size_t M, size_t N,
+                           size_t K, void* workspace, size_t workspace_bytes, hipStream_t stream);
+size_t gemm_q4k_workspace_bytes(size_t M, size_t N, size_t K);
+
+int device_cu_count();
+
+}  // namespace ssdq

@@ -1,0 +1,211 @@
+"""ctypes binding of libssdq.so (the C ABI declared in include/ssdq.h).
+
+This is plumbing for tests and benchmarks: device buffers and streams come
+from PyTorch, the compute is the HIP library.  Every call goes through the
+C ABI and raises SsdqError on a negative status; there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+PKG_ROOT = os.path.dirname(_HERE)
+LIB_PATH = os.path.join(PKG_ROOT, "libssdq.so")
+
+# GgmlType ids, src/model/gguf.rs:17-48
+F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, BF16 = 0, 1, 2, 8, 12, 14, 30
+QUANT_TYPES = (Q4_0, Q8_0, Q4_K, Q6_K)
+TYPE_NAMES = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K"}
+
+OK = 0
+WARN_UNSUPPORTED_ZEROED = 1
+
+
+class SsdqError(RuntimeError):
+    def __init__(self, fn: str, code: int, msg: str):
+        super().__init__(f"{fn} failed with status {code}: {msg}")
+        self.code = code
+
+
+_c = ctypes
+_vp, _sz, _i = _c.c_void_p, _c.c_size_t, _c.c_int
+
+# name -> (restype, argtypes); mirrors include/ssdq.h
+SIGNATURES = {
+    "ssdq_abi_version": (_i, []),
+    "ssdq_last_error": (_c.c_char_p, []),
+    "ssdq_block_size": (_sz, [_i]),
+    "ssdq_type_size": (_sz, [_i]),
+    "ssdq_row_bytes": (_sz, [_i, _sz]),
+    "ssdq_ctx_create": (_i, [_i, _c.POINTER(_vp)]),
+    "ssdq_ctx_destroy": (None, [_vp]),
+    "ssdq_ctx_device": (_i, [_vp]),
+    "ssdq_dequant_dev": (_i, [_i, _vp, _sz, _vp, _vp]),
+    "ssdq_matvec_dev": (_i, [_i, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    "ssdq_matvec_generic_dev": (_i, [_i, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    "ssdq_matvec_quantized": (_i, [_vp, _vp, _sz, _vp, _sz, _sz, _sz, _i, _vp]),
+    "ssdq_gemm_q4k_bf16_dev": (_i, [_vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    "ssdq_kv_quantize_rows_dev": (_i, [_vp, _vp, _vp, _sz, _sz, _vp]),
+    "ssdq_kv_dequantize_rows_dev": (_i, [_vp, _vp, _vp, _sz, _sz, _vp]),
+    "ssdq_paged_kv_append_dev": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _vp]),
+    "ssdq_paged_attention_int8_dev": (
+        _i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _vp]),
+    "ssdq_flash_attention_f32_dev": (_i, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _vp]),
+    "ssdq_flash_attention_f32": (_i, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _vp]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+def lib() -> ctypes.CDLL:
+    """Load libssdq.so (built in-tree by __graft_entry__.build()); raises if absent."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise FileNotFoundError(
+                    f"{LIB_PATH} is missing: build it first (python -c 'import __graft_entry__ as g; g.build()')")
+            l = ctypes.CDLL(LIB_PATH)
+            for name, (res, args) in SIGNATURES.items():
+                f = getattr(l, name)
+                f.restype = res
+                f.argtypes = args
+            _lib = l
+    return _lib
+
+
+def last_error() -> str:
+    return (lib().ssdq_last_error() or b"").decode()
+
+
+def check(fn: str, rc: int) -> int:
+    if rc < 0:
+        raise SsdqError(fn, rc, last_error())
+    return rc
+
+
+def block_size(dtype: int) -> int:
+    return lib().ssdq_block_size(dtype)
+
+
+def type_size(dtype: int) -> int:
+    return lib().ssdq_type_size(dtype)
+
+
+def row_bytes(dtype: int, in_dim: int) -> int:
+    return lib().ssdq_row_bytes(dtype, in_dim)
+
+
+# ----------------------------------------------------------- torch helpers
+def _ptr(t):
+    if t is None:
+        return None
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream=None):
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def dequant(dtype, w, n_elements, out, stream=None):
+    return check("ssdq_dequant_dev",
+                 lib().ssdq_dequant_dev(dtype, _ptr(w), n_elements, _ptr(out), _stream(stream)))
+
+
+def matvec(dtype, w, x, y, out_dim, in_dim, batch=1, stream=None, generic=False):
+    f = lib().ssdq_matvec_generic_dev if generic else lib().ssdq_matvec_dev
+    return check("ssdq_matvec_dev",
+                 f(dtype, _ptr(w), _ptr(x), _ptr(y), out_dim, in_dim, batch, _stream(stream)))
+
+
+def gemm_q4k_bf16(w, x_bf16, y, M, N, K, stream=None):
+    return check("ssdq_gemm_q4k_bf16_dev",
+                 lib().ssdq_gemm_q4k_bf16_dev(_ptr(w), _ptr(x_bf16), _ptr(y), M, N, K,
+                                              _stream(stream)))
+
+
+def kv_quantize_rows(x, codes, scales, n_rows, row_len, stream=None):
+    return check("ssdq_kv_quantize_rows_dev",
+                 lib().ssdq_kv_quantize_rows_dev(_ptr(x), _ptr(codes), _ptr(scales), n_rows,
+                                                 row_len, _stream(stream)))
+
+
+def kv_dequantize_rows(codes, scales, out, n_rows, row_len, stream=None):
+    return check("ssdq_kv_dequantize_rows_dev",
+                 lib().ssdq_kv_dequantize_rows_dev(_ptr(codes), _ptr(scales), _ptr(out), n_rows,
+                                                   row_len, _stream(stream)))
+
+
+def paged_kv_append(k, v, slot_mapping, k_codes, k_scales, v_codes, v_scales, n_tokens, kv_dim,
+                    stream=None):
+    return check("ssdq_paged_kv_append_dev",
+                 lib().ssdq_paged_kv_append_dev(_ptr(k), _ptr(v), _ptr(slot_mapping),
+                                                _ptr(k_codes), _ptr(k_scales), _ptr(v_codes),
+                                                _ptr(v_scales), n_tokens, kv_dim, _stream(stream)))
+
+
+def paged_attention_int8(q, k_codes, k_scales, v_codes, v_scales, block_tables, ctx_lens, out,
+                         n_seq, n_head, n_head_kv, head_dim, block_size, max_blocks_per_seq,
+                         max_ctx, stream=None):
+    return check("ssdq_paged_attention_int8_dev",
+                 lib().ssdq_paged_attention_int8_dev(
+                     _ptr(q), _ptr(k_codes), _ptr(k_scales), _ptr(v_codes), _ptr(v_scales),
+                     _ptr(block_tables), _ptr(ctx_lens), _ptr(out), n_seq, n_head, n_head_kv,
+                     head_dim, block_size, max_blocks_per_seq, max_ctx, _stream(stream)))
+
+
+def flash_attention_f32(q, k, v, out, n_head, n_head_kv, head_dim, seq_len, window_start,
+                        window_end, stream=None):
+    return check("ssdq_flash_attention_f32_dev",
+                 lib().ssdq_flash_attention_f32_dev(_ptr(q), _ptr(k), _ptr(v), _ptr(out), n_head,
+                                                    n_head_kv, head_dim, seq_len, window_start,
+                                                    window_end, _stream(stream)))
+
+
+class Context:
+    """Host-pointer API with the MetalCompute contract (synchronous, copies in/out)."""
+
+    def __init__(self, device: int = -1):
+        h = ctypes.c_void_p()
+        check("ssdq_ctx_create", lib().ssdq_ctx_create(device, ctypes.byref(h)))
+        self._h = h
+
+    def close(self):
+        if self._h:
+            lib().ssdq_ctx_destroy(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def matvec_quantized(self, w_raw, x, out_dim, in_dim, dtype):
+        """numpy in, numpy out: MetalCompute::matvec_quantized (compute.rs:157-191)."""
+        import numpy as np
+        w_raw = np.ascontiguousarray(w_raw, dtype=np.uint8)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.empty(out_dim, np.float32)
+        rc = lib().ssdq_matvec_quantized(self._h, w_raw.ctypes.data, w_raw.size, x.ctypes.data,
+                                         x.size, out_dim, in_dim, dtype, y.ctypes.data)
+        check("ssdq_matvec_quantized", rc)
+        return y
+
+    def flash_attention_f32(self, q, k, v, n_head, n_head_kv, head_dim, seq_len, window_start,
+                            window_end):
+        import numpy as np
+        q = np.ascontiguousarray(q, dtype=np.float32)
+        k = np.ascontiguousarray(k, dtype=np.float32)
+        v = np.ascontiguousarray(v, dtype=np.float32)
+        out = np.empty(n_head * head_dim, np.float32)
+        rc = lib().ssdq_flash_attention_f32(self._h, q.ctypes.data, k.ctypes.data, v.ctypes.data,
+                                            n_head, n_head_kv, head_dim, seq_len, window_start,
+                                            window_end, out.ctypes.data)
+        check("ssdq_flash_attention_f32", rc)
+        return out

@@ -1,0 +1,96 @@
+"""Seeded synthetic inputs for the quantized compute path (numpy, host side).
+
+Distributions follow the benchmark configurations of the reference path:
+  Q4_0  d ~ U[0.002, 0.02] stored as f16 (round to nearest even), 16 random
+        code bytes per 32-element block (value = (q - 8) * d, streamer.rs:153-178)
+  Q8_0  d ~ U[0.002, 0.02] -> f16, int8 codes uniform in [-127, 127]
+  Q4_K  d, dmin ~ U[0.001, 0.01] -> f16, 12 uniform scale bytes (uniform 6-bit
+        fields under the reference unpacking, compute.rs:724-731), 128 random
+        code bytes
+  Q6_K  d ~ U[0.001, 0.01] -> f16, random ql / qh bytes, int8 scales uniform in
+        [-32, 31] (6-bit range)
+  activations / K / V / Q  ~ N(0, 1) f32; bf16 activations are the f32 draws
+        rounded to nearest even.
+Both the device path and the CPU oracle consume the same bytes, so any seeded
+generator works; numpy's PCG64 keeps generation fast at full sizes.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from . import Q4_0, Q8_0, Q4_K, Q6_K
+
+BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
+
+
+def rng(seed: int) -> np.random.Generator:
+    return np.random.default_rng(seed)
+
+
+def _f16_bytes(vals: np.ndarray) -> np.ndarray:
+    return vals.astype(np.float16).view(np.uint8).reshape(-1, 2)
+
+
+def quant_weights(dtype: int, out_dim: int, in_dim: int, seed: int) -> np.ndarray:
+    """Raw GGUF blocks for an out_dim x in_dim matrix, shape [out_dim * row_bytes] uint8."""
+    bs, bb = BLOCK[dtype]
+    nb = out_dim * (in_dim // bs)
+    g = rng(seed)
+    blk = np.empty((nb, bb), np.uint8)
+    if dtype == Q4_0:
+        blk[:, 0:2] = _f16_bytes(g.uniform(0.002, 0.02, nb).astype(np.float32))
+        blk[:, 2:18] = g.integers(0, 256, (nb, 16), dtype=np.uint8)
+    elif dtype == Q8_0:
+        blk[:, 0:2] = _f16_bytes(g.uniform(0.002, 0.02, nb).astype(np.float32))
+        blk[:, 2:34] = g.integers(-127, 128, (nb, 32), dtype=np.int16).astype(np.int8).view(np.uint8)
+    elif dtype == Q4_K:
+        blk[:, 0:2] = _f16_bytes(g.uniform(0.001, 0.01, nb).astype(np.float32))
+        blk[:, 2:4] = _f16_bytes(g.uniform(0.001, 0.01, nb).astype(np.float32))
+        blk[:, 4:144] = g.integers(0, 256, (nb, 140), dtype=np.uint8)
+    elif dtype == Q6_K:
+        blk[:, 0:192] = g.integers(0, 256, (nb, 192), dtype=np.uint8)
+        blk[:, 192:208] = g.integers(-32, 32, (nb, 16), dtype=np.int16).astype(np.int8).view(np.uint8)
+        blk[:, 208:210] = _f16_bytes(g.uniform(0.001, 0.01, nb).astype(np.float32))
+    else:
+        raise ValueError(f"unsupported dtype {dtype}")
+    return blk.reshape(-1)
+
+
+def normal_f32(shape, seed: int) -> np.ndarray:
+    return rng(seed).standard_normal(shape, dtype=np.float32)
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even f32 -> bf16 bit patterns (uint16)."""
+    b = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    lsb = (b >> 16) & 1
+    r = ((b + 0x7FFF + lsb) >> 16).astype(np.uint16)
+    nan = np.isnan(x)
+    if nan.any():
+        r[nan] = ((b[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+def bf16_bits_to_f32(h: np.ndarray) -> np.ndarray:
+    return (h.astype(np.uint32) << 16).view(np.float32)
+
+
+def block_tables(n_seq: int, blocks_per_seq: int, seed: int, n_phys: int | None = None):
+    """Random permutation of the physical blocks, [n_seq, blocks_per_seq] int32."""
+    n_phys = n_phys or n_seq * blocks_per_seq
+    perm = rng(seed).permutation(n_phys).astype(np.int32)
+    return perm[: n_seq * blocks_per_seq].reshape(n_seq, blocks_per_seq)
+
+
+def slot_mapping(tables: np.ndarray, ctx_lens, block_size: int) -> np.ndarray:
+    """Pool row of every (sequence, position) in order: table[p // bs] * bs + p % bs."""
+    out = []
+    for s, n in enumerate(ctx_lens):
+        p = np.arange(n)
+        out.append(tables[s, p // block_size].astype(np.int64) * block_size + p % block_size)
+    return np.concatenate(out).astype(np.int32) if out else np.zeros(0, np.int32)
+
+
+# Seeds per configuration (stable across tests and the benchmark)
+def seed(config: int, tensor: int) -> int:
+    return 0x55D00000 + 16 * config + tensor

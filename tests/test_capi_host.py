@@ -1,0 +1,69 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol the
+header declares, and its pure-host helpers agree with the GGUF type table."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import ssdq
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "ssdq.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ssdq_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_boundary():
+    names = declared_functions()
+    for required in ("ssdq_matvec_dev", "ssdq_matvec_quantized", "ssdq_dequant_dev",
+                     "ssdq_gemm_q4k_bf16_dev", "ssdq_kv_quantize_rows_dev",
+                     "ssdq_kv_dequantize_rows_dev", "ssdq_paged_kv_append_dev",
+                     "ssdq_paged_attention_int8_dev", "ssdq_flash_attention_f32_dev",
+                     "ssdq_flash_attention_f32", "ssdq_ctx_create", "ssdq_ctx_destroy"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ssdq.lib()
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+    # and the Python binding covers all of them with signatures
+    assert set(declared_functions()) <= set(ssdq.SIGNATURES)
+
+
+def test_type_helpers():
+    assert ssdq.lib().ssdq_abi_version() == 1
+    for dt, bs, ts in ((ssdq.Q4_0, 32, 18), (ssdq.Q8_0, 32, 34), (ssdq.Q4_K, 256, 144),
+                       (ssdq.Q6_K, 256, 210)):
+        assert ssdq.block_size(dt) == bs and ssdq.type_size(dt) == ts
+        assert ssdq.row_bytes(dt, 4096) == 4096 // bs * ts
+        assert ssdq.row_bytes(dt, 4096 + bs - 1) == 4096 // bs * ts  # partial block ignored
+    assert ssdq.block_size(99) == 0 and ssdq.row_bytes(99, 4096) == 0
+
+
+def test_null_arguments_are_rejected_without_a_device():
+    lib = ssdq.lib()
+    # zero-sized calls are no-ops; NULL outputs are argument errors, checked before any HIP call
+    assert lib.ssdq_matvec_dev(ssdq.Q4_K, None, None, None, 0, 4096, 1, None) == 0
+    assert lib.ssdq_matvec_dev(ssdq.Q4_K, None, None, None, 16, 4096, 1, None) == -1
+    assert "NULL" in ssdq.last_error()
+    assert lib.ssdq_kv_quantize_rows_dev(None, None, None, 4, 16, None) == -1
+    assert lib.ssdq_paged_attention_int8_dev(*([None] * 8), 1, 8, 2, 100, 16, 4, 64, None) == -1
+    assert lib.ssdq_gemm_q4k_bf16_dev(None, None, None, 4, 4, 256, None) == -1
+
+
+def test_ctx_create_reports_missing_device():
+    try:
+        import torch
+        if torch.cuda.is_available():
+            pytest.skip("a GPU is present")
+    except ImportError:
+        pass
+    h = ctypes.c_void_p()
+    rc = ssdq.lib().ssdq_ctx_create(-1, ctypes.byref(h))
+    assert rc == -4 and not h.value  # SSDQ_ERR_NO_DEVICE: callers keep their CPU path

@@ -1,0 +1,164 @@
+"""Fused dequant-matvec parity (matvec_*_cpu, src/metal/compute.rs:680-925).
+
+Tolerance: |gpu - ref| <= 1e-4 + 1e-3 |ref| against the serial fp32 oracle,
+with the exact-sum substitution of helpers.assert_close_attributed where the
+reference's own fp32 chain is off by more than half a tolerance.
+"""
+import numpy as np
+import pytest
+import torch
+
+import encoders as enc
+import ssdq
+import ssdq_oracle as o
+from helpers import (announce, assert_close, assert_close_attributed, empty_dev, from_dev,
+                     to_dev)
+from ssdq import synth
+
+pytestmark = pytest.mark.gpu
+
+Q4_0, Q8_0, Q4_K, Q6_K = ssdq.Q4_0, ssdq.Q8_0, ssdq.Q4_K, ssdq.Q6_K
+
+
+def run(dtype, w, x, out_dim, in_dim, batch=1, generic=False, w_dev=None):
+    y = empty_dev(out_dim * batch, torch.float32)
+    rc = ssdq.matvec(dtype, w_dev if w_dev is not None else to_dev(w), to_dev(x), y, out_dim,
+                     in_dim, batch, generic=generic)
+    return from_dev(y), rc
+
+
+def reference(dtype, w, x, out_dim, in_dim, batch=1):
+    x = np.asarray(x, np.float32).reshape(batch, -1)
+    ys, ex = [], []
+    for b in range(batch):
+        ys.append(o.matvec(dtype, w, x[b], out_dim, in_dim, threads=16)[0])
+        ex.append(o.matvec_exact(dtype, w, x[b], out_dim, in_dim))
+    return np.concatenate(ys), np.concatenate(ex)
+
+
+CONFIGS = [
+    # (dtype, out_dim, in_dim, batch, label)
+    (Q4_0, 4096, 4096, 1, "config1"),
+    (Q4_0, 14336, 4096, 1, "north-star Q4_0"),
+    (Q8_0, 11008, 4096, 1, "config2 B=1"),
+    (Q8_0, 11008, 4096, 4, "config2 B=4"),
+    (Q8_0, 11008, 4096, 8, "config2 B=8"),
+    (Q4_K, 14336, 4096, 1, "config3 W_up"),
+    (Q6_K, 4096, 14336, 1, "config3 W_down"),
+]
+
+
+@pytest.mark.parametrize("dtype,out_dim,in_dim,batch,label", CONFIGS)
+def test_matvec_configs(dtype, out_dim, in_dim, batch, label):
+    cfg = 1 if "config1" in label else 2 if "config2" in label else 3
+    w = synth.quant_weights(dtype, out_dim, in_dim, synth.seed(cfg, 0))
+    x = synth.normal_f32((batch, in_dim), synth.seed(cfg, 1 + batch))
+    announce("matvec", label, ssdq.TYPE_NAMES[dtype], out_dim, in_dim, batch)
+    y, rc = run(dtype, w, x, out_dim, in_dim, batch)
+    ref, exact = reference(dtype, w, x, out_dim, in_dim, batch)
+    assert rc == 0
+    n = assert_close_attributed(y, ref, exact, label)
+    print(f"{label}: {n} ill-conditioned outputs compared to the exact sum")
+
+
+@pytest.mark.parametrize("dtype", ssdq.QUANT_TYPES)
+def test_generic_kernel_matches(dtype):
+    in_dim = 4096 if dtype != Q6_K else 14336 // 2
+    w = synth.quant_weights(dtype, 300, in_dim, 41)
+    x = synth.normal_f32((3, in_dim), 42)
+    announce("matvec generic", ssdq.TYPE_NAMES[dtype])
+    y, rc = run(dtype, w, x, 300, in_dim, 3, generic=True)
+    ref, exact = reference(dtype, w, x, 300, in_dim, 3)
+    assert rc == 0
+    assert_close_attributed(y, ref, exact, "generic")
+
+
+@pytest.mark.parametrize("dtype", ssdq.QUANT_TYPES)
+def test_misaligned_weights_take_generic_path(dtype):
+    out_dim, in_dim = 65, 1024
+    w = synth.quant_weights(dtype, out_dim, in_dim, 43)
+    buf = torch.zeros(w.size + 16, dtype=torch.uint8, device="cuda")
+    buf[1:1 + w.size] = to_dev(w)
+    x = synth.normal_f32(in_dim, 44)
+    announce("matvec misaligned", ssdq.TYPE_NAMES[dtype])
+    y, rc = run(dtype, None, x, out_dim, in_dim, 1, w_dev=buf[1:])
+    ref, exact = reference(dtype, w, x, out_dim, in_dim)
+    assert rc == 0
+    assert_close_attributed(y, ref, exact, "misaligned")
+
+
+ODD = [
+    (Q4_0, 1, 32, 1), (Q4_0, 3, 96, 2), (Q4_0, 257, 4096 + 17, 3), (Q4_0, 70, 32 * 9, 1),
+    (Q8_0, 5, 64, 5), (Q8_0, 129, 32 * 7, 7), (Q8_0, 64, 8192, 16),
+    (Q4_K, 1, 256, 1), (Q4_K, 33, 256 * 3, 6), (Q4_K, 200, 256 * 40 + 100, 2), (Q4_K, 64, 4096, 9),
+    (Q6_K, 2, 256, 1), (Q6_K, 31, 256 * 5, 3), (Q6_K, 100, 256 * 7, 8),
+]
+
+
+@pytest.mark.parametrize("dtype,out_dim,in_dim,batch", ODD)
+def test_ragged_shapes(dtype, out_dim, in_dim, batch):
+    w = synth.quant_weights(dtype, out_dim, in_dim, 50 + out_dim)
+    x = synth.normal_f32((batch, in_dim), 51 + in_dim)
+    announce("matvec ragged", ssdq.TYPE_NAMES[dtype], out_dim, in_dim, batch)
+    y, rc = run(dtype, w, x, out_dim, in_dim, batch)
+    ref, exact = reference(dtype, w, x, out_dim, in_dim, batch)
+    assert rc == 0
+    assert_close_attributed(y, ref, exact, "ragged")
+
+
+def test_q4_k_closed_form_all_scales():
+    # 64 rows, row i uses 6-bit scales / mins (i + 7 sb) % 64 and (3 i + 11 sb + 5) % 64,
+    # d = 1, dmin = 0.5, q = j % 16, x = 1 -> exact integers / halves
+    rows = []
+    want = []
+    q = np.arange(256) % 16
+    for i in range(64):
+        s = (i + 7 * np.arange(8)) % 64
+        m = (3 * i + 11 * np.arange(8) + 5) % 64
+        rows.append(enc.enc_q4_k(enc.f16_bits(1.0), enc.f16_bits(0.5), s, m, q))
+        want.append((s * q.reshape(8, 32).sum(1)).sum() - 0.5 * (m * 32).sum())
+    w = np.concatenate(rows)
+    announce("matvec q4_k closed form")
+    y, _ = run(Q4_K, w, np.ones(256, np.float32), 64, 256)
+    assert np.array_equal(y, np.array(want, np.float32))
+
+
+def test_reference_known_answers_through_host_twin():
+    # compute.rs:2347-2381 through the MetalCompute-style synchronous API
+    with ssdq.Context() as ctx:
+        blk = np.concatenate([np.array([0x00, 0x3C], np.uint8), np.full(16, 0x88, np.uint8)])
+        announce("host twin KAT")
+        assert abs(ctx.matvec_quantized(blk, np.ones(32, np.float32), 1, 32, Q4_0)[0]) < 1e-5
+        blk = np.concatenate([np.array([0x00, 0x3C], np.uint8), np.ones(32, np.uint8)])
+        assert abs(ctx.matvec_quantized(blk, np.ones(32, np.float32), 1, 32, Q8_0)[0] - 32.0) < 1e-3
+        # a short weight buffer is an error, not a crash
+        with pytest.raises(ssdq.SsdqError):
+            ctx.matvec_quantized(blk[:20], np.ones(32, np.float32), 1, 32, Q8_0)
+        # unsupported dtype -> zeros (compute.rs:672-675)
+        y = ctx.matvec_quantized(np.zeros(64, np.uint8), np.ones(32, np.float32), 3, 32, 3)
+        assert np.all(y == 0)
+        # a config-sized call through the host twin
+        w = synth.quant_weights(Q4_K, 1024, 4096, 61)
+        x = synth.normal_f32(4096, 62)
+        y = ctx.matvec_quantized(w, x, 1024, 4096, Q4_K)
+        ref, exact = reference(Q4_K, w, x, 1024, 4096)
+        assert_close_attributed(y, ref, exact, "host twin")
+
+
+def test_unsupported_dtype_zero_fills_device():
+    y = empty_dev(16, torch.float32)
+    y.fill_(3.0)
+    x = to_dev(np.ones(64, np.float32))
+    announce("matvec unsupported")
+    rc = ssdq.matvec(3, x, x, y, 16, 64)
+    assert rc == ssdq.WARN_UNSUPPORTED_ZEROED and np.all(from_dev(y) == 0)
+
+
+def test_repeat_is_deterministic():
+    w = synth.quant_weights(Q4_K, 14336, 4096, 7)
+    x = synth.normal_f32(4096, 8)
+    wd = to_dev(w)
+    announce("matvec determinism")
+    a, _ = run(Q4_K, None, x, 14336, 4096, w_dev=wd)
+    b, _ = run(Q4_K, None, x, 14336, 4096, w_dev=wd)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))

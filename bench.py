@@ -1,0 +1,280 @@
+"""Benchmark of the quantized compute path on one MI355X.
+
+Headline workload (BASELINE metric "quant matvec HBM GB/s (% of peak) at
+14336x4096 b=1; decode-attn tok/s @32k ctx"): one step = one batch-1 Q4_K
+matvec of the Llama-3-8B FFN up projection (W 14336x4096, config 3), with the
+weights resident in HBM.  Steps rotate over enough weight copies that the
+working set exceeds twice the 256 MB last-level cache, so every step streams
+W from HBM.  value = algorithmic bytes per step * steps / elapsed.
+
+The JSON line also carries, measured the same way in shorter runs, the other
+configurations (Q4_0 at the target shape and 4096^2, Q8_0 B=1/4/8, Q6_K, the
+prefill GEMM, INT8 KV quantization and paged INT8 decode attention), the
+roofline record of the headline kernel and the CPU oracle baseline.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "ssd-llm_amd"))
+
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+LLC_BYTES = 256 << 20
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--no-extras", action="store_true", help="only the headline workload")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--graph", action="store_true", help="replay steps from a captured HIP graph")
+    return ap.parse_args()
+
+
+def copies_for(nbytes):
+    return max(2, min(64, (2 * LLC_BYTES) // max(1, nbytes) + 1))
+
+
+class Timer:
+    """Events on the stream the kernels are launched on (torch's current stream)."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.e0 = torch.cuda.Event(enable_timing=True)
+        self.e1 = torch.cuda.Event(enable_timing=True)
+
+    def run(self, fn, steps, warmup):
+        torch = self.torch
+        for i in range(warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        self.e0.record()
+        for i in range(steps):
+            fn(i)
+        self.e1.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        return self.e0.elapsed_time(self.e1) * 1e-3, wall  # seconds (events), seconds (host)
+
+
+def matvec_case(torch, ssdq, synth, dtype, out_dim, in_dim, batch, seed_cfg):
+    rb = ssdq.row_bytes(dtype, in_dim)
+    wbytes = out_dim * rb
+    n = copies_for(wbytes)
+    base = torch.from_numpy(synth.quant_weights(dtype, out_dim, in_dim, synth.seed(seed_cfg, 0))).cuda()
+    ws = [base] + [base.clone() for _ in range(n - 1)]
+    x = torch.randn(batch * in_dim, device="cuda")
+    y = torch.empty(batch * out_dim, device="cuda")
+    algo_bytes = wbytes + 4 * batch * (in_dim + out_dim)
+
+    def step(i):
+        ssdq.matvec(dtype, ws[i % n], x, y, out_dim, in_dim, batch)
+
+    return step, algo_bytes, 2.0 * batch * out_dim * (in_dim // ssdq.block_size(dtype)) * ssdq.block_size(dtype)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 (multi-GPU sharding is "
+                                   "described in DESIGN.md, not run)"}))
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    import ssdq
+    from ssdq import synth
+
+    torch.cuda.set_device(0)
+    timer = Timer(torch)
+
+    # ---------------------------------------------------------- headline
+    step, algo_bytes, _ = matvec_case(torch, ssdq, synth, ssdq.Q4_K, 14336, 4096, 1, 3)
+    if args.graph:
+        chunk = 50
+        g = torch.cuda.CUDAGraph()
+        for i in range(3):
+            step(i)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            for i in range(chunk):
+                step(i)
+        reps = max(1, args.steps // chunk)
+        t_ev, wall = timer.run(lambda i: g.replay(), reps, max(1, args.warmup // chunk))
+        steps = reps * chunk
+    else:
+        steps = args.steps
+        t_ev, wall = timer.run(step, steps, args.warmup)
+    sec_per_step = t_ev / steps
+    value = algo_bytes / sec_per_step / 1e9
+
+    result = {
+        "metric": "quant matvec HBM GB/s (% of peak) at 14336x4096 b=1; decode-attn tok/s @32k ctx",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(sec_per_step * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_k weights, f32 activations and accumulation",
+        "data": "synthetic (seeded GGUF Q4_K blocks per config 3, x ~ N(0,1)); weights HBM-resident, "
+                "rotated over copies larger than 2x the last-level cache",
+        "config": {"workload": "Q4_K matvec 14336x4096 batch 1 (Llama-3-8B FFN up, config 3)",
+                   "out_dim": 14336, "in_dim": 4096, "batch": 1,
+                   "weight_copies": copies_for(14336 * ssdq.row_bytes(ssdq.Q4_K, 4096)),
+                   "graph": bool(args.graph)},
+        "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "roofline": {
+            "bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(value / HBM_PEAK_GBS, 4),
+            "traffic": traffic_from_profiles("q4k_matvec_14336x4096"),
+            "kernel": "mv_fast<Q4_K,B=1>", "algo_bytes_per_launch": algo_bytes,
+        },
+        "host_wall_s": round(wall, 4),
+    }
+
+    if not args.no_extras:
+        result["extras"] = extras(torch, ssdq, synth, timer, np)
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(np, synth, ssdq, sec_per_step)
+    print(json.dumps(result))
+
+
+def traffic_from_profiles(key):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
+    calibrated on a copy kernel), recorded in profiles/hbm_traffic.txt."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.txt")
+    try:
+        for line in open(path):
+            parts = line.split()
+            if len(parts) >= 2 and parts[0] == key:
+                return float(parts[1])
+    except OSError:
+        pass
+    return None
+
+
+def extras(torch, ssdq, synth, timer, np):
+    out = {}
+    cases = [
+        ("q4_0_matvec_14336x4096_b1", ssdq.Q4_0, 14336, 4096, 1, 1),
+        ("q4_0_matvec_4096x4096_b1", ssdq.Q4_0, 4096, 4096, 1, 1),
+        ("q8_0_matvec_11008x4096_b1", ssdq.Q8_0, 11008, 4096, 1, 2),
+        ("q8_0_matvec_11008x4096_b4", ssdq.Q8_0, 11008, 4096, 4, 2),
+        ("q8_0_matvec_11008x4096_b8", ssdq.Q8_0, 11008, 4096, 8, 2),
+        ("q6_k_matvec_4096x14336_b1", ssdq.Q6_K, 4096, 14336, 1, 3),
+    ]
+    for name, dt, od, idim, b, cfg in cases:
+        step, nbytes, _ = matvec_case(torch, ssdq, synth, dt, od, idim, b, cfg)
+        t, _ = timer.run(step, 200, 20)
+        gbs = nbytes / (t / 200) / 1e9
+        out[name] = {"GB/s": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+                     "us": round(t / 200 * 1e6, 3)}
+        torch.cuda.empty_cache()
+
+    # config 4: one Llama-3-8B layer of Q4_K prefill GEMMs at M = 512
+    layer = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
+             ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]
+    M = 512
+    mats = []
+    flops = 0
+    for i, (nm, N, K) in enumerate(layer):
+        w = torch.from_numpy(synth.quant_weights(ssdq.Q4_K, N, K, synth.seed(4, i))).cuda()
+        x = torch.randn(M, K, device="cuda").to(torch.bfloat16).view(torch.int16)
+        y = torch.empty(M * N, device="cuda")
+        mats.append((w, x, y, N, K))
+        flops += 2.0 * M * N * K
+
+    def layer_step(i):
+        for w, x, y, N, K in mats:
+            ssdq.gemm_q4k_bf16(w, x, y, M, N, K)
+
+    t, _ = timer.run(layer_step, 5, 1)
+    tfl = flops / (t / 5) / 1e12
+    out["prefill_gemm_q4k_layer_m512"] = {"TFLOP/s": round(tfl, 2),
+                                          "pct_bf16_peak": round(100 * tfl / BF16_PEAK_TFLOPS, 2),
+                                          "ms_per_layer": round(t / 5 * 1e3, 3)}
+    del mats
+    torch.cuda.empty_cache()
+
+    # config 5a: INT8 quantize of 8 x 32768 tokens x {K, V} x 1024
+    n_rows, dim = 8 * 32768 * 2, 1024
+    xk = torch.randn(n_rows * dim, device="cuda")
+    codes = torch.empty(n_rows * dim, dtype=torch.int8, device="cuda")
+    scales = torch.empty(n_rows, device="cuda")
+    t, _ = timer.run(lambda i: ssdq.kv_quantize_rows(xk, codes, scales, n_rows, dim), 20, 3)
+    qbytes = n_rows * dim * 5 + n_rows * 4
+    out["kv_int8_quantize_8x32768x2x1024"] = {"GB/s": round(qbytes / (t / 20) / 1e9, 1),
+                                              "pct_hbm_peak": round(100 * qbytes / (t / 20) / 1e9 / HBM_PEAK_GBS, 2),
+                                              "us": round(t / 20 * 1e6, 1)}
+    del xk
+    # config 5b: paged INT8 GQA decode attention, reusing the quantized pool
+    n_seq, n_head, n_kv, hd, bs, ctx = 8, 32, 8, 128, 16, 32768
+    mb = ctx // bs
+    kc = codes[: n_seq * mb * bs * n_kv * hd]
+    vc = codes[n_seq * mb * bs * n_kv * hd:]
+    ks = scales[: n_seq * mb * bs]
+    vs = scales[n_seq * mb * bs:]
+    tables = torch.from_numpy(synth.block_tables(n_seq, mb, synth.seed(5, 3))).cuda()
+    cl = torch.full((n_seq,), ctx, dtype=torch.int32, device="cuda")
+    q = torch.randn(n_seq * n_head * hd, device="cuda")
+    o = torch.empty_like(q)
+    t, _ = timer.run(lambda i: ssdq.paged_attention_int8(q, kc, ks, vc, vs, tables, cl, o, n_seq,
+                                                         n_head, n_kv, hd, bs, mb, ctx), 50, 5)
+    abytes = 536870912 + 2097152 + 131072 + 131072 + 65536
+    step_s = t / 50
+    out["paged_int8_decode_attention_32k"] = {
+        "tok/s": round(n_seq / step_s, 1), "GB/s": round(abytes / step_s / 1e9, 1),
+        "pct_hbm_peak": round(100 * abytes / step_s / 1e9 / HBM_PEAK_GBS, 2),
+        "us_per_step": round(step_s * 1e6, 2)}
+    return out
+
+
+def cpu_baseline(np, synth, ssdq, gpu_sec_per_step):
+    """The CPU oracle (C restatement of matvec_q4_k_cpu, compute.rs:707-750) on this
+    host's cores: single thread like the reference, on a bounded sample."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import ssdq_oracle as o
+    out_dim, in_dim = 14336, 4096
+    w = synth.quant_weights(ssdq.Q4_K, out_dim, in_dim, synth.seed(3, 0))
+    x = synth.normal_f32(in_dim, 1)
+    nbytes = w.size + 4 * (in_dim + out_dim)
+    o.matvec(ssdq.Q4_K, w, x, out_dim, in_dim)  # warm-up
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        o.matvec(ssdq.Q4_K, w, x, out_dim, in_dim)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el > 10.0 or reps >= 200:
+            break
+    st = el / reps
+    res = {"value": round(nbytes / st / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+           "sample": f"{reps} single-thread Q4_K matvecs 14336x4096 in {el:.1f} s "
+                     f"({st * 1e3:.1f} ms each) on {os.cpu_count()} visible host cores",
+           "gpu_over_cpu": round(st / gpu_sec_per_step, 1)}
+    # all-cores variant (row shards, tensor_parallel.rs:45-96)
+    nt = min(16, os.cpu_count() or 1)
+    o.matvec(ssdq.Q4_K, w, x, out_dim, in_dim, threads=nt)
+    reps2, t0 = 0, time.perf_counter()
+    while True:
+        o.matvec(ssdq.Q4_K, w, x, out_dim, in_dim, threads=nt)
+        reps2 += 1
+        el2 = time.perf_counter() - t0
+        if el2 > 5.0 or reps2 >= 500:
+            break
+    res["all_cores"] = {"value": round(nbytes / (el2 / reps2) / 1e9, 3), "unit": "GB/s", "cores": nt}
+    return res
+
+
+if __name__ == "__main__":
+    main()

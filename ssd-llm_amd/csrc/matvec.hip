@@ -34,21 +34,26 @@ namespace ssdq {
 namespace {
 
 // ------------------------------------------------------------ unit geometry
+// A "unit" is the slice of one row a lane owns:
+//   Q4_K: two sub-blocks of one super-block (64 elements, one 16-byte header)
+//   Q4_0 / Q8_0: two consecutive 18- / 34-byte blocks (64 elements, dword aligned)
+//   Q6_K: a 32-element quarter of a 210-byte block
+// E elements, NSUM x-sum groups of SUMG elements, NW dwords of raw data.
 template <int F> struct FastUnit;
 template <> struct FastUnit<kQ4_K> {
-  static constexpr int E = 32, NSUM = 1, SUMG = 32, NW = 8;
+  static constexpr int E = 64, NSUM = 2, SUMG = 32, NW = 12, PER_BLOCK = 4;
   static constexpr bool prescale = true;
 };
 template <> struct FastUnit<kQ4_0> {
-  static constexpr int E = 64, NSUM = 2, SUMG = 32, NW = 9;
+  static constexpr int E = 64, NSUM = 2, SUMG = 32, NW = 9, PER_BLOCK = 0;
   static constexpr bool prescale = true;
 };
 template <> struct FastUnit<kQ8_0> {
-  static constexpr int E = 64, NSUM = 2, SUMG = 32, NW = 17;
+  static constexpr int E = 64, NSUM = 2, SUMG = 32, NW = 17, PER_BLOCK = 0;
   static constexpr bool prescale = false;
 };
 template <> struct FastUnit<kQ6_K> {
-  static constexpr int E = 32, NSUM = 2, SUMG = 16, NW = 10;
+  static constexpr int E = 32, NSUM = 2, SUMG = 16, NW = 10, PER_BLOCK = 8;
   static constexpr bool prescale = false;
 };
 
@@ -75,9 +80,10 @@ __device__ __forceinline__ uint32_t ldh(const uint8_t* p) {
 template <int F>
 __device__ __forceinline__ void load_unit(const uint8_t* __restrict__ row, int u, uint32_t* raw) {
   if constexpr (F == kQ4_K) {
-    const uint8_t* blk = row + (size_t)(u >> 3) * 144;
+    const uint8_t* blk = row + (size_t)(u >> 2) * 144;
     ld4(blk, raw);                          // d, dmin, scales[12]
-    ld4(blk + 16 + 16 * (u & 7), raw + 4);  // qs of sub-block u&7
+    ld4(blk + 16 + 32 * (u & 3), raw + 4);  // qs of sub-block 2*(u&3)
+    ld4(blk + 32 + 32 * (u & 3), raw + 8);  // qs of sub-block 2*(u&3)+1
   } else if constexpr (F == kQ4_0) {
     const uint8_t* p = row + (size_t)u * 36;  // two 18-byte blocks, dword aligned
     ld4(p, raw);
@@ -102,46 +108,52 @@ __device__ __forceinline__ void load_unit(const uint8_t* __restrict__ row, int u
   }
 }
 
-// Decodes one unit into per-element integer-valued floats (offsets folded
-// out) and applies it to B activations.  xg(b, e): x' of element e of the unit,
+// 4-bit codes of one dword: q[2i] = low nibble of byte i, q[2i+1] = 16 * high nibble
+__device__ __forceinline__ void nibbles8(uint32_t w, float* q) {
+  const uint32_t lo = opaque(w & 0x0F0F0F0Fu);
+  const uint32_t hi = opaque(w & 0xF0F0F0F0u);  // x' of odd elements is x / 16
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    q[2 * i] = (float)byte_of(lo, i);
+    q[2 * i + 1] = (float)byte_of(hi, i);
+  }
+}
+
+// 6-bit scale / min of sub-block sb, branch-free form of the reference unpacking
+// (compute.rs:724-731): sb < 4 -> low six bits of sc[sb] / sc[sb+4]; sb >= 4 ->
+// bits 6-7 of sc[sb-4] / sc[sb] as the LOW two bits, sc[sb+4] nibbles as the high four.
+__device__ __forceinline__ void q4k_sm(uint32_t sc1, uint32_t sc2, uint32_t sc3, int sb,
+                                       float& s, float& m) {
+  const uint32_t i = sb & 3, hi = sb >> 2;
+  const uint32_t off = 8 * i + 6 * hi, wl = hi ? 2u : 6u, wh = hi ? 4u : 0u;
+  const uint32_t si = __builtin_amdgcn_ubfe(sc1, off, wl) | (__builtin_amdgcn_ubfe(sc3, 8 * i, wh) << 2);
+  const uint32_t mi = __builtin_amdgcn_ubfe(sc2, off, wl) | (__builtin_amdgcn_ubfe(sc3, 8 * i + 4, wh) << 2);
+  s = (float)si;
+  m = (float)mi;
+}
+
+// Decodes one unit into integer-valued floats (offsets folded out) and
+// applies it to B activations.  xg(b, e): x' of element e of the unit;
 // sg(b, g): sum of the raw x over sum-group g of the unit.
 template <int F, int B, class XG, class SG>
 __device__ __forceinline__ void accumulate(const uint32_t* raw, int u, XG xg, SG sg, float* acc) {
   constexpr int E = FastUnit<F>::E;
   float q[E];
-  if constexpr (F == kQ4_K || F == kQ4_0) {
-    uint32_t qd[E / 8];
-    if constexpr (F == kQ4_K) {
+  if constexpr (F == kQ4_K) {
 #pragma unroll
-      for (int k = 0; k < 4; k++) qd[k] = raw[4 + k];
-    } else {
+    for (int k = 0; k < 8; k++) nibbles8(raw[4 + k], q + 8 * k);
+  } else if constexpr (F == kQ4_0) {
 #pragma unroll
-      for (int k = 0; k < 4; k++) qd[k] = __builtin_amdgcn_alignbit(raw[k + 1], raw[k], 16);
+    for (int k = 0; k < 4; k++) nibbles8(__builtin_amdgcn_alignbit(raw[k + 1], raw[k], 16), q + 8 * k);
 #pragma unroll
-      for (int k = 0; k < 4; k++) qd[4 + k] = raw[5 + k];
-    }
-#pragma unroll
-    for (int k = 0; k < E / 8; k++) {
-      const uint32_t lo = qd[k] & 0x0F0F0F0Fu;
-      const uint32_t hi = qd[k] & 0xF0F0F0F0u;  // 16 * nibble; x' of odd elements is x/16
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        q[8 * k + 2 * i] = (float)byte_of(lo, i);
-        q[8 * k + 2 * i + 1] = (float)byte_of(hi, i);
-      }
-    }
+    for (int k = 0; k < 4; k++) nibbles8(raw[5 + k], q + 32 + 8 * k);
   } else if constexpr (F == kQ8_0) {
 #pragma unroll
-    for (int c = 0; c < 8; c++) {
-      const uint32_t v = __builtin_amdgcn_alignbit(raw[c + 1], raw[c], 16) ^ 0x80808080u;
+    for (int c = 0; c < 16; c++) {
+      const uint32_t src = c < 8 ? __builtin_amdgcn_alignbit(raw[c + 1], raw[c], 16) : raw[1 + c];
+      const uint32_t v = opaque(src ^ 0x80808080u);  // code + 128
 #pragma unroll
-      for (int i = 0; i < 4; i++) q[4 * c + i] = (float)byte_of(v, i);  // code + 128
-    }
-#pragma unroll
-    for (int c = 0; c < 8; c++) {
-      const uint32_t v = raw[9 + c] ^ 0x80808080u;
-#pragma unroll
-      for (int i = 0; i < 4; i++) q[32 + 4 * c + i] = (float)byte_of(v, i);
+      for (int i = 0; i < 4; i++) q[4 * c + i] = (float)byte_of(v, i);
     }
   } else {  // kQ6_K
     const uint32_t sh = raw[9];
@@ -157,58 +169,57 @@ __device__ __forceinline__ void accumulate(const uint32_t* raw, int u, XG xg, SG
           __builtin_amdgcn_perm(qh[k >> 1], qh[k >> 1], (k & 1) ? 0x03030202u : 0x01010000u);
       const uint32_t he = ((p << 4) & 0x00300030u) | (p & 0x30003000u);
       const uint32_t ho = ((p << 2) & 0x00300030u) | ((p >> 2) & 0x30003000u);
-      const uint32_t ee = (ql[k] & 0x0F0F0F0Fu) | he;          // elements 8k+2i
-      const uint32_t eo = ((ql[k] >> 4) & 0x0F0F0F0Fu) | ho;   // elements 8k+2i+1
+      const uint32_t ee = opaque((ql[k] & 0x0F0F0F0Fu) | he);         // q + 32, elements 8k+2i
+      const uint32_t eo = opaque(((ql[k] >> 4) & 0x0F0F0F0Fu) | ho);  // elements 8k+2i+1
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        q[8 * k + 2 * i] = (float)byte_of(ee, i);   // q + 32
+        q[8 * k + 2 * i] = (float)byte_of(ee, i);
         q[8 * k + 2 * i + 1] = (float)byte_of(eo, i);
       }
     }
   }
 
-  // Per-unit scales
-  float sA, oA, sB = 0.f, oB = 0.f;  // acc += sA*(pxA - oA*sumA) + sB*(pxB - oB*sumB)
+  // per-half scale and offset: acc += sA * pA - oA * sum_A + sB * pB - oB * sum_B
+  float sA, sB, oA, oB;
   if constexpr (F == kQ4_K) {
     const float d = f16_to_f32(raw[0] & 0xFFFFu), dmin = f16_to_f32(raw[0] >> 16);
-    uint32_t s, m;
-    q4k_scale_min(raw[1], raw[2], raw[3], u & 7, s, m);
-    sA = d * (float)s;
-    oA = dmin * (float)m;  // used as acc += S*px - M*sum
+    const int sb = 2 * (u & 3);
+    float s0, m0, s1, m1;
+    q4k_sm(raw[1], raw[2], raw[3], sb, s0, m0);
+    q4k_sm(raw[1], raw[2], raw[3], sb + 1, s1, m1);
+    sA = d * s0;
+    sB = d * s1;
+    oA = dmin * m0;
+    oB = dmin * m1;
   } else if constexpr (F == kQ4_0) {
     sA = f16_to_f32(raw[0] & 0xFFFFu);
     sB = f16_to_f32(raw[4] >> 16);
-    oA = oB = 8.0f;
+    oA = 8.0f * sA;
+    oB = 8.0f * sB;
   } else if constexpr (F == kQ8_0) {
     sA = f16_to_f32(raw[0] & 0xFFFFu);
     sB = f16_to_f32(raw[8] >> 16);
-    oA = oB = 128.0f;
+    oA = 128.0f * sA;
+    oB = 128.0f * sB;
   } else {
     const float d = f16_to_f32(raw[8] >> 16);
     sA = d * (float)(int8_t)(raw[8] & 0xFFu);
     sB = d * (float)(int8_t)((raw[8] >> 8) & 0xFFu);
-    oA = oB = 32.0f;
+    oA = 32.0f * sA;
+    oB = 32.0f * sB;
   }
 
 #pragma unroll
   for (int b = 0; b < B; b++) {
-    if constexpr (F == kQ4_K) {
-      float p0 = 0.f, p1 = 0.f;
+    float pa = 0.f, pb = 0.f;
 #pragma unroll
-      for (int e = 0; e < E; e += 2) {
-        p0 = fmaf(q[e], xg(b, e), p0);
-        p1 = fmaf(q[e + 1], xg(b, e + 1), p1);
-      }
-      acc[b] = fmaf(sA, p0 + p1, fmaf(-oA, sg(b, 0), acc[b]));
-    } else {
-      float pa = 0.f, pb = 0.f;
+    for (int e = 0; e < E / 2; e++) pa = fmaf(q[e], xg(b, e), pa);
 #pragma unroll
-      for (int e = 0; e < E / 2; e++) pa = fmaf(q[e], xg(b, e), pa);
-#pragma unroll
-      for (int e = E / 2; e < E; e++) pb = fmaf(q[e], xg(b, e), pb);
-      acc[b] = fmaf(sA, fmaf(-oA, sg(b, 0), pa), acc[b]);
-      acc[b] = fmaf(sB, fmaf(-oB, sg(b, 1), pb), acc[b]);
-    }
+    for (int e = E / 2; e < E; e++) pb = fmaf(q[e], xg(b, e), pb);
+    float a = fmaf(-oA, sg(b, 0), acc[b]);
+    a = fmaf(-oB, sg(b, 1), a);
+    a = fmaf(sA, pa, a);
+    acc[b] = fmaf(sB, pb, a);
   }
 }
 
@@ -217,33 +228,361 @@ __host__ __device__ constexpr size_t lds_floats(int U, int B) {
   return (size_t)B * U * (FastUnit<F>::E + 4) + (size_t)B * U * FastUnit<F>::NSUM;
 }
 
-// UPL > 0: B must be 1; each lane keeps x for its UPL units in registers.
-// UPL == 0: x read from LDS per use (any B).
-template <int F, int B, int R, int UPL>
-__global__ __launch_bounds__(256) void mv_fast(const uint8_t* __restrict__ w,
-                                               const float* __restrict__ x, float* __restrict__ y,
-                                               int out_dim, int in_dim, int bpr,
-                                               int rows_per_wg) {
+// Stages x' (pre-scaled, per-unit padded) for B activations into LDS.
+template <int F, int B>
+__device__ __forceinline__ void stage_x(const float* __restrict__ x, int in_dim, int keff, int U,
+                                        float* xs) {
+  using FU = FastUnit<F>;
+  constexpr int E = FU::E, ES = E + 4;
+  const int n4 = keff >> 2;  // keff is a multiple of 32
+  for (int i = threadIdx.x; i < B * n4; i += blockDim.x) {
+    const int b = i / n4, e = (i - b * n4) * 4;
+    float4 v = *reinterpret_cast<const float4*>(x + (size_t)b * in_dim + e);
+    if (FU::prescale) {  // elements e+1, e+3 are odd
+      v.y *= 0.0625f;
+      v.w *= 0.0625f;
+    }
+    const int u = e / E, t = e - u * E;
+    *reinterpret_cast<float4*>(xs + ((size_t)b * U + u) * ES + t) = v;
+  }
+}
+
+// ---------------------------------------------------------- batch 1 path
+// Integer dot products on "digit planes" of x.  Each 32-element group of x is
+// scaled by a power of two so its largest magnitude sits just under 2^22 and
+// rounded to an integer xi (|xi| <= 2^22: the rounding error is at most 2^-23
+// of the group maximum).  xi is written in three balanced base-256 digits
+// (signed bytes), and the digits of the elements that meet one weight dword are
+// packed into "planes" of four bytes.  A weight dword of 4-bit codes then
+// costs two masks and six v_dot4_i32_i8; the three per-digit integer sums of a
+// group are recombined exactly (I0 + 256 I1 + 65536 I2), converted to float
+// once and scaled by the group's power of two.  Per element this is ~1.5 VALU
+// instructions instead of a float conversion plus an FMA.
+//
+// Group record in LDS (GW dwords): 24 plane dwords [k][parity][digit] for the
+// four 8-element weight dwords k (parity 0 = elements 8k+0,2,4,6, parity 1 =
+// 8k+1,3,5,7; Q8_0 instead uses elements 8k+0..3 / 8k+4..7), the scale 2^(E-22)
+// and the sum of x over the group (two half sums for Q6_K's 16-element scales).
+template <int F> struct Dig;
+template <> struct Dig<kQ4_K> { static constexpr int NG = 2, GW = 26, US = 52; static constexpr bool contig = false; };
+template <> struct Dig<kQ4_0> { static constexpr int NG = 2, GW = 26, US = 52; static constexpr bool contig = false; };
+template <> struct Dig<kQ8_0> { static constexpr int NG = 2, GW = 26, US = 52; static constexpr bool contig = true; };
+template <> struct Dig<kQ6_K> { static constexpr int NG = 1, GW = 28, US = 28; static constexpr bool contig = false; };
+
+__device__ __forceinline__ uint32_t plane_bytes(uint32_t a, uint32_t b, uint32_t c, uint32_t e, int d) {
+  // byte d of a, b, c, e -> bytes 0, 1, 2, 3
+  const uint32_t lo = __builtin_amdgcn_perm(b, a, (uint32_t)d | ((uint32_t)(4 + d) << 8) | 0x0C0C0000u);
+  const uint32_t hi = __builtin_amdgcn_perm(e, c, 0x00000C0Cu | ((uint32_t)d << 16) | ((uint32_t)(4 + d) << 24));
+  return lo | hi;
+}
+
+// Staging of x in two phases so the x loads can be issued before the weight
+// prefetch: vector loads return in order, so x fetched after the weights would
+// wait for them.  One thread per 8 elements (the four threads of a 32-element
+// group are adjacent lanes); each thread holds up to kStageIt chunks.
+constexpr int kStageIt = 4;  // largest chunk count per thread the kernels instantiate
+
+template <int SIT>
+struct XChunks {
+  float v[SIT][8];
+};
+
+template <int SIT>
+__device__ __forceinline__ void stage_load(const float* __restrict__ x, int keff, XChunks<SIT>& st,
+                                           int nthreads) {
+  const int nchunk = keff >> 3;
+#pragma unroll
+  for (int it = 0; it < SIT; it++) {
+    const int c = it * nthreads + threadIdx.x;
+    if (c < nchunk) {
+      const float4 a = *reinterpret_cast<const float4*>(x + 8 * c);
+      const float4 b = *reinterpret_cast<const float4*>(x + 8 * c + 4);
+      st.v[it][0] = a.x; st.v[it][1] = a.y; st.v[it][2] = a.z; st.v[it][3] = a.w;
+      st.v[it][4] = b.x; st.v[it][5] = b.y; st.v[it][6] = b.z; st.v[it][7] = b.w;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; j++) st.v[it][j] = 0.f;
+    }
+  }
+}
+
+template <int F, int SIT>
+__device__ __forceinline__ void stage_store(const XChunks<SIT>& st, int keff, uint32_t* lds, int nthreads) {
+  using D = Dig<F>;
+  const int nchunk = keff >> 3;
+#pragma unroll
+  for (int it = 0; it < SIT; it++) {
+    if (it * nthreads >= nchunk) break;  // uniform across the staging waves
+    const int c = it * nthreads + threadIdx.x;
+    const bool live = c < nchunk;
+    const float* v = st.v[it];
+    float m = 0.f, s = 0.f;
+    bool bad = false;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      m = fmaxf(m, fabsf(v[j]));
+      s += v[j];
+      bad |= !(fabsf(v[j]) < INFINITY);  // NaN or infinity
+    }
+    m = fmaxf(m, dpp_mov<0xB1>(m));
+    m = fmaxf(m, dpp_mov<0x4E>(m));
+    const float s_half = s + dpp_mov<0xB1>(s);  // Q6_K: sum over this half of the group
+    s = s_half + dpp_mov<0x4E>(s_half);
+    const int k = c & 3;
+    int e = 0;
+    if (m > 0.f) (void)frexpf(m, &e);  // m < 2^e
+    const float up = ldexpf(1.0f, 22 - e);
+    uint32_t u[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const int xi = (int)rintf(v[j] * up);           // |xi| <= 2^22
+      u[j] = ((uint32_t)(xi + 0x808080)) ^ 0x808080u;  // bytes 0-2: balanced digits
+    }
+    bool gbad = bad;
+    gbad |= __shfl_xor(gbad ? 1 : 0, 1, 64) != 0;
+    gbad |= __shfl_xor(gbad ? 1 : 0, 2, 64) != 0;
+    if (live) {
+      const int g = c >> 2;
+      uint32_t* rec = lds + (size_t)(g / D::NG) * D::US + (g % D::NG) * D::GW;
+      uint32_t* pl = rec + 6 * k;
+#pragma unroll
+      for (int d = 0; d < 3; d++) {
+        if (D::contig) {
+          pl[d] = plane_bytes(u[0], u[1], u[2], u[3], d);
+          pl[3 + d] = plane_bytes(u[4], u[5], u[6], u[7], d);
+        } else {
+          pl[d] = plane_bytes(u[0], u[2], u[4], u[6], d);
+          pl[3 + d] = plane_bytes(u[1], u[3], u[5], u[7], d);
+        }
+      }
+      if (k == 0) {
+        // a non-finite input poisons its group's result instead of being rounded
+        rec[24] = __float_as_uint(gbad ? __builtin_nanf("") : ldexpf(1.0f, e - 22));
+        rec[25] = __float_as_uint(D::GW == 28 ? s_half : s);
+      }
+      if (D::GW == 28 && k == 2) rec[26] = __float_as_uint(s_half);
+    }
+  }
+}
+
+__device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
+  return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// I0 + 256 I1 + 65536 I2 (|I1| <= 2^16 so the first two combine exactly in int)
+__device__ __forceinline__ float digits_value(int i0, int i1, int i2) {
+  return fmaf(65536.0f, (float)i2, (float)(i0 + (i1 << 8)));
+}
+
+// Applies one unit (raw weight dwords) to x given as digit planes pl[] (the
+// unit's US dwords).
+template <int F, class PL>
+__device__ __forceinline__ void accumulate_dig(const uint32_t* raw, int u, PL pl, float& acc) {
+  using D = Dig<F>;
+  if constexpr (F == kQ4_K || F == kQ4_0) {
+    float sc[2], off[2];
+    if constexpr (F == kQ4_K) {
+      const float d = f16_to_f32(raw[0] & 0xFFFFu), dmin = f16_to_f32(raw[0] >> 16);
+      const int sb = 2 * (u & 3);
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        float s, m;
+        q4k_sm(raw[1], raw[2], raw[3], sb + h, s, m);
+        sc[h] = d * s;
+        off[h] = dmin * m;  // acc += S * sum(q x) - M * sum(x)
+      }
+    } else {
+      sc[0] = f16_to_f32(raw[0] & 0xFFFFu);
+      sc[1] = f16_to_f32(raw[4] >> 16);
+      off[0] = 8.0f * sc[0];  // value (q - 8) d
+      off[1] = 8.0f * sc[1];
+    }
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      int i0 = 0, i1 = 0, i2 = 0;
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        uint32_t wd;
+        if constexpr (F == kQ4_K) wd = raw[4 + 4 * h + k];
+        else wd = h == 0 ? __builtin_amdgcn_alignbit(raw[k + 1], raw[k], 16) : raw[5 + k];
+        const uint32_t lo = wd & 0x0F0F0F0Fu, hi = (wd >> 4) & 0x0F0F0F0Fu;
+        const int b = h * D::GW + 6 * k;
+        i0 = dot4(lo, pl(b + 0), i0);
+        i1 = dot4(lo, pl(b + 1), i1);
+        i2 = dot4(lo, pl(b + 2), i2);
+        i0 = dot4(hi, pl(b + 3), i0);
+        i1 = dot4(hi, pl(b + 4), i1);
+        i2 = dot4(hi, pl(b + 5), i2);
+      }
+      const float f = digits_value(i0, i1, i2);
+      const float xscale = __uint_as_float(pl(h * D::GW + 24));
+      const float xsum = __uint_as_float(pl(h * D::GW + 25));
+      acc = fmaf(sc[h] * xscale, f, fmaf(-off[h], xsum, acc));
+    }
+  } else if constexpr (F == kQ8_0) {
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const float d = h == 0 ? f16_to_f32(raw[0] & 0xFFFFu) : f16_to_f32(raw[8] >> 16);
+      int i0 = 0, i1 = 0, i2 = 0;
+#pragma unroll
+      for (int c = 0; c < 8; c++) {
+        const uint32_t wd = h == 0 ? __builtin_amdgcn_alignbit(raw[c + 1], raw[c], 16) : raw[9 + c];
+        const int b = h * D::GW + 6 * (c >> 1) + 3 * (c & 1);
+        i0 = dot4(wd, pl(b + 0), i0);
+        i1 = dot4(wd, pl(b + 1), i1);
+        i2 = dot4(wd, pl(b + 2), i2);
+      }
+      const float xscale = __uint_as_float(pl(h * D::GW + 24));
+      acc = fmaf(d * xscale, digits_value(i0, i1, i2), acc);
+    }
+  } else {  // kQ6_K quarter: 6-bit codes + 32 as bytes, two 16-element scale groups
+    const uint32_t sh = raw[9];
+    uint32_t ql[4], qh[2];
+#pragma unroll
+    for (int k = 0; k < 4; k++) ql[k] = __builtin_amdgcn_alignbit(raw[k + 1], raw[k], sh);
+#pragma unroll
+    for (int j = 0; j < 2; j++) qh[j] = __builtin_amdgcn_alignbit(raw[6 + j], raw[5 + j], sh);
+    const float d = f16_to_f32(raw[8] >> 16);
+    const float xscale = __uint_as_float(pl(24));
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      int i0 = 0, i1 = 0, i2 = 0;
+#pragma unroll
+      for (int kk = 0; kk < 2; kk++) {
+        const int k = 2 * h + kk;
+        const uint32_t p =
+            __builtin_amdgcn_perm(qh[k >> 1], qh[k >> 1], (k & 1) ? 0x03030202u : 0x01010000u);
+        const uint32_t he = ((p << 4) & 0x00300030u) | (p & 0x30003000u);
+        const uint32_t ho = ((p << 2) & 0x00300030u) | ((p >> 2) & 0x30003000u);
+        const uint32_t ee = (ql[k] & 0x0F0F0F0Fu) | he;
+        const uint32_t eo = ((ql[k] >> 4) & 0x0F0F0F0Fu) | ho;
+        const int b = 6 * k;
+        i0 = dot4(ee, pl(b + 0), i0);
+        i1 = dot4(ee, pl(b + 1), i1);
+        i2 = dot4(ee, pl(b + 2), i2);
+        i0 = dot4(eo, pl(b + 3), i0);
+        i1 = dot4(eo, pl(b + 4), i1);
+        i2 = dot4(eo, pl(b + 5), i2);
+      }
+      const float sg = d * (float)(int8_t)((raw[8] >> (8 * h)) & 0xFFu);
+      const float xsum = __uint_as_float(pl(25 + h));
+      acc = fmaf(sg * xscale, digits_value(i0, i1, i2), fmaf(-32.0f * sg, xsum, acc));
+    }
+  }
+}
+
+// Every lane keeps the digit planes of its units in registers.  KS waves split
+// each row's units (KS > 1 for long rows; partial sums meet in LDS); the
+// workgroup's other waves take other rows.  Rows are spread evenly over all
+// row streams of the grid (at most RMAX per stream).  One workgroup runs per
+// CU.  Schedule (from timelines of the kernel phases on MI355X): x is fetched
+// and staged before any weight is requested.  Requested during the weight
+// stream, x (which every CU reads, and which the previous call's weights have
+// pushed out of L2) waits behind that stream for several microseconds; fetched
+// first it arrives in about one.  Then every row of the stream is requested
+// (straight-line code, rows clamped to valid memory, so the compiler's
+// in-order wait counts stay exact) and each row is consumed as soon as its own
+// loads have returned.
+template <int F, int UPL, int RMAX, bool FULL, int SIT>
+__global__ __launch_bounds__(768) void mv_b1(const uint8_t* __restrict__ w,
+                                             const float* __restrict__ x, float* __restrict__ y,
+                                             int out_dim, int bpr, int ks) {
+  using FU = FastUnit<F>;
+  using D = Dig<F>;
+  constexpr int NW = FU::NW, US = D::US;
+  extern __shared__ uint32_t lds[];
+  const int keff = bpr * Geom<F>::bs;
+  const int U = keff / FU::E;
+  float* red = reinterpret_cast<float*>(lds + (size_t)U * US);  // [RMAX][ks]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nw = blockDim.x >> 6, kw = wave % ks, stream = wave / ks, rs = nw / ks;
+  const size_t row_bytes = (size_t)bpr * Geom<F>::bb;
+  const long n_streams = (long)gridDim.x * rs, gs = (long)blockIdx.x * rs + stream;
+  const int r_begin = (int)(gs * out_dim / n_streams);
+  const int n_rows = (int)((gs + 1) * out_dim / n_streams) - r_begin;  // <= RMAX
+  const int ubase = kw * 64 * UPL + lane;
+
+  XChunks<SIT> st;
+  stage_load<SIT>(x, keff, st, blockDim.x);
+  stage_store<F, SIT>(st, keff, lds, blockDim.x);
+  __syncthreads();
+
+  uint32_t pr[UPL][US];
+#pragma unroll
+  for (int i = 0; i < UPL; i++) {
+    const int u = ubase + 64 * i;
+    const bool ok = FULL || u < U;
+#pragma unroll
+    for (int t = 0; t < US; t += 4) {
+      const uint4 v = ok ? *reinterpret_cast<const uint4*>(lds + (size_t)u * US + t) : make_uint4(0, 0, 0, 0);
+      pr[i][t] = v.x; pr[i][t + 1] = v.y; pr[i][t + 2] = v.z; pr[i][t + 3] = v.w;
+    }
+  }
+
+  uint32_t buf[RMAX][UPL][NW];
+#pragma unroll
+  for (int rr = 0; rr < RMAX; rr++) {
+    const int row = max(0, min(r_begin + rr, out_dim - 1));
+    const uint8_t* rp = w + (size_t)row * row_bytes;
+#pragma unroll
+    for (int i = 0; i < UPL; i++) {
+      const int u = ubase + 64 * i;
+      if (FULL || u < U) load_unit<F>(rp, u, buf[rr][i]);
+    }
+  }
+
+  float acc[RMAX];
+#pragma unroll
+  for (int rr = 0; rr < RMAX; rr++) {
+    float a = 0.f;
+    if (ks > 1 || rr < n_rows) {  // uniform per wave: padding rows are not computed
+#pragma unroll
+      for (int i = 0; i < UPL; i++) {
+        const int u = ubase + 64 * i;
+        if (FULL || u < U) accumulate_dig<F>(buf[rr][i], u, [&](int t) { return pr[i][t]; }, a);
+      }
+      a = wave_sum_dpp(a);
+      if (ks == 1 && lane == 0) y[r_begin + rr] = a;
+    }
+    acc[rr] = a;
+  }
+  if (ks > 1) {
+    if (lane == 0) {
+#pragma unroll
+      for (int rr = 0; rr < RMAX; rr++) red[rr * ks + kw] = acc[rr];
+    }
+    __syncthreads();
+    if (wave == 0 && lane < n_rows) {
+      float s = 0.f;
+      for (int k = 0; k < ks; k++) s += red[lane * ks + k];
+      y[r_begin + lane] = s;
+    }
+  }
+}
+
+// ------------------------------------------------------ batched (B > 1) path
+// x' for all B activations lives in LDS; each lane reads its unit's x' per use
+// and applies one decoded unit to R rows x B activations.
+template <int F, int B, int R>
+__global__ __launch_bounds__(256) void mv_lds(const uint8_t* __restrict__ w,
+                                              const float* __restrict__ x, float* __restrict__ y,
+                                              int out_dim, int in_dim, int bpr, int rows_per_wg) {
   using FU = FastUnit<F>;
   constexpr int E = FU::E, NS = FU::NSUM, SG = FU::SUMG, ES = E + 4, NW = FU::NW;
   extern __shared__ float smem[];
   const int keff = bpr * Geom<F>::bs;
   const int U = keff / E;
-  float* xs = smem;                      // [B][U][ES]
-  float* xsum = smem + (size_t)B * U * ES;  // [B][U*NS]
-
-  for (int i = threadIdx.x; i < B * keff; i += blockDim.x) {
-    const int b = i / keff, e = i - b * keff;
-    float v = x[(size_t)b * in_dim + e];
-    const int u = e / E, t = e - u * E;
-    if (FU::prescale && (t & 1)) v *= 0.0625f;
-    xs[((size_t)b * U + u) * ES + t] = v;
-  }
+  float* xs = smem;                          // [B][U][ES]
+  float* xsum = smem + (size_t)B * U * ES;   // [B][U*NS]
+  stage_x<F, B>(x, in_dim, keff, U, xs);
   for (int i = threadIdx.x; i < B * U * NS; i += blockDim.x) {
     const int b = i / (U * NS), g = i - b * (U * NS);
     const float* xp = x + (size_t)b * in_dim + (size_t)g * SG;
     float s = 0.f;
-    for (int t = 0; t < SG; t++) s += xp[t];
+    for (int t = 0; t < SG; t += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(xp + t);
+      s += (v.x + v.y) + (v.z + v.w);
+    }
     xsum[i] = s;
   }
   __syncthreads();
@@ -253,82 +592,34 @@ __global__ __launch_bounds__(256) void mv_fast(const uint8_t* __restrict__ w,
   const size_t row_bytes = (size_t)bpr * Geom<F>::bb;
   const int r_begin = blockIdx.x * rows_per_wg;
   const int r_end = min(out_dim, r_begin + rows_per_wg);
-
-  if constexpr (UPL > 0) {
-    static_assert(B == 1, "register-resident x needs B == 1");
-    float xr[UPL][E];
-    float sr[UPL][NS];
+  for (int r0 = r_begin + wave * R; r0 < r_end; r0 += nwaves * R) {
+    float acc[R][B];
 #pragma unroll
-    for (int i = 0; i < UPL; i++) {
-      const int u = lane + 64 * i;
-      const bool ok = u < U;
+    for (int rr = 0; rr < R; rr++)
 #pragma unroll
-      for (int t = 0; t < E; t++) xr[i][t] = ok ? xs[(size_t)u * ES + t] : 0.f;
-#pragma unroll
-      for (int g = 0; g < NS; g++) sr[i][g] = ok ? xsum[(size_t)u * NS + g] : 0.f;
-    }
-    for (int r0 = r_begin + wave * R; r0 < r_end; r0 += nwaves * R) {
-      uint32_t raw[R][UPL][NW];
+      for (int b = 0; b < B; b++) acc[rr][b] = 0.f;
+    for (int u = lane; u < U; u += 64) {
+      uint32_t raw[R][NW];
 #pragma unroll
       for (int rr = 0; rr < R; rr++) {
         const int row = min(r0 + rr, r_end - 1);
-        const uint8_t* rp = w + (size_t)row * row_bytes;
-#pragma unroll
-        for (int i = 0; i < UPL; i++) {
-          const int u = lane + 64 * i;
-          if (u < U) load_unit<F>(rp, u, raw[rr][i]);
-        }
+        load_unit<F>(w + (size_t)row * row_bytes, u, raw[rr]);
       }
-      float acc[R];
-#pragma unroll
-      for (int rr = 0; rr < R; rr++) {
-        acc[rr] = 0.f;
-#pragma unroll
-        for (int i = 0; i < UPL; i++) {
-          const int u = lane + 64 * i;
-          if (u < U)
-            accumulate<F, 1>(
-                raw[rr][i], u, [&](int, int e) { return xr[i][e]; },
-                [&](int, int g) { return sr[i][g]; }, &acc[rr]);
-        }
-      }
-#pragma unroll
-      for (int rr = 0; rr < R; rr++) {
-        const float s = wave_sum(acc[rr]);
-        if (lane == 0 && r0 + rr < r_end) y[r0 + rr] = s;
-      }
-    }
-  } else {
-    for (int r0 = r_begin + wave * R; r0 < r_end; r0 += nwaves * R) {
-      float acc[R][B];
+      const float* xu = xs + (size_t)u * ES;
+      const float* su = xsum + (size_t)u * NS;
 #pragma unroll
       for (int rr = 0; rr < R; rr++)
-#pragma unroll
-        for (int b = 0; b < B; b++) acc[rr][b] = 0.f;
-      for (int u = lane; u < U; u += 64) {
-        uint32_t raw[R][NW];
-#pragma unroll
-        for (int rr = 0; rr < R; rr++) {
-          const int row = min(r0 + rr, r_end - 1);
-          load_unit<F>(w + (size_t)row * row_bytes, u, raw[rr]);
-        }
-        const float* xu = xs + (size_t)u * ES;
-        const float* su = xsum + (size_t)u * NS;
-#pragma unroll
-        for (int rr = 0; rr < R; rr++)
-          accumulate<F, B>(
-              raw[rr], u,
-              [&](int b, int e) { return xu[(size_t)b * U * ES + e]; },
-              [&](int b, int g) { return su[(size_t)b * U * NS + g]; }, acc[rr]);
-      }
-#pragma unroll
-      for (int rr = 0; rr < R; rr++)
-#pragma unroll
-        for (int b = 0; b < B; b++) {
-          const float s = wave_sum(acc[rr][b]);
-          if (lane == 0 && r0 + rr < r_end) y[(size_t)b * out_dim + r0 + rr] = s;
-        }
+        accumulate<F, B>(
+            raw[rr], u, [&](int b, int e) { return xu[(size_t)b * U * ES + e]; },
+            [&](int b, int g) { return su[(size_t)b * U * NS + g]; }, acc[rr]);
     }
+#pragma unroll
+    for (int rr = 0; rr < R; rr++)
+#pragma unroll
+      for (int b = 0; b < B; b++) {
+        const float s = wave_sum_dpp(acc[rr][b]);
+        if (lane == 0 && r0 + rr < r_end) y[(size_t)b * out_dim + r0 + rr] = s;
+      }
   }
 }
 
@@ -476,52 +767,132 @@ hipError_t generic_dispatch(const uint8_t* w, const float* x, float* y, int out_
   return hipSuccess;
 }
 
-template <int F, int B, int R, int UPL>
-hipError_t run_fast(const uint8_t* w, const float* x, float* y, int out_dim, int in_dim, int bpr,
-                    size_t lds_bytes, hipStream_t s) {
-  auto kern = mv_fast<F, B, R, UPL>;
-  static bool attr_set = false;
-  if (!attr_set && lds_bytes > 65536) {
-    hipError_t e = hipFuncSetAttribute((const void*)kern,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       lds_limit());
-    if (e != hipSuccess) return e;
-    attr_set = true;
+template <class K>
+hipError_t set_lds_attr(K kern, size_t lds_bytes) {
+  if (lds_bytes <= 65536) return hipSuccess;
+  return hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                             lds_limit());
+}
+
+// Splits out_dim into contiguous row ranges, a multiple of `quantum` rows each,
+// for about `target` workgroups.
+void row_split(int out_dim, int quantum, int target, int* n_wg, int* rows_per_wg) {
+  int n = std::max(1, std::min((out_dim + quantum - 1) / quantum, target));
+  int r = (out_dim + n - 1) / n;
+  r = (r + quantum - 1) / quantum * quantum;
+  *rows_per_wg = r;
+  *n_wg = (out_dim + r - 1) / r;
+}
+
+template <int F, int UPL, int RMAX, bool FULL, int SIT>
+hipError_t run_b1_sit(const uint8_t* w, const float* x, float* y, int out_dim, int bpr, int ks,
+                      int rs, size_t lds, hipStream_t s) {
+  auto kern = mv_b1<F, UPL, RMAX, FULL, SIT>;
+  hipError_t e = set_lds_attr(kern, lds);
+  if (e != hipSuccess) return e;
+  const int threads = 64 * ks * rs;
+  const long streams_needed = (out_dim + RMAX - 1) / RMAX;
+  long n_wg = std::max<long>(device_cu_count(), (streams_needed + rs - 1) / rs);
+  n_wg = std::max<long>(1, std::min<long>(n_wg, (out_dim + rs - 1) / rs));
+  hipLaunchKernelGGL(kern, dim3((unsigned)n_wg), dim3(threads), lds, s, w, x, y, out_dim, bpr, ks);
+  return hipGetLastError();
+}
+
+template <int F, int UPL, int RMAX, bool FULL>
+hipError_t run_b1(const uint8_t* w, const float* x, float* y, int out_dim, int bpr, int ks,
+                  hipStream_t s) {
+  const int U = bpr * Geom<F>::bs / FastUnit<F>::E;
+  const size_t lds = ((size_t)U * Dig<F>::US + (size_t)RMAX * ks) * sizeof(uint32_t);
+  if (lds > (size_t)lds_limit()) return hipErrorInvalidValue;
+  // One workgroup per CU holding as many waves as fit (ks waves per row
+  // stream); the occupancy is the same for every staging depth.
+  auto probe = mv_b1<F, UPL, RMAX, FULL, kStageIt>;
+  hipError_t e = set_lds_attr(probe, lds);
+  if (e != hipSuccess) return e;
+  int rs = 1;
+  for (int cand = 768 / (64 * ks); cand >= 1; cand--) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, probe, 64 * ks * cand, lds) == hipSuccess &&
+        per_cu >= 1) {
+      rs = cand;
+      break;
+    }
   }
-  const int cus = device_cu_count();
-  const int waves_per_wg = 4;
-  // Enough workgroups to fill every CU twice; each takes a contiguous row range.
-  const int rows_per_pass = waves_per_wg * R;
-  int n_wg = std::max(1, std::min((out_dim + rows_per_pass - 1) / rows_per_pass, 2 * cus));
-  int rows_per_wg = (out_dim + n_wg - 1) / n_wg;
-  rows_per_wg = (rows_per_wg + rows_per_pass - 1) / rows_per_pass * rows_per_pass;
-  n_wg = (out_dim + rows_per_wg - 1) / rows_per_wg;
-  hipLaunchKernelGGL(kern, dim3(n_wg), dim3(64 * waves_per_wg), lds_bytes, s, w, x, y, out_dim,
-                     in_dim, bpr, rows_per_wg);
+  const int threads = 64 * ks * rs;
+  const int nchunk = bpr * Geom<F>::bs / 8;
+  const int sit = (nchunk + threads - 1) / threads;
+  switch (sit) {
+    case 0:
+    case 1: return run_b1_sit<F, UPL, RMAX, FULL, 1>(w, x, y, out_dim, bpr, ks, rs, lds, s);
+    case 2: return run_b1_sit<F, UPL, RMAX, FULL, 2>(w, x, y, out_dim, bpr, ks, rs, lds, s);
+    case 3:
+    case 4: return run_b1_sit<F, UPL, RMAX, FULL, 4>(w, x, y, out_dim, bpr, ks, rs, lds, s);
+    default: return hipErrorNotSupported;  // x too long to stage
+  }
+}
+
+template <int F, int B, int R>
+hipError_t run_lds(const uint8_t* w, const float* x, float* y, int out_dim, int in_dim, int bpr,
+                   size_t lds, hipStream_t s) {
+  auto kern = mv_lds<F, B, R>;
+  hipError_t e = set_lds_attr(kern, lds);
+  if (e != hipSuccess) return e;
+  int n_wg, rows;
+  row_split(out_dim, 4 * R, 2 * device_cu_count(), &n_wg, &rows);
+  hipLaunchKernelGGL(kern, dim3(n_wg), dim3(256), lds, s, w, x, y, out_dim, in_dim, bpr, rows);
   return hipGetLastError();
 }
 
 template <int F>
-bool fast_aligned(const uint8_t* w, int bpr) {
+bool fast_aligned(const uint8_t* w, const float* x, int in_dim, int bpr) {
   const uintptr_t a = (uintptr_t)w;
+  if ((((uintptr_t)x) & 15) || (in_dim & 3)) return false;  // float4 staging of x
   if constexpr (F == kQ4_K) return (a & 15u) == 0;
   else return (a & 3u) == 0 && (bpr % 2) == 0;  // Q4_0 / Q8_0 pairs, Q6_K dword rows
+}
+
+template <int F>
+hipError_t b1_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, int bpr,
+                       hipStream_t s, bool* used) {
+  const int U = bpr * Geom<F>::bs / FastUnit<F>::E;
+  if (U == 0) return hipSuccess;
+  int ks, upl;
+  if (U <= 128) {
+    ks = 1;
+    upl = U <= 64 ? 1 : 2;
+  } else if (U <= 512) {
+    ks = (U + 63) / 64;
+    upl = 1;
+  } else {
+    return hipSuccess;  // long rows: batched LDS kernel
+  }
+  const bool full = (U == ks * upl * 64);
+  *used = true;
+  hipError_t e;
+  if (upl == 1)
+    e = full ? run_b1<F, 1, 5, true>(w, x, y, out_dim, bpr, ks, s)
+             : run_b1<F, 1, 5, false>(w, x, y, out_dim, bpr, ks, s);
+  else
+    e = full ? run_b1<F, 2, 3, true>(w, x, y, out_dim, bpr, ks, s)
+             : run_b1<F, 2, 3, false>(w, x, y, out_dim, bpr, ks, s);
+  if (e == hipErrorNotSupported) {  // not launched: the caller takes the batched path
+    *used = false;
+    return hipSuccess;
+  }
+  return e;
 }
 
 template <int F>
 hipError_t fast_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, int in_dim,
                          int bpr, int batch, hipStream_t s, bool* used) {
   *used = false;
-  if (!fast_aligned<F>(w, bpr)) return hipSuccess;
+  if (!fast_aligned<F>(w, x, in_dim, bpr)) return hipSuccess;
   const int keff = bpr * Geom<F>::bs;
   const int U = keff / FastUnit<F>::E;
   const int limit = lds_limit();
-  if (batch == 1 && U <= 128) {
-    const size_t lds = lds_floats<F>(U, 1) * 4;
-    if (lds > (size_t)limit) return hipSuccess;
-    *used = true;
-    if (U <= 64) return run_fast<F, 1, 4, 1>(w, x, y, out_dim, in_dim, bpr, lds, s);
-    return run_fast<F, 1, 4, 2>(w, x, y, out_dim, in_dim, bpr, lds, s);
+  if (batch == 1) {
+    hipError_t e = b1_dispatch<F>(w, x, y, out_dim, bpr, s, used);
+    if (e != hipSuccess || *used) return e;
   }
   // LDS-resident x; batch processed in chunks of 8/4/2/1 that each fit LDS
   int b0 = 0;
@@ -535,10 +906,10 @@ hipError_t fast_dispatch(const uint8_t* w, const float* x, float* y, int out_dim
     float* yb = y + (size_t)b0 * out_dim;
     hipError_t e;
     switch (take) {
-      case 8: e = run_fast<F, 8, 2, 0>(w, xb, yb, out_dim, in_dim, bpr, lds, s); break;
-      case 4: e = run_fast<F, 4, 2, 0>(w, xb, yb, out_dim, in_dim, bpr, lds, s); break;
-      case 2: e = run_fast<F, 2, 2, 0>(w, xb, yb, out_dim, in_dim, bpr, lds, s); break;
-      default: e = run_fast<F, 1, 4, 0>(w, xb, yb, out_dim, in_dim, bpr, lds, s); break;
+      case 8: e = run_lds<F, 8, 2>(w, xb, yb, out_dim, in_dim, bpr, lds, s); break;
+      case 4: e = run_lds<F, 4, 2>(w, xb, yb, out_dim, in_dim, bpr, lds, s); break;
+      case 2: e = run_lds<F, 2, 2>(w, xb, yb, out_dim, in_dim, bpr, lds, s); break;
+      default: e = run_lds<F, 1, 4>(w, xb, yb, out_dim, in_dim, bpr, lds, s); break;
     }
     if (e != hipSuccess) return e;
     *used = true;

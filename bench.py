@@ -33,7 +33,11 @@ def parse():
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--no-extras", action="store_true", help="only the headline workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--graph", action="store_true", help="replay steps from a captured HIP graph")
+    ap.add_argument("--profile-pass", action="store_true",
+                    help="short run for hardware-counter passes: a Q8_0 dequant of known size (the "
+                         "counter calibration), then 20 headline matvec launches; prints no JSON")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch every matvec step from Python instead of replaying captured HIP graphs")
     return ap.parse_args()
 
 
@@ -42,26 +46,52 @@ def copies_for(nbytes):
 
 
 class Timer:
-    """Events on the stream the kernels are launched on (torch's current stream)."""
+    """Events on the stream the kernels are launched on (torch's current stream).
 
-    def __init__(self, torch):
+    Short kernels (the matvecs take ~10 us) are replayed from HIP graphs of
+    GRAPH_CHUNK captured launches, so the host's per-launch cost (ctypes
+    marshalling, ~15 us) does not set the step time."""
+
+    GRAPH_CHUNK = 50
+
+    def __init__(self, torch, graph=True):
         self.torch = torch
+        self.graph = graph
         self.e0 = torch.cuda.Event(enable_timing=True)
         self.e1 = torch.cuda.Event(enable_timing=True)
 
-    def run(self, fn, steps, warmup):
+    def _timed(self, fn, reps, warmup):
         torch = self.torch
         for i in range(warmup):
             fn(i)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         self.e0.record()
-        for i in range(steps):
+        for i in range(reps):
             fn(i)
         self.e1.record()
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
         return self.e0.elapsed_time(self.e1) * 1e-3, wall  # seconds (events), seconds (host)
+
+    def run(self, fn, steps, warmup, graph=None):
+        """Returns (seconds for `steps` steps by events, host wall seconds, steps run)."""
+        torch = self.torch
+        if not (self.graph if graph is None else graph):
+            t, wall = self._timed(fn, steps, warmup)
+            return t, wall, steps
+        chunk = min(self.GRAPH_CHUNK, steps)
+        for i in range(2):
+            fn(i)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(chunk):
+                fn(i)
+        reps = max(1, steps // chunk)
+        t, wall = self._timed(lambda i: g.replay(), reps, max(1, warmup // chunk))
+        del g
+        return t, wall, reps * chunk
 
 
 def matvec_case(torch, ssdq, synth, dtype, out_dim, in_dim, batch, seed_cfg):
@@ -93,25 +123,14 @@ def main():
     from ssdq import synth
 
     torch.cuda.set_device(0)
-    timer = Timer(torch)
+    if args.profile_pass:
+        profile_pass(torch, ssdq, synth)
+        return
+    timer = Timer(torch, graph=not args.eager)
 
     # ---------------------------------------------------------- headline
     step, algo_bytes, _ = matvec_case(torch, ssdq, synth, ssdq.Q4_K, 14336, 4096, 1, 3)
-    if args.graph:
-        chunk = 50
-        g = torch.cuda.CUDAGraph()
-        for i in range(3):
-            step(i)
-        torch.cuda.synchronize()
-        with torch.cuda.graph(g):
-            for i in range(chunk):
-                step(i)
-        reps = max(1, args.steps // chunk)
-        t_ev, wall = timer.run(lambda i: g.replay(), reps, max(1, args.warmup // chunk))
-        steps = reps * chunk
-    else:
-        steps = args.steps
-        t_ev, wall = timer.run(step, steps, args.warmup)
+    t_ev, wall, steps = timer.run(step, args.steps, args.warmup)
     sec_per_step = t_ev / steps
     value = algo_bytes / sec_per_step / 1e9
 
@@ -126,19 +145,20 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_k weights, f32 activations and accumulation",
+        "dtype": "f32",
         "data": "synthetic (seeded GGUF Q4_K blocks per config 3, x ~ N(0,1)); weights HBM-resident, "
                 "rotated over copies larger than 2x the last-level cache",
         "config": {"workload": "Q4_K matvec 14336x4096 batch 1 (Llama-3-8B FFN up, config 3)",
                    "out_dim": 14336, "in_dim": 4096, "batch": 1,
                    "weight_copies": copies_for(14336 * ssdq.row_bytes(ssdq.Q4_K, 4096)),
-                   "graph": bool(args.graph)},
+                   "weights": "GGUF Q4_K", "activations": "f32", "accumulate": "f32",
+                   "launch": "eager" if args.eager else f"hip graph of {Timer.GRAPH_CHUNK} launches"},
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "roofline": {
             "bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(value / HBM_PEAK_GBS, 4),
             "traffic": traffic_from_profiles("q4k_matvec_14336x4096"),
-            "kernel": "mv_fast<Q4_K,B=1>", "algo_bytes_per_launch": algo_bytes,
+            "kernel": "mv_b1<Q4_K>", "algo_bytes_per_launch": algo_bytes,
         },
         "host_wall_s": round(wall, 4),
     }
@@ -148,6 +168,32 @@ def main():
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(np, synth, ssdq, sec_per_step)
     print(json.dumps(result))
+
+
+CAL_ELEMS = 1 << 26  # Q8_0 dequant calibration: 71,303,168 B read, 268,435,456 B written
+
+
+def profile_pass(torch, ssdq, synth):
+    """Launch sequence profiled with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE.
+
+    Dispatches, in order: 3 x dequant_kernel (Q8_0, CAL_ELEMS elements: a plain
+    streaming kernel whose bytes are known exactly, used to scale the counters
+    to bytes), then 20 x the headline Q4_K 14336x4096 matvec over rotating
+    weight copies."""
+    nb = CAL_ELEMS // 32
+    raw = torch.randint(0, 256, (nb * 34,), dtype=torch.uint8, device="cuda")
+    raw.view(nb, 34)[:, 0:2] = torch.tensor([0x00, 0x3C], dtype=torch.uint8, device="cuda")  # d = 1.0
+    out = torch.empty(CAL_ELEMS, device="cuda")
+    step, algo_bytes, _ = matvec_case(torch, ssdq, synth, ssdq.Q4_K, 14336, 4096, 1, 3)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        ssdq.dequant(ssdq.Q8_0, raw, CAL_ELEMS, out)
+    torch.cuda.synchronize()
+    for i in range(20):
+        step(i)
+    torch.cuda.synchronize()
+    print(f"profile pass done: calibration read {nb * 34} B write {CAL_ELEMS * 4} B; "
+          f"headline algorithmic bytes {algo_bytes}", flush=True)
 
 
 def traffic_from_profiles(key):
@@ -176,11 +222,27 @@ def extras(torch, ssdq, synth, timer, np):
     ]
     for name, dt, od, idim, b, cfg in cases:
         step, nbytes, _ = matvec_case(torch, ssdq, synth, dt, od, idim, b, cfg)
-        t, _ = timer.run(step, 200, 20)
-        gbs = nbytes / (t / 200) / 1e9
+        t, _, n = timer.run(step, 200, 20)
+        gbs = nbytes / (t / n) / 1e9
         out[name] = {"GB/s": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
-                     "us": round(t / 200 * 1e6, 3)}
+                     "us": round(t / n * 1e6, 3)}
         torch.cuda.empty_cache()
+
+    # the synchronous host-pointer twin (MetalCompute::matvec_quantized contract):
+    # W and x cross PCIe on every call, so this is the PCIe-inclusive rate
+    w_host = synth.quant_weights(ssdq.Q4_K, 14336, 4096, synth.seed(3, 0))
+    x_host = synth.normal_f32(4096, 1)
+    with ssdq.Context() as ctx:
+        ctx.matvec_quantized(w_host, x_host, 14336, 4096, ssdq.Q4_K)
+        reps, t0 = 0, time.perf_counter()
+        while reps < 20:
+            ctx.matvec_quantized(w_host, x_host, 14336, 4096, ssdq.Q4_K)
+            reps += 1
+        el = (time.perf_counter() - t0) / reps
+    hb = w_host.size + 4 * (4096 + 14336)
+    out["host_twin_q4k_matvec_14336x4096_pcie_inclusive"] = {
+        "GB/s": round(hb / el / 1e9, 2), "us": round(el * 1e6, 1),
+        "note": "ssdq_matvec_quantized: host W and x copied in, y copied out, per call"}
 
     # config 4: one Llama-3-8B layer of Q4_K prefill GEMMs at M = 512
     layer = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
@@ -199,7 +261,7 @@ def extras(torch, ssdq, synth, timer, np):
         for w, x, y, N, K in mats:
             ssdq.gemm_q4k_bf16(w, x, y, M, N, K)
 
-    t, _ = timer.run(layer_step, 5, 1)
+    t, _, _ = timer.run(layer_step, 5, 1, graph=False)
     tfl = flops / (t / 5) / 1e12
     out["prefill_gemm_q4k_layer_m512"] = {"TFLOP/s": round(tfl, 2),
                                           "pct_bf16_peak": round(100 * tfl / BF16_PEAK_TFLOPS, 2),
@@ -212,7 +274,7 @@ def extras(torch, ssdq, synth, timer, np):
     xk = torch.randn(n_rows * dim, device="cuda")
     codes = torch.empty(n_rows * dim, dtype=torch.int8, device="cuda")
     scales = torch.empty(n_rows, device="cuda")
-    t, _ = timer.run(lambda i: ssdq.kv_quantize_rows(xk, codes, scales, n_rows, dim), 20, 3)
+    t, _, _ = timer.run(lambda i: ssdq.kv_quantize_rows(xk, codes, scales, n_rows, dim), 20, 3, graph=False)
     qbytes = n_rows * dim * 5 + n_rows * 4
     out["kv_int8_quantize_8x32768x2x1024"] = {"GB/s": round(qbytes / (t / 20) / 1e9, 1),
                                               "pct_hbm_peak": round(100 * qbytes / (t / 20) / 1e9 / HBM_PEAK_GBS, 2),
@@ -229,8 +291,9 @@ def extras(torch, ssdq, synth, timer, np):
     cl = torch.full((n_seq,), ctx, dtype=torch.int32, device="cuda")
     q = torch.randn(n_seq * n_head * hd, device="cuda")
     o = torch.empty_like(q)
-    t, _ = timer.run(lambda i: ssdq.paged_attention_int8(q, kc, ks, vc, vs, tables, cl, o, n_seq,
-                                                         n_head, n_kv, hd, bs, mb, ctx), 50, 5)
+    t, _, _ = timer.run(lambda i: ssdq.paged_attention_int8(q, kc, ks, vc, vs, tables, cl, o, n_seq,
+                                                            n_head, n_kv, hd, bs, mb, ctx), 50, 5,
+                        graph=False)
     abytes = 536870912 + 2097152 + 131072 + 131072 + 65536
     step_s = t / 50
     out["paged_int8_decode_attention_32k"] = {
@@ -255,7 +318,7 @@ def cpu_baseline(np, synth, ssdq, gpu_sec_per_step):
         o.matvec(ssdq.Q4_K, w, x, out_dim, in_dim)
         reps += 1
         el = time.perf_counter() - t0
-        if el > 10.0 or reps >= 200:
+        if el > 10.0:
             break
     st = el / reps
     res = {"value": round(nbytes / st / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",

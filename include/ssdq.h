@@ -21,7 +21,8 @@
  *   - "host" functions take host pointers, copy in, compute, copy out and
  *     return when the result is in place: the synchronous, allocate-per-call
  *     contract of MetalCompute (gpu.rs:492-535), on a context that is created
- *     once (not per forward pass, unlike transformer.rs:301-302).
+ *     once (not per forward pass, unlike transformer.rs:301-302). Calls on one
+ *     context are serialized by the context; contexts are independent.
  *   - dtype uses the GgmlType numeric ids of src/model/gguf.rs:17-48.
  *   - Sizes are element counts unless named *_bytes.
  */
@@ -83,10 +84,19 @@ int ssdq_ctx_device(const ssdq_ctx* ctx);
  * to the reference: dequantize_q4_0 / q8_0 / q6_k (src/ssd/streamer.rs:128-220)
  * and the Q4_K values of matvec_q4_k_cpu (compute.rs:716-744; the reference's
  * loader has no Q4_K path and returns zeros, streamer.rs:119-123). Elements past
- * the last whole block are zero (streamer.rs `output.resize`). Replaces
- * dequantize_to_f32 (streamer.rs:93-125) for quantized types. */
+ * the last whole block are zero (streamer.rs `output.resize`). F32 / F16 /
+ * BF16 tensors are copied / widened (streamer.rs:95-115; w element-aligned).
+ * Replaces dequantize_to_f32 (streamer.rs:93-125) on the device. */
 int ssdq_dequant_dev(int dtype, const void* w, size_t n_elements, float* out,
                      ssdq_stream_t stream);
+/* Host twin of dequantize_to_f32 (streamer.rs:93-125): data_len bytes in,
+ * n_elements floats out. Quantized types decode the whole blocks present in
+ * data_len and zero the rest (the dequantizers' early `break` + `resize`);
+ * float types need n_elements values; unsupported dtypes give zeros and
+ * SSDQ_WARN_UNSUPPORTED_ZEROED (streamer.rs:117-123). Q4_K, zeros in the
+ * reference's loader, is decoded. Synchronous. */
+int ssdq_dequantize_to_f32(ssdq_ctx* ctx, int dtype, const uint8_t* data, size_t data_len,
+                           size_t n_elements, float* out);
 
 /* ---------------------------------------------------------------- matvec */
 /* y[b, r] = sum_k dequant(W)[r, k] * x[b, k] for b < batch, r < out_dim, over
@@ -125,6 +135,13 @@ int ssdq_kv_quantize_rows_dev(const float* in, int8_t* codes, float* scales, siz
  * QuantizedVec::dequantize (quantized_kv_cache.rs:44-53). */
 int ssdq_kv_dequantize_rows_dev(const int8_t* codes, const float* scales, float* out,
                                 size_t n_rows, size_t row_len, ssdq_stream_t stream);
+/* Host twins (synchronous, copy in/out): quantize_vectors_int8 /
+ * dequantize_vectors_int8 (src/ssd/block_swap.rs:36-74) over n_rows rows of
+ * dim elements. */
+int ssdq_quantize_vectors_int8(ssdq_ctx* ctx, const float* data, size_t n_rows, size_t dim,
+                               int8_t* codes, float* scales);
+int ssdq_dequantize_vectors_int8(ssdq_ctx* ctx, const int8_t* codes, const float* scales,
+                                 size_t n_rows, size_t dim, float* out);
 /* Quantize-on-append into the paged INT8 pool: token t's K and V rows
  * (kv_dim floats each) are quantized like ssdq_kv_quantize_rows_dev and stored
  * at pool row slot_mapping[t] (= physical_block * block_size + slot, see

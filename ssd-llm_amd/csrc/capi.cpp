@@ -41,6 +41,10 @@ bool supported_quant(int dtype) {
          dtype == SSDQ_TYPE_Q6_K;
 }
 
+bool float_type(int dtype) {
+  return dtype == SSDQ_TYPE_F32 || dtype == SSDQ_TYPE_F16 || dtype == SSDQ_TYPE_BF16;
+}
+
 bool fits_int(size_t v) { return v <= (size_t)INT_MAX; }
 
 // Grow-only device buffers keyed by (device, stream), so calls on different
@@ -96,6 +100,7 @@ int device_cu_count() {
 }  // namespace ssdq
 
 struct ssdq_ctx {
+  std::mutex mu;  // host twins on one context run one at a time
   int device = 0;
   hipStream_t stream = nullptr;
   void* buf[4] = {nullptr, nullptr, nullptr, nullptr};
@@ -192,6 +197,14 @@ int ssdq_dequant_dev(int dtype, const void* w, size_t n_elements, float* out,
   if (n_elements == 0) return ok();
   if (!out) return fail(SSDQ_ERR_INVALID_ARG, "ssdq_dequant_dev: out is NULL");
   hipStream_t s = (hipStream_t)stream;
+  if (float_type(dtype)) {
+    if (!w) return fail(SSDQ_ERR_INVALID_ARG, "ssdq_dequant_dev: w is NULL");
+    if ((uintptr_t)w % ssdq_type_size(dtype) || ((uintptr_t)out & 3))
+      return fail(SSDQ_ERR_INVALID_ARG, "ssdq_dequant_dev: w / out not element aligned");
+    hipError_t e = ssdq::launch_widen(dtype, w, n_elements, out, s);
+    if (e != hipSuccess) return hip_fail(e, "ssdq_dequant_dev: widen");
+    return ok();
+  }
   if (!supported_quant(dtype)) {
     hipError_t e = ssdq::launch_fill_zero(out, n_elements, s);
     if (e != hipSuccess) return hip_fail(e, "ssdq_dequant_dev: fill");
@@ -267,6 +280,7 @@ int ssdq_matvec_quantized(ssdq_ctx* c, const uint8_t* w_raw, size_t w_len, const
   if (x_len < keff)
     return fail(SSDQ_ERR_INVALID_ARG, "ssdq_matvec_quantized: x has %zu floats, need %zu", x_len, keff);
   if ((rb && !w_raw) || (keff && !x)) return fail(SSDQ_ERR_INVALID_ARG, "ssdq_matvec_quantized: NULL input");
+  std::lock_guard<std::mutex> lk(c->mu);
   hipError_t e = hipSetDevice(c->device);
   if (e != hipSuccess) return hip_fail(e, "ssdq_matvec_quantized: hipSetDevice");
   void *dw, *dx, *dy;
@@ -408,6 +422,7 @@ int ssdq_flash_attention_f32(ssdq_ctx* c, const float* q, const float* k, const 
   if (!c) return fail(SSDQ_ERR_INVALID_ARG, "ssdq_flash_attention_f32: ctx is NULL");
   if (n_head == 0) return ok();
   if (!q || !out || (seq_len && (!k || !v))) return fail(SSDQ_ERR_INVALID_ARG, "ssdq_flash_attention_f32: NULL pointer");
+  std::lock_guard<std::mutex> lk(c->mu);
   hipError_t e = hipSetDevice(c->device);
   if (e != hipSuccess) return hip_fail(e, "ssdq_flash_attention_f32: hipSetDevice");
   const size_t qn = n_head * head_dim, kvn = seq_len * n_head_kv * head_dim;
@@ -427,6 +442,113 @@ int ssdq_flash_attention_f32(ssdq_ctx* c, const float* q, const float* k, const 
     return hip_fail(e, "ssdq_flash_attention_f32: copy out");
   if ((e = hipStreamSynchronize(c->stream)) != hipSuccess)
     return hip_fail(e, "ssdq_flash_attention_f32: sync");
+  return ok();
+}
+
+// ------------------------------------------------------------ host twins
+// dequantize_to_f32 (src/ssd/streamer.rs:93-125): F32 / F16 / BF16 widen,
+// Q4_0 / Q8_0 / Q6_K per the load-time dequantizers and Q4_K per the matvec
+// element values; only whole blocks present in data_len are decoded, the rest
+// of the n_elements outputs is zero (the dequantizers' `break` + `resize`).
+int ssdq_dequantize_to_f32(ssdq_ctx* c, int dtype, const uint8_t* data, size_t data_len,
+                           size_t n_elements, float* out) {
+  if (!c) return fail(SSDQ_ERR_INVALID_ARG, "ssdq_dequantize_to_f32: ctx is NULL");
+  if (n_elements == 0) return ok();
+  if (!out) return fail(SSDQ_ERR_INVALID_ARG, "ssdq_dequantize_to_f32: out is NULL");
+  if (!float_type(dtype) && !supported_quant(dtype)) {
+    memset(out, 0, n_elements * sizeof(float));
+    fail(SSDQ_WARN_UNSUPPORTED_ZEROED, "ssdq_dequantize_to_f32: dtype %d unsupported, zeros", dtype);
+    return SSDQ_WARN_UNSUPPORTED_ZEROED;
+  }
+  const size_t bs = ssdq_block_size(dtype), tsz = ssdq_type_size(dtype);
+  size_t units = n_elements / bs;  // whole blocks (elements for float types)
+  if (float_type(dtype)) {
+    // the reference reads n_elements values unconditionally and would read
+    // past a short slice; that is an error here
+    if (data_len < n_elements * tsz)
+      return fail(SSDQ_ERR_INVALID_ARG, "ssdq_dequantize_to_f32: data has %zu bytes, need %zu",
+                  data_len, n_elements * tsz);
+  } else if (units > data_len / tsz) {
+    units = data_len / tsz;
+  }
+  const size_t in_bytes = units * tsz, decoded = units * bs;
+  if (in_bytes && !data) return fail(SSDQ_ERR_INVALID_ARG, "ssdq_dequantize_to_f32: data is NULL");
+  std::lock_guard<std::mutex> lk(c->mu);
+  hipError_t e = hipSetDevice(c->device);
+  if (e != hipSuccess) return hip_fail(e, "ssdq_dequantize_to_f32: hipSetDevice");
+  void *dw, *dy;
+  if ((e = ctx_buf(c, 0, in_bytes, &dw)) != hipSuccess ||
+      (e = ctx_buf(c, 2, n_elements * sizeof(float), &dy)) != hipSuccess)
+    return hip_fail(e, "ssdq_dequantize_to_f32: staging allocation");
+  if (in_bytes && (e = hipMemcpyAsync(dw, data, in_bytes, hipMemcpyHostToDevice, c->stream)) != hipSuccess)
+    return hip_fail(e, "ssdq_dequantize_to_f32: copy in");
+  int rc = ssdq_dequant_dev(dtype, dw, decoded, (float*)dy, c->stream);
+  if (rc < 0) return rc;
+  if ((e = hipMemcpyAsync(out, dy, decoded * sizeof(float), hipMemcpyDeviceToHost, c->stream)) != hipSuccess)
+    return hip_fail(e, "ssdq_dequantize_to_f32: copy out");
+  if ((e = hipStreamSynchronize(c->stream)) != hipSuccess)
+    return hip_fail(e, "ssdq_dequantize_to_f32: sync");
+  if (decoded < n_elements) memset(out + decoded, 0, (n_elements - decoded) * sizeof(float));
+  return ok();
+}
+
+// quantize_vectors_int8 (src/ssd/block_swap.rs:36-60): n_rows = data_len / dim
+// whole rows; codes [n_rows * dim], scales [n_rows].
+int ssdq_quantize_vectors_int8(ssdq_ctx* c, const float* data, size_t n_rows, size_t dim,
+                               int8_t* codes, float* scales) {
+  if (!c) return fail(SSDQ_ERR_INVALID_ARG, "ssdq_quantize_vectors_int8: ctx is NULL");
+  if (n_rows == 0) return ok();
+  if (!scales || (dim && (!data || !codes)))
+    return fail(SSDQ_ERR_INVALID_ARG, "ssdq_quantize_vectors_int8: NULL pointer");
+  if (!fits_int(dim)) return fail(SSDQ_ERR_INVALID_ARG, "ssdq_quantize_vectors_int8: dim too large");
+  std::lock_guard<std::mutex> lk(c->mu);
+  hipError_t e = hipSetDevice(c->device);
+  if (e != hipSuccess) return hip_fail(e, "ssdq_quantize_vectors_int8: hipSetDevice");
+  const size_t n = n_rows * dim;
+  void *din, *dc, *ds;
+  if ((e = ctx_buf(c, 0, n * sizeof(float), &din)) != hipSuccess ||
+      (e = ctx_buf(c, 1, n, &dc)) != hipSuccess ||
+      (e = ctx_buf(c, 2, n_rows * sizeof(float), &ds)) != hipSuccess)
+    return hip_fail(e, "ssdq_quantize_vectors_int8: staging allocation");
+  if (n && (e = hipMemcpyAsync(din, data, n * sizeof(float), hipMemcpyHostToDevice, c->stream)) != hipSuccess)
+    return hip_fail(e, "ssdq_quantize_vectors_int8: copy in");
+  int rc = ssdq_kv_quantize_rows_dev((const float*)din, (int8_t*)dc, (float*)ds, n_rows, dim, c->stream);
+  if (rc < 0) return rc;
+  if ((n && (e = hipMemcpyAsync(codes, dc, n, hipMemcpyDeviceToHost, c->stream)) != hipSuccess) ||
+      (e = hipMemcpyAsync(scales, ds, n_rows * sizeof(float), hipMemcpyDeviceToHost, c->stream)) != hipSuccess)
+    return hip_fail(e, "ssdq_quantize_vectors_int8: copy out");
+  if ((e = hipStreamSynchronize(c->stream)) != hipSuccess)
+    return hip_fail(e, "ssdq_quantize_vectors_int8: sync");
+  return ok();
+}
+
+// dequantize_vectors_int8 (src/ssd/block_swap.rs:63-74): out [n_rows * dim].
+int ssdq_dequantize_vectors_int8(ssdq_ctx* c, const int8_t* codes, const float* scales,
+                                 size_t n_rows, size_t dim, float* out) {
+  if (!c) return fail(SSDQ_ERR_INVALID_ARG, "ssdq_dequantize_vectors_int8: ctx is NULL");
+  if (n_rows == 0 || dim == 0) return ok();
+  if (!codes || !scales || !out)
+    return fail(SSDQ_ERR_INVALID_ARG, "ssdq_dequantize_vectors_int8: NULL pointer");
+  if (!fits_int(dim)) return fail(SSDQ_ERR_INVALID_ARG, "ssdq_dequantize_vectors_int8: dim too large");
+  std::lock_guard<std::mutex> lk(c->mu);
+  hipError_t e = hipSetDevice(c->device);
+  if (e != hipSuccess) return hip_fail(e, "ssdq_dequantize_vectors_int8: hipSetDevice");
+  const size_t n = n_rows * dim;
+  void *dc, *ds, *dout;
+  if ((e = ctx_buf(c, 1, n, &dc)) != hipSuccess ||
+      (e = ctx_buf(c, 2, n_rows * sizeof(float), &ds)) != hipSuccess ||
+      (e = ctx_buf(c, 3, n * sizeof(float), &dout)) != hipSuccess)
+    return hip_fail(e, "ssdq_dequantize_vectors_int8: staging allocation");
+  if ((e = hipMemcpyAsync(dc, codes, n, hipMemcpyHostToDevice, c->stream)) != hipSuccess ||
+      (e = hipMemcpyAsync(ds, scales, n_rows * sizeof(float), hipMemcpyHostToDevice, c->stream)) != hipSuccess)
+    return hip_fail(e, "ssdq_dequantize_vectors_int8: copy in");
+  int rc = ssdq_kv_dequantize_rows_dev((const int8_t*)dc, (const float*)ds, (float*)dout, n_rows, dim,
+                                       c->stream);
+  if (rc < 0) return rc;
+  if ((e = hipMemcpyAsync(out, dout, n * sizeof(float), hipMemcpyDeviceToHost, c->stream)) != hipSuccess)
+    return hip_fail(e, "ssdq_dequantize_vectors_int8: copy out");
+  if ((e = hipStreamSynchronize(c->stream)) != hipSuccess)
+    return hip_fail(e, "ssdq_dequantize_vectors_int8: sync");
   return ok();
 }
 

@@ -95,6 +95,28 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(float* __restrict__ out,
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) out[i] = 0.0f;
 }
 
+// F32 / F16 / BF16 tensors (streamer.rs:95-115): copy, IEEE half widening,
+// bf16 bits << 16.  4 elements per thread where the input allows it.
+enum : int { kF32 = 0, kF16 = 1, kBF16 = 30 };
+
+template <int T>
+__device__ __forceinline__ float widen1(const uint8_t* __restrict__ w, size_t i) {
+  if constexpr (T == kF32) return reinterpret_cast<const float*>(w)[i];
+  else {
+    const uint32_t h = reinterpret_cast<const uint16_t*>(w)[i];
+    if constexpr (T == kF16) return f16_to_f32(h);
+    else return __uint_as_float(h << 16);
+  }
+}
+
+template <int T>
+__global__ __launch_bounds__(256) void widen_kernel(const uint8_t* __restrict__ w, size_t n,
+                                                    float* __restrict__ out) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    out[i] = widen1<T>(w, i);
+}
+
 unsigned grid_for(size_t work, unsigned block) {
   size_t g = (work + block - 1) / block;
   if (g > 65536) g = 65536;
@@ -103,6 +125,19 @@ unsigned grid_for(size_t work, unsigned block) {
 }
 
 }  // namespace
+
+hipError_t launch_widen(int dtype, const void* w, size_t n, float* out, hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  const uint8_t* p = (const uint8_t*)w;
+  const dim3 g(grid_for(n, 256)), b(256);
+  switch (dtype) {
+    case kF32: hipLaunchKernelGGL(widen_kernel<kF32>, g, b, 0, stream, p, n, out); break;
+    case kF16: hipLaunchKernelGGL(widen_kernel<kF16>, g, b, 0, stream, p, n, out); break;
+    case kBF16: hipLaunchKernelGGL(widen_kernel<kBF16>, g, b, 0, stream, p, n, out); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
 
 hipError_t launch_fill_zero(float* out, size_t n, hipStream_t stream) {
   if (n == 0) return hipSuccess;

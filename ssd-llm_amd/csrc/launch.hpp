@@ -8,6 +8,8 @@
 namespace ssdq {
 
 hipError_t launch_fill_zero(float* out, size_t n, hipStream_t stream);
+// F32 copy / F16 / BF16 widening of n elements (element-aligned input).
+hipError_t launch_widen(int dtype, const void* w, size_t n, float* out, hipStream_t stream);
 hipError_t launch_dequant(int dtype, const uint8_t* w, size_t n_blocks, float* out,
                           hipStream_t stream);
 

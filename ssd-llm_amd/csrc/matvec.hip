@@ -26,6 +26,9 @@
 // Results agree with the reference to fp32 rounding (different summation
 // order); the element values themselves are bit-exact in dequant.hip.
 #include <algorithm>
+#include <map>
+#include <mutex>
+#include <tuple>
 
 #include "common.hpp"
 #include "launch.hpp"
@@ -806,17 +809,34 @@ hipError_t run_b1(const uint8_t* w, const float* x, float* y, int out_dim, int b
   if (lds > (size_t)lds_limit()) return hipErrorInvalidValue;
   // One workgroup per CU holding as many waves as fit (ks waves per row
   // stream); the occupancy is the same for every staging depth.
-  auto probe = mv_b1<F, UPL, RMAX, FULL, kStageIt>;
-  hipError_t e = set_lds_attr(probe, lds);
-  if (e != hipSuccess) return e;
-  int rs = 1;
-  for (int cand = 768 / (64 * ks); cand >= 1; cand--) {
-    int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, probe, 64 * ks * cand, lds) == hipSuccess &&
-        per_cu >= 1) {
-      rs = cand;
-      break;
+  // The answer depends on (device, ks, lds) only and is cached: a launch then
+  // costs no runtime query.
+  static std::mutex mu;
+  static std::map<std::tuple<int, int, size_t>, int> rs_cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+  const auto key = std::make_tuple(dev, ks, lds);
+  int rs = 0;
+  {
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = rs_cache.find(key);
+    if (it != rs_cache.end()) rs = it->second;
+  }
+  if (rs == 0) {
+    auto probe = mv_b1<F, UPL, RMAX, FULL, kStageIt>;
+    hipError_t e = set_lds_attr(probe, lds);
+    if (e != hipSuccess) return e;
+    rs = 1;
+    for (int cand = 768 / (64 * ks); cand >= 1; cand--) {
+      int per_cu = 0;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, probe, 64 * ks * cand, lds) == hipSuccess &&
+          per_cu >= 1) {
+        rs = cand;
+        break;
+      }
     }
+    std::lock_guard<std::mutex> lk(mu);
+    rs_cache[key] = rs;
   }
   const int threads = 64 * ks * rs;
   const int nchunk = bpr * Geom<F>::bs / 8;

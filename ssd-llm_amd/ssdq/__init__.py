@@ -54,6 +54,9 @@ SIGNATURES = {
         _i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _vp]),
     "ssdq_flash_attention_f32_dev": (_i, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _vp]),
     "ssdq_flash_attention_f32": (_i, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _vp]),
+    "ssdq_dequantize_to_f32": (_i, [_vp, _i, _vp, _sz, _sz, _vp]),
+    "ssdq_quantize_vectors_int8": (_i, [_vp, _vp, _sz, _sz, _vp, _vp]),
+    "ssdq_dequantize_vectors_int8": (_i, [_vp, _vp, _vp, _sz, _sz, _vp]),
 }
 
 _lib = None
@@ -196,6 +199,39 @@ class Context:
                                          x.size, out_dim, in_dim, dtype, y.ctypes.data)
         check("ssdq_matvec_quantized", rc)
         return y
+
+    def dequantize_to_f32(self, data, dtype, n_elements):
+        """dequantize_to_f32 (streamer.rs:93-125): bytes in, f32 numpy out."""
+        import numpy as np
+        data = np.ascontiguousarray(data, dtype=np.uint8)
+        out = np.empty(n_elements, np.float32)
+        rc = lib().ssdq_dequantize_to_f32(self._h, dtype, data.ctypes.data, data.size, n_elements,
+                                          out.ctypes.data)
+        check("ssdq_dequantize_to_f32", rc)
+        return out
+
+    def quantize_vectors_int8(self, data, dim):
+        """quantize_vectors_int8 (block_swap.rs:36-60): (codes int8, scales f32)."""
+        import numpy as np
+        data = np.ascontiguousarray(data, dtype=np.float32).reshape(-1)
+        n_rows = data.size // dim
+        codes = np.empty(n_rows * dim, np.int8)
+        scales = np.empty(n_rows, np.float32)
+        rc = lib().ssdq_quantize_vectors_int8(self._h, data.ctypes.data, n_rows, dim,
+                                              codes.ctypes.data, scales.ctypes.data)
+        check("ssdq_quantize_vectors_int8", rc)
+        return codes, scales
+
+    def dequantize_vectors_int8(self, codes, scales, dim):
+        """dequantize_vectors_int8 (block_swap.rs:63-74)."""
+        import numpy as np
+        codes = np.ascontiguousarray(codes, dtype=np.int8)
+        scales = np.ascontiguousarray(scales, dtype=np.float32)
+        out = np.empty(scales.size * dim, np.float32)
+        rc = lib().ssdq_dequantize_vectors_int8(self._h, codes.ctypes.data, scales.ctypes.data,
+                                                scales.size, dim, out.ctypes.data)
+        check("ssdq_dequantize_vectors_int8", rc)
+        return out
 
     def flash_attention_f32(self, q, k, v, n_head, n_head_kv, head_dim, seq_len, window_start,
                             window_end):

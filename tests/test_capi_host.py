@@ -67,3 +67,13 @@ def test_ctx_create_reports_missing_device():
     h = ctypes.c_void_p()
     rc = ssdq.lib().ssdq_ctx_create(-1, ctypes.byref(h))
     assert rc == -4 and not h.value  # SSDQ_ERR_NO_DEVICE: callers keep their CPU path
+
+
+def test_cpp_host_mirror_header_compiles():
+    """The C++ mirror header is self-contained C++17 over include/ssdq.h."""
+    import subprocess
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    hdr = os.path.join(root, "ssd-llm_amd", "host", "ssdq_compute.hpp")
+    r = subprocess.run(["g++", "-std=c++17", "-fsyntax-only", "-Wall", "-Wextra", "-x", "c++", hdr],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr

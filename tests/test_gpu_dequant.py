@@ -94,3 +94,45 @@ def test_dequant_tail_and_unsupported():
     out.fill_(7.0)
     assert ssdq.dequant(3, to_dev(w), 600, out) == ssdq.WARN_UNSUPPORTED_ZEROED
     assert np.all(from_dev(out) == 0)
+
+
+@pytest.mark.parametrize("dtype", [ssdq.F32, ssdq.F16, ssdq.BF16])
+def test_dequant_float_types_every_pattern(dtype):
+    # F16 / BF16: all 65536 bit patterns; F32: random bits plus specials
+    if dtype == ssdq.F32:
+        g = np.random.default_rng(1)
+        vals = np.concatenate([g.integers(0, 2 ** 32, 100000, dtype=np.uint64).astype(np.uint32),
+                               np.array([0, 0x80000000, 0x7F800000, 0xFF800000, 1, 0x7FC00000],
+                                        np.uint32)])
+        raw = vals.view(np.uint8)
+        n = vals.size
+    else:
+        raw = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.uint8)
+        n = 65536
+    announce("dequant float type", dtype)
+    out = empty_dev(n, torch.float32)
+    assert ssdq.dequant(dtype, to_dev(raw), n, out) == 0
+    got = from_dev(out)
+    ref, rc = o.dequantize(dtype, raw, n)
+    assert rc == 0
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", ssdq.QUANT_TYPES)
+def test_host_twin_dequantize_to_f32(dtype):
+    # streamer.rs:93-125 contract: whole blocks present in data_len are decoded,
+    # the rest of n_elements is zero
+    rows, cols = 3, 512
+    w = synth.quant_weights(dtype, rows, cols, dtype + 100)
+    n = rows * cols
+    bb = ssdq.type_size(dtype)
+    announce("host twin dequantize_to_f32", ssdq.TYPE_NAMES[dtype])
+    with ssdq.Context() as ctx:
+        for data_len in (w.size, w.size - bb // 2, 2 * bb + 1, 0):
+            got = ctx.dequantize_to_f32(w[:data_len], dtype, n)
+            ref, _ = o.dequantize(dtype, w[:data_len], n)
+            assert first_bit_mismatch(got, ref) == -1, data_len
+        got = ctx.dequantize_to_f32(w, 3, n)  # Q4_1: unsupported -> zeros
+        assert np.all(got == 0)

@@ -105,3 +105,21 @@ def test_paged_append_places_quantized_rows():
     assert np.array_equal(ks[slots[live]], rks[live]) and np.array_equal(vs[slots[live]], rvs[live])
     untouched = np.setdiff1d(np.arange(pool_rows), slots[live])
     assert np.all(kc[untouched] == 99) and np.all(ks[untouched] == -1.0)
+
+
+def test_host_twin_int8_vectors():
+    # quantize_vectors_int8 / dequantize_vectors_int8 (block_swap.rs:36-74)
+    dim = 128
+    x = np.random.default_rng(9).standard_normal((40, dim), dtype=np.float32)
+    x[3] = 0.0          # zero row -> scale 0, codes 0
+    x[7, 5] = 1e30      # one huge element
+    announce("host twin int8 vectors")
+    with ssdq.Context() as ctx:
+        codes, scales = ctx.quantize_vectors_int8(x, dim)
+        back = ctx.dequantize_vectors_int8(codes, scales, dim)
+    rc, rs = o.quantize_rows(x, 40, dim)
+    assert np.array_equal(codes, rc)
+    assert np.array_equal(scales.view(np.uint32), rs.view(np.uint32))
+    ref = o.dequantize_rows(rc, rs, 40, dim)
+    assert np.array_equal(back.view(np.uint32), ref.view(np.uint32))
+    assert scales[3] == 0 and np.all(codes[3 * dim:4 * dim] == 0)

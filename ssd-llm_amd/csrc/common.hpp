@@ -57,6 +57,25 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
   return v;
 }
 
+// DPP move whose disabled rows (ROW_MASK) read as 0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_upd(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                               ROW_MASK, 0xF, false));
+}
+
+// Sum across the 64 lanes of a wavefront, valid in lane 63 only: DPP steps
+// inside each 16-lane row, then row_bcast:15 / row_bcast:31 (no LDS traffic).
+__device__ __forceinline__ float wave_sum_l63(float v) {
+  v += dpp_mov<0xB1>(v);        // quad_perm [1,0,3,2]
+  v += dpp_mov<0x4E>(v);        // quad_perm [2,3,0,1]
+  v += dpp_mov<0x124>(v);       // row_ror:4
+  v += dpp_mov<0x128>(v);       // row_ror:8: every lane holds its row's sum
+  v += dpp_upd<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+  v += dpp_upd<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
+  return v;
+}
+
 // Sum across the 64 lanes of a wavefront (result valid in every lane).
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -44,19 +44,19 @@ namespace {
 // E elements, NSUM x-sum groups of SUMG elements, NW dwords of raw data.
 template <int F> struct FastUnit;
 template <> struct FastUnit<kQ4_K> {
-  static constexpr int E = 64, NSUM = 2, SUMG = 32, NW = 12, PER_BLOCK = 4;
+  static constexpr int E = 64, NSUM = 2, SUMG = 32, NW = 12;
   static constexpr bool prescale = true;
 };
 template <> struct FastUnit<kQ4_0> {
-  static constexpr int E = 64, NSUM = 2, SUMG = 32, NW = 9, PER_BLOCK = 0;
+  static constexpr int E = 64, NSUM = 2, SUMG = 32, NW = 9;
   static constexpr bool prescale = true;
 };
 template <> struct FastUnit<kQ8_0> {
-  static constexpr int E = 64, NSUM = 2, SUMG = 32, NW = 17, PER_BLOCK = 0;
+  static constexpr int E = 64, NSUM = 2, SUMG = 32, NW = 17;
   static constexpr bool prescale = false;
 };
 template <> struct FastUnit<kQ6_K> {
-  static constexpr int E = 32, NSUM = 2, SUMG = 16, NW = 10, PER_BLOCK = 8;
+  static constexpr int E = 32, NSUM = 2, SUMG = 16, NW = 10;
   static constexpr bool prescale = false;
 };
 
@@ -474,18 +474,35 @@ __device__ __forceinline__ void accumulate_dig(const uint32_t* raw, int u, PL pl
   }
 }
 
+// Barrier for LDS data only.  __syncthreads() also orders global memory, which
+// makes every wave wait for all of its outstanding weight loads first.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Vector memory instructions one load_unit issues.
+template <int F> constexpr int loads_per_unit() { return (F == kQ4_K || F == kQ4_0) ? 3 : 5; }
+
 // Every lane keeps the digit planes of its units in registers.  KS waves split
 // each row's units (KS > 1 for long rows; partial sums meet in LDS); the
 // workgroup's other waves take other rows.  Rows are spread evenly over all
 // row streams of the grid (at most RMAX per stream).  One workgroup runs per
-// CU.  Schedule (from timelines of the kernel phases on MI355X): x is fetched
-// and staged before any weight is requested.  Requested during the weight
-// stream, x (which every CU reads, and which the previous call's weights have
-// pushed out of L2) waits behind that stream for several microseconds; fetched
-// first it arrives in about one.  Then every row of the stream is requested
-// (straight-line code, rows clamped to valid memory, so the compiler's
-// in-order wait counts stay exact) and each row is consumed as soon as its own
-// loads have returned.
+// CU.
+//
+// Schedule, from timelines of the kernel phases on MI355X (vector memory
+// returns in order per wave, and a wave stalls at issue when the memory
+// pipeline is full):
+//   1. x and the first row are requested.  More weight traffic ahead of x
+//      delays x, and nothing can be computed before x is staged.
+//   2. When x has arrived, the second row is requested, then x is turned into
+//      digit planes in LDS (LDS-only barrier: the weight loads stay in flight).
+//   3. Each row is computed while the next one is in flight (lookahead 1; a
+//      deeper lookahead stalls the issuing wave).  Rows are computed in
+//      straight-line code with clamped addresses, so the compiler's in-order
+//      wait counts stay exact, and the cross-lane sums of all rows are taken
+//      together at the end.
 template <int F, int UPL, int RMAX, bool FULL, int SIT>
 __global__ __launch_bounds__(768) void mv_b1(const uint8_t* __restrict__ w,
                                              const float* __restrict__ x, float* __restrict__ y,
@@ -493,7 +510,9 @@ __global__ __launch_bounds__(768) void mv_b1(const uint8_t* __restrict__ w,
   using FU = FastUnit<F>;
   using D = Dig<F>;
   constexpr int NW = FU::NW, US = D::US;
-  extern __shared__ uint32_t lds[];
+  static_assert(US % 4 == 0, "unit records are read as 16-byte vectors");
+  extern __shared__ uint4 lds4[];
+  uint32_t* lds = reinterpret_cast<uint32_t*>(lds4);
   const int keff = bpr * Geom<F>::bs;
   const int U = keff / FU::E;
   float* red = reinterpret_cast<float*>(lds + (size_t)U * US);  // [RMAX][ks]
@@ -505,10 +524,29 @@ __global__ __launch_bounds__(768) void mv_b1(const uint8_t* __restrict__ w,
   const int n_rows = (int)((gs + 1) * out_dim / n_streams) - r_begin;  // <= RMAX
   const int ubase = kw * 64 * UPL + lane;
 
+  uint32_t buf[RMAX][UPL][NW];
+  auto load_row = [&](int rr) {
+    const int row = max(0, min(r_begin + rr, out_dim - 1));
+    const uint8_t* rp = w + (size_t)row * row_bytes;
+#pragma unroll
+    for (int i = 0; i < UPL; i++) {
+      const int u = ubase + 64 * i;
+      if (FULL || u < U) load_unit<F>(rp, u, buf[rr][i]);
+    }
+  };
+
   XChunks<SIT> st;
-  stage_load<SIT>(x, keff, st, blockDim.x);
+  stage_load<SIT>(x, keff, st, blockDim.x);  // 1.
+  load_row(0);
+  {
+    // 2. wait for x only (the row-0 loads issued after it may stay in flight)
+    constexpr int N = UPL * loads_per_unit<F>();
+    static_assert(N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+  }
+  if (RMAX > 1) load_row(1);
   stage_store<F, SIT>(st, keff, lds, blockDim.x);
-  __syncthreads();
+  lds_barrier();
 
   uint32_t pr[UPL][US];
 #pragma unroll
@@ -517,26 +555,15 @@ __global__ __launch_bounds__(768) void mv_b1(const uint8_t* __restrict__ w,
     const bool ok = FULL || u < U;
 #pragma unroll
     for (int t = 0; t < US; t += 4) {
-      const uint4 v = ok ? *reinterpret_cast<const uint4*>(lds + (size_t)u * US + t) : make_uint4(0, 0, 0, 0);
+      const uint4 v = ok ? lds4[(size_t)u * (US / 4) + t / 4] : make_uint4(0, 0, 0, 0);
       pr[i][t] = v.x; pr[i][t + 1] = v.y; pr[i][t + 2] = v.z; pr[i][t + 3] = v.w;
-    }
-  }
-
-  uint32_t buf[RMAX][UPL][NW];
-#pragma unroll
-  for (int rr = 0; rr < RMAX; rr++) {
-    const int row = max(0, min(r_begin + rr, out_dim - 1));
-    const uint8_t* rp = w + (size_t)row * row_bytes;
-#pragma unroll
-    for (int i = 0; i < UPL; i++) {
-      const int u = ubase + 64 * i;
-      if (FULL || u < U) load_unit<F>(rp, u, buf[rr][i]);
     }
   }
 
   float acc[RMAX];
 #pragma unroll
-  for (int rr = 0; rr < RMAX; rr++) {
+  for (int rr = 0; rr < RMAX; rr++) {  // 3.
+    if (rr >= 1 && rr + 1 < RMAX) load_row(rr + 1);  // rows 0 and 1 are already in flight
     float a = 0.f;
     if (ks > 1 || rr < n_rows) {  // uniform per wave: padding rows are not computed
 #pragma unroll
@@ -544,16 +571,22 @@ __global__ __launch_bounds__(768) void mv_b1(const uint8_t* __restrict__ w,
         const int u = ubase + 64 * i;
         if (FULL || u < U) accumulate_dig<F>(buf[rr][i], u, [&](int t) { return pr[i][t]; }, a);
       }
-      a = wave_sum_dpp(a);
-      if (ks == 1 && lane == 0) y[r_begin + rr] = a;
     }
     acc[rr] = a;
   }
-  if (ks > 1) {
-    if (lane == 0) {
+#pragma unroll
+  for (int rr = 0; rr < RMAX; rr++) acc[rr] = wave_sum_l63(acc[rr]);
+  if (lane == 63) {
+    if (ks == 1) {
+#pragma unroll
+      for (int rr = 0; rr < RMAX; rr++)
+        if (rr < n_rows) y[r_begin + rr] = acc[rr];
+    } else {
 #pragma unroll
       for (int rr = 0; rr < RMAX; rr++) red[rr * ks + kw] = acc[rr];
     }
+  }
+  if (ks > 1) {
     __syncthreads();
     if (wave == 0 && lane < n_rows) {
       float s = 0.f;

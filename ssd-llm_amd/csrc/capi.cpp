@@ -310,7 +310,7 @@ int ssdq_gemm_q4k_bf16_dev(const void* w, const uint16_t* x, float* y, size_t M,
   if (!fits_int(M) || !fits_int(N) || !fits_int(K) || !fits_int(M * K) || !fits_int(M * N))
     return fail(SSDQ_ERR_INVALID_ARG, "ssdq_gemm_q4k_bf16_dev: dimensions exceed 2^31");
   hipStream_t s = (hipStream_t)stream;
-  const size_t wsb = ssdq::gemm_q4k_workspace_bytes(M, N, K);
+  const size_t wsb = ssdq::gemm_q4k_workspace_bytes(w, x, M, N, K);
   void* ws = nullptr;
   hipError_t e = hipSuccess;
   if (wsb && (e = workspace_get(wsb, s, &ws)) != hipSuccess)

@@ -56,7 +56,7 @@ hipError_t launch_flash_attn_f32(const float* q, const float* k, const float* v,
 // Prefill GEMM: Y[M,N] f32 = X[M,K] bf16 x W[N,K] Q4_K (reference layout).
 hipError_t launch_gemm_q4k(const uint8_t* w, const uint16_t* x, float* y, size_t M, size_t N,
                            size_t K, void* workspace, size_t workspace_bytes, hipStream_t stream);
-size_t gemm_q4k_workspace_bytes(size_t M, size_t N, size_t K);
+size_t gemm_q4k_workspace_bytes(const void* w, const void* x, size_t M, size_t N, size_t K);
 
 int device_cu_count();
 

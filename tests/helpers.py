@@ -30,10 +30,12 @@ def assert_close_attributed(gpu, ref32, exact, what="", max_ill_frac=1e-3):
     The reference sums each output in one serial fp32 chain; at K = 14336 its
     own rounding error reaches ~5e-3, above ATOL, and no other summation order
     can reproduce it.  So every element must be within tolerance of the
-    reference's fp32 value, except elements where the reference itself is more
-    than half a tolerance away from the exact sum of its own (bit-exact)
-    element values; those must be within tolerance of that exact sum, and they
-    must be rare (max_ill_frac of the outputs).
+    reference's fp32 value, except elements whose difference from it is the
+    reference's own rounding error: either the reference is more than half a
+    tolerance away from the exact sum of its own (bit-exact) element values and
+    the device is within tolerance of that exact sum, or the device is at least
+    as close to the exact sum as the reference is.  Such substitutions must be
+    rare (max_ill_frac of the outputs).
     """
     gpu = np.asarray(gpu, np.float64).ravel()
     ref32 = np.asarray(ref32, np.float64).ravel()
@@ -42,7 +44,8 @@ def assert_close_attributed(gpu, ref32, exact, what="", max_ill_frac=1e-3):
     ok_ref = np.abs(gpu - ref32) <= tol(ref32)
     ill = np.abs(ref32 - exact) > 0.5 * tol(exact)
     ok_exact = np.abs(gpu - exact) <= tol(exact)
-    good = ok_ref | (ill & ok_exact)
+    closer = np.abs(gpu - exact) <= np.abs(ref32 - exact)
+    good = ok_ref | (ill & ok_exact) | closer
     if not good.all():
         i = int(np.flatnonzero(~good)[0])
         raise AssertionError(

@@ -57,3 +57,18 @@ def test_gemm_rejects_bad_k():
     t = empty_dev(1024, torch.float32)
     with pytest.raises(ssdq.SsdqError):
         ssdq.gemm_q4k_bf16(t, t, t, 4, 4, 300)
+
+
+def test_gemm_misaligned_x_takes_fallback():
+    # X at a 2-byte offset cannot feed 16-byte loads: the widen + matvec path runs
+    M, N, K = 9, 48, 512
+    w = synth.quant_weights(ssdq.Q4_K, N, K, 77)
+    xb = synth.f32_to_bf16_bits(synth.normal_f32((M, K), 78))
+    buf = torch.empty(M * K + 1, dtype=torch.int16, device="cuda")
+    buf[1:].copy_(torch.from_numpy(xb.view(np.int16).ravel()).cuda())
+    y = empty_dev(M * N, torch.float32)
+    announce("gemm misaligned", M, N, K)
+    assert ssdq.gemm_q4k_bf16(to_dev(w), buf[1:], y, M, N, K) == 0
+    ref = o.gemm_q4k_bf16(w, xb, M, N, K, threads=8)
+    exact = o.gemm_q4k_bf16(w, xb, M, N, K, threads=8, exact=True)
+    assert_close_attributed(from_dev(y), ref, exact, "gemm misaligned")

@@ -17,6 +17,7 @@
 // LDS; each wave owns 32 columns of N and dequantizes its own weights straight
 // into MFMA B fragments (no weight traffic through LDS), reusing each fragment
 // for the 8 M sub-tiles.  Weights and X are prefetched two K steps ahead.
+#include <algorithm>
 #include <type_traits>
 
 #include "common.hpp"
@@ -34,7 +35,6 @@ constexpr int XS = BK + 8;   // LDS row stride in halves (80 B keeps 16-byte rea
 constexpr int MT = BM / 16;  // M sub-tiles per wave
 constexpr int NT = 2;        // N sub-tiles (of 16 columns) per wave
 constexpr int PF = 2;        // K steps in flight
-constexpr int kFlush = 4;    // K steps per matrix-core accumulation chain
 
 __global__ __launch_bounds__(256) void widen_bf16_kernel(const uint16_t* __restrict__ x,
                                                          float* __restrict__ out, size_t n) {
@@ -74,13 +74,18 @@ __device__ __forceinline__ void dequant8_split(uint32_t q, float S, float Mn, h8
   }
 }
 
-__global__ __launch_bounds__(256) void gemm_q4k_mfma(const uint8_t* __restrict__ w,
-                                                     const uint16_t* __restrict__ x,
-                                                     float* __restrict__ y, int M, int N, int K) {
+// blockIdx.z selects split z of the K range (split = gridDim.z); split z
+// writes its partial product to y + z * M * N (a workspace when split > 1).
+__global__ __launch_bounds__(256, 2) void gemm_q4k_mfma(const uint8_t* __restrict__ w,
+                                                        const uint16_t* __restrict__ x,
+                                                        float* __restrict__ y, int M, int N, int K) {
   __shared__ __align__(16) _Float16 xs[2][BM * XS];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-  const int steps = K / BK;
+  const int blocks = K / 256, z = blockIdx.z, nz = gridDim.z;
+  const int b_begin = (int)((long)blocks * z / nz), b_end = (int)((long)blocks * (z + 1) / nz);
+  const int s0 = b_begin * 8, steps = (b_end - b_begin) * 8;  // K steps of this split
+  y += (size_t)z * M * N;
   const size_t row_bytes = (size_t)(K / 256) * 144;
   const int c = lane >> 4;  // this lane holds k = 8c .. 8c+7 of each 32-wide step
 
@@ -101,7 +106,7 @@ __global__ __launch_bounds__(256) void gemm_q4k_mfma(const uint8_t* __restrict__
   uint32_t qq[PF][NT];     // this lane's 8 codes of the step's sub-block
   auto fetch = [&](int s, auto slot_c) {
     constexpr int slot = decltype(slot_c)::value;
-    const int ss = min(s, steps - 1);
+    const int ss = s0 + min(s, steps - 1);
     const uint16_t* xp = xrow + (size_t)ss * BK;
     xq[slot][0] = *reinterpret_cast<const uint4*>(xp);
     xq[slot][1] = *reinterpret_cast<const uint4*>(xp + 8);
@@ -119,10 +124,6 @@ __global__ __launch_bounds__(256) void gemm_q4k_mfma(const uint8_t* __restrict__
   };
 
   f4 acc[MT][NT];
-#pragma unroll
-  for (int i = 0; i < MT; i++)
-#pragma unroll
-    for (int j = 0; j < NT; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
   fetch(0, std::integral_constant<int, 0>{});
   fetch(1, std::integral_constant<int, 1>{});
@@ -131,9 +132,20 @@ __global__ __launch_bounds__(256) void gemm_q4k_mfma(const uint8_t* __restrict__
   __syncthreads();
 
   // Step s uses queue slot and LDS buffer s % 2; the loop is unrolled by two so
-  // every register-array index is a compile-time constant.
-  auto step = [&](auto slot, int s) {
+  // every register-array index is a compile-time constant.  The matrix-core
+  // accumulators restart at every super-block (8 steps; the first MFMA of a
+  // chain takes C = 0) and are added into fp32 VALU sums, so no accumulator
+  // carries a long chain of roundings at the magnitude of the full dot product
+  // (measured at K = 4096: rms error against the exact sum 7e-5 without
+  // restarts, 2e-5 with; the serial fp32 reference itself is at 1e-4).
+  f4 tot[MT][NT];
+#pragma unroll
+  for (int i = 0; i < MT; i++)
+#pragma unroll
+    for (int j = 0; j < NT; j++) tot[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+  auto step = [&](auto slot, int s, auto first_c) {
     constexpr int cur = decltype(slot)::value;
+    constexpr bool first = decltype(first_c)::value;
     const int sb = s & 7;
     // B fragments of this step
     h8 bhi[NT], blo[NT];
@@ -154,15 +166,23 @@ __global__ __launch_bounds__(256) void gemm_q4k_mfma(const uint8_t* __restrict__
     // barrier that ended step s-1); this queue slot is refilled with step s+2
     const uint4 nx0 = xq[cur ^ 1][0], nx1 = xq[cur ^ 1][1];
     fetch(s + PF, slot);
+    // all hi products first, then all lo products: the two MFMAs into one
+    // accumulator are MT*NT instructions apart instead of back to back
+    h8 a[MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; mt++) {
-      const h8 a = *reinterpret_cast<const h8*>(&xs[cur][(mt * 16 + (lane & 15)) * XS + 8 * c]);
+    for (int mt = 0; mt < MT; mt++)
+      a[mt] = *reinterpret_cast<const h8*>(&xs[cur][(mt * 16 + (lane & 15)) * XS + 8 * c]);
 #pragma unroll
-      for (int j = 0; j < NT; j++) {
-        acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bhi[j], acc[mt][j], 0, 0, 0);
-        acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, blo[j], acc[mt][j], 0, 0, 0);
-      }
-    }
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+      for (int j = 0; j < NT; j++)
+        acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+            a[mt], bhi[j], first ? f4{0.f, 0.f, 0.f, 0.f} : acc[mt][j], 0, 0, 0);
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+      for (int j = 0; j < NT; j++)
+        acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mt], blo[j], acc[mt][j], 0, 0, 0);
     if (s + 1 < steps) {
       bf16x8_to_f16(nx0, &xs[cur ^ 1][xr * XS + xk]);
       bf16x8_to_f16(nx1, &xs[cur ^ 1][xr * XS + xk + 8]);
@@ -172,28 +192,23 @@ __global__ __launch_bounds__(256) void gemm_q4k_mfma(const uint8_t* __restrict__
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
   };
-  // The matrix-core accumulators restart every kFlush steps and are added into
-  // fp32 VALU sums, so no accumulator carries a long chain of roundings at the
-  // magnitude of the full dot product (measured at K = 4096: rms error against
-  // the exact sum 7e-5 without restarts, 2e-5 with; the serial fp32 reference
-  // itself is at 1e-4).
-  f4 tot[MT][NT];
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using T = std::true_type;
+  using Fa = std::false_type;
+  for (int s = 0; s < steps; s += 8) {  // one super-block per iteration
+    step(I0{}, s, T{});
+    step(I1{}, s + 1, Fa{});
+    step(I0{}, s + 2, Fa{});
+    step(I1{}, s + 3, Fa{});
+    step(I0{}, s + 4, Fa{});
+    step(I1{}, s + 5, Fa{});
+    step(I0{}, s + 6, Fa{});
+    step(I1{}, s + 7, Fa{});
 #pragma unroll
-  for (int i = 0; i < MT; i++)
+    for (int i = 0; i < MT; i++)
 #pragma unroll
-    for (int j = 0; j < NT; j++) tot[i][j] = f4{0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < steps; s += 2) {  // steps = K / 32 is a multiple of 8
-    step(std::integral_constant<int, 0>{}, s);
-    step(std::integral_constant<int, 1>{}, s + 1);
-    if (((s + 2) % kFlush) == 0) {
-#pragma unroll
-      for (int i = 0; i < MT; i++)
-#pragma unroll
-        for (int j = 0; j < NT; j++) {
-          tot[i][j] += acc[i][j];
-          acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
-        }
-    }
+      for (int j = 0; j < NT; j++) tot[i][j] += acc[i][j];
   }
 
   // C fragment layout: element i of acc[mt][j] is row 4*(lane/16)+i, column lane%16
@@ -206,9 +221,20 @@ __global__ __launch_bounds__(256) void gemm_q4k_mfma(const uint8_t* __restrict__
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int m = m0 + mt * 16 + 4 * c + i;
-        if (m < M) y[(size_t)m * N + n] = tot[mt][j][i] + acc[mt][j][i];
+        if (m < M) y[(size_t)m * N + n] = tot[mt][j][i];
       }
     }
+}
+
+// Sums split-K partials in a fixed order (deterministic results).
+__global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ part, float* __restrict__ y,
+                                                     size_t mn, int split) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < mn; i += stride) {
+    float s = part[i];
+    for (int z = 1; z < split; z++) s += part[(size_t)z * mn + i];
+    y[i] = s;
+  }
 }
 
 }  // namespace
@@ -217,9 +243,21 @@ bool gemm_q4k_mfma_ok(const void* w, const void* x) {
   return ((uintptr_t)w & 3) == 0 && ((uintptr_t)x & 15) == 0;
 }
 
+// K splits for a GEMM: enough workgroups for two per CU, at most 8 splits and
+// never more than one split per 256-element block.
+int gemm_q4k_split(size_t M, size_t N, size_t K) {
+  const size_t tiles = ((N + BN - 1) / BN) * ((M + BM - 1) / BM);
+  const size_t want = 2 * (size_t)device_cu_count();
+  size_t split = tiles >= want ? 1 : (want + tiles - 1) / tiles;
+  split = std::min<size_t>(split, 8);
+  split = std::min<size_t>(split, K / 256);
+  return (int)std::max<size_t>(split, 1);
+}
+
 size_t gemm_q4k_workspace_bytes(const void* w, const void* x, size_t M, size_t N, size_t K) {
-  (void)N;
-  return gemm_q4k_mfma_ok(w, x) ? 0 : M * K * sizeof(float);
+  if (!gemm_q4k_mfma_ok(w, x)) return M * K * sizeof(float);
+  const int split = gemm_q4k_split(M, N, K);
+  return split > 1 ? (size_t)split * M * N * sizeof(float) : 0;
 }
 
 hipError_t launch_gemm_q4k(const uint8_t* w, const uint16_t* x, float* y, size_t M, size_t N,
@@ -227,9 +265,21 @@ hipError_t launch_gemm_q4k(const uint8_t* w, const uint16_t* x, float* y, size_t
   if (M == 0 || N == 0) return hipSuccess;
   if (K % 256 != 0) return hipErrorInvalidValue;
   if (gemm_q4k_mfma_ok(w, x)) {
-    const dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM));
+    const int split = gemm_q4k_split(M, N, K);
+    const dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM), (unsigned)split);
     if (grid.y > 65535) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(gemm_q4k_mfma, grid, dim3(256), 0, s, w, x, y, (int)M, (int)N, (int)K);
+    if (split == 1) {
+      hipLaunchKernelGGL(gemm_q4k_mfma, grid, dim3(256), 0, s, w, x, y, (int)M, (int)N, (int)K);
+      return hipGetLastError();
+    }
+    if (workspace_bytes < (size_t)split * M * N * sizeof(float)) return hipErrorInvalidValue;
+    float* part = static_cast<float*>(workspace);
+    hipLaunchKernelGGL(gemm_q4k_mfma, grid, dim3(256), 0, s, w, x, part, (int)M, (int)N, (int)K);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const size_t mn = M * N;
+    const unsigned g = (unsigned)std::min<size_t>((mn + 255) / 256, 8192);
+    hipLaunchKernelGGL(splitk_reduce, dim3(g), dim3(256), 0, s, part, y, mn, split);
     return hipGetLastError();
   }
   // Misaligned operands: widen X to f32 (exact) and run the batched matvec,

@@ -254,6 +254,260 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
   }
 }
 
+// ------------------------------------------------------------------------
+// Paged INT8 decode attention on the matrix cores (QK) and the VALU (PV).
+//
+// One wavefront owns one split of one (sequence, KV head, chunk of up to 4
+// query heads); there are no workgroup barriers.  Per 64-token tile:
+//  * QK^T on v_mfma_i32_16x16x64_i8.  The A operand holds q as integer digit
+//    planes: q of head h is scaled by a power of two so |q| < 2^22, rounded,
+//    and written as three balanced base-256 signed digits; A row 4h+j is digit
+//    j of head h (row 4h+3 is zero).  The B operand is the K codes as stored
+//    (int8, head_dim contiguous per token), so each lane loads 16 contiguous
+//    bytes per MFMA.  With the MFMA output layout (lane l holds rows
+//    4*(l/16)..+3 of column l%16) every lane ends up with the three exact
+//    digit sums of one (head, token) pair: score = (I0 + 256 I1 + 65536 I2) *
+//    2^(e-22) * k_scale * 1/sqrt(head_dim).  The only rounding beyond the
+//    reference's is q's 23-bit rounding relative to its head's maximum.
+//  * online softmax per head inside each 16-lane row (DPP reductions).
+//  * PV on the VALU: p * v_scale goes through LDS to a lane layout where each
+//    lane owns head_dim/16 dimensions of one token per round; V codes (xor
+//    0x80, so v_cvt_f32_ubyte gives code + 128) are accumulated for all 4
+//    heads, and 128 * sum(p * v_scale) is subtracted at the end.
+// Partial records (m, l, acc[head_dim]) per split go to the combine kernel.
+constexpr int kAt = 64;  // tokens per tile
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+// max / sum over the 16 lanes of a DPP row, result in every lane of the row
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));
+  v = fmaxf(v, dpp_f<0x4E>(v));
+  v = fmaxf(v, dpp_f<0x124>(v));
+  return fmaxf(v, dpp_f<0x128>(v));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_f<0xB1>(v);
+  v += dpp_f<0x4E>(v);
+  v += dpp_f<0x124>(v);
+  return v + dpp_f<0x128>(v);
+}
+
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+template <int HD>
+__global__ __launch_bounds__(256, 2) void paged_attn_mfma_kernel(
+    const float* __restrict__ q, const int8_t* __restrict__ kc, const float* __restrict__ ks,
+    const int8_t* __restrict__ vc, const float* __restrict__ vs, const int32_t* __restrict__ tables,
+    const int32_t* __restrict__ ctx_lens, int max_blocks, int bs_log2, int n_head, int n_head_kv,
+    int n_hchunks, int split_len, int n_splits, float* __restrict__ partial) {
+  constexpr int NMI = HD / 64;  // MFMAs per 16-token sub-tile
+  constexpr int VD = HD / 16;   // dims per lane in the PV layout
+  constexpr int VW = VD / 4;    // V dwords per lane per round
+  __shared__ float p_s[4][kAt * 4];  // per wave: p * v_scale [token][head]
+  __shared__ int row_s[4][kAt];      // per wave: pool row of each token of the tile
+  __shared__ float ks_s[4][kAt], vs_s[4][kAt];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int split = blockIdx.x * 4 + wave;
+  if (split >= n_splits) return;  // no barriers follow: the wave can leave
+  const int hc = blockIdx.y % n_hchunks, kvh = blockIdx.y / n_hchunks, seq = blockIdx.z;
+  const int group = n_head / n_head_kv;
+  const int h0 = kvh * group + hc * 4;
+  const int G = min(4, group - hc * 4);
+  const int kv_dim = n_head_kv * HD;
+  const int32_t* table = tables + (size_t)seq * max_blocks;
+  const int p_end = min(ctx_lens[seq], max_blocks << bs_log2);
+  const int s_begin = split * split_len;
+  const int s_end = min(p_end, s_begin + split_len);
+  float* pw = p_s[wave];
+  int* rw = row_s[wave];
+  float* ksw = ks_s[wave];
+  float* vsw = vs_s[wave];
+
+  // ---- q digit planes (A operand): row r = lane%16 is digit r%4 of head r/4,
+  // lane group c = lane/16 holds dims 64*mi + 16c .. +16 of MFMA mi
+  const int r = lane & 15, c = lane >> 4;
+  i32x4 qa[NMI];
+  float qscale;  // 2^(e-22) of head c (the head of this lane's scores)
+  {
+    const int qh = r >> 2, qj = r & 3;
+    const bool hv = qh < G;
+    const float* qp = q + ((size_t)seq * n_head + h0 + (hv ? qh : 0)) * HD;
+    float qv[NMI][16];
+    float m = 0.f;
+    bool bad = false;
+#pragma unroll
+    for (int mi = 0; mi < NMI; mi++)
+#pragma unroll
+      for (int i = 0; i < 16; i += 4) {
+        const float4 f = hv ? *reinterpret_cast<const float4*>(qp + 64 * mi + 16 * c + i)
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
+        qv[mi][i] = f.x; qv[mi][i + 1] = f.y; qv[mi][i + 2] = f.z; qv[mi][i + 3] = f.w;
+      }
+#pragma unroll
+    for (int mi = 0; mi < NMI; mi++)
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        m = fmaxf(m, fabsf(qv[mi][i]));
+        bad |= !(fabsf(qv[mi][i]) < INFINITY);
+      }
+    m = fmaxf(m, __shfl_xor(m, 16, 64));  // same head, the other dims
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    int badi = bad ? 1 : 0;
+    badi |= __shfl_xor(badi, 16, 64);
+    badi |= __shfl_xor(badi, 32, 64);
+    int e = 0;
+    if (m > 0.f) (void)frexpf(m, &e);  // m < 2^e
+    const float up = ldexpf(1.0f, 22 - e);
+    const float qs_row = badi ? __builtin_nanf("") : ldexpf(1.0f, e - 22);
+#pragma unroll
+    for (int mi = 0; mi < NMI; mi++) {
+      uint32_t dw[4];
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        uint32_t acc = 0;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+          const int qi = (int)rintf(qv[mi][4 * k + b] * up);       // |qi| <= 2^22
+          const uint32_t u = ((uint32_t)(qi + 0x808080)) ^ 0x808080u;  // balanced digits
+          acc |= ((u >> (8 * (qj & 3))) & 0xFFu) << (8 * b);
+        }
+        dw[k] = (qj == 3 || !hv) ? 0u : acc;
+      }
+      qa[mi] = i32x4{(int)dw[0], (int)dw[1], (int)dw[2], (int)dw[3]};
+    }
+    qscale = __shfl(qs_row, 4 * c, 64);  // lane 4c holds digit 0 of head c
+  }
+  const float inv_sqrt = 1.0f / sqrtf((float)HD);
+  const int bs_mask = (1 << bs_log2) - 1;
+
+  float run_m = -INFINITY, run_l = 0.f;  // head c, replicated over the 16-lane row
+  const int tg = lane >> 4, dg = lane & 15;  // PV layout: token group, dimension group
+  float acc[4][VD];
+  float psum[4];
+#pragma unroll
+  for (int h = 0; h < 4; h++) {
+    psum[h] = 0.f;
+#pragma unroll
+    for (int d = 0; d < VD; d++) acc[h][d] = 0.f;
+  }
+
+  for (int t0 = s_begin; t0 < s_end; t0 += kAt) {
+    // pool rows and scales of the tile's tokens (clamped to the last valid one)
+    {
+      const int t = min(t0 + lane, s_end - 1);
+      const int row = table[t >> bs_log2] * (1 << bs_log2) + (t & bs_mask);
+      rw[lane] = row;
+      ksw[lane] = ks[row];
+      vsw[lane] = vs[row];
+    }
+    // K (B operand): token 16*sub + r, dims 64*mi + 16c .. +16
+    i32x4 kb[4][NMI];
+#pragma unroll
+    for (int sub = 0; sub < 4; sub++) {
+      const int8_t* kp = kc + (size_t)rw[16 * sub + r] * kv_dim + (size_t)kvh * HD + 16 * c;
+#pragma unroll
+      for (int mi = 0; mi < NMI; mi++) kb[sub][mi] = *reinterpret_cast<const i32x4*>(kp + 64 * mi);
+    }
+    // V (PV layout): round rr covers token 4*rr + tg, dims VD*dg .. +VD
+    uint32_t vraw[16][VW];
+#pragma unroll
+    for (int rr = 0; rr < 16; rr++) {
+      const int8_t* vp = vc + (size_t)rw[4 * rr + tg] * kv_dim + (size_t)kvh * HD + VD * dg;
+      if constexpr (VW == 1) {
+        vraw[rr][0] = *reinterpret_cast<const uint32_t*>(vp);
+      } else if constexpr (VW == 2) {
+        const uint2 v2 = *reinterpret_cast<const uint2*>(vp);
+        vraw[rr][0] = v2.x; vraw[rr][1] = v2.y;
+      } else {
+        const uint4 v4 = *reinterpret_cast<const uint4*>(vp);
+        vraw[rr][0] = v4.x; vraw[rr][1] = v4.y; vraw[rr][2] = v4.z; vraw[rr][3] = v4.w;
+      }
+    }
+    // scores of head c, tokens 16*sub + r
+    float sc[4];
+#pragma unroll
+    for (int sub = 0; sub < 4; sub++) {
+      i32x4 cacc = i32x4{0, 0, 0, 0};
+#pragma unroll
+      for (int mi = 0; mi < NMI; mi++)
+        cacc = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa[mi], kb[sub][mi], cacc, 0, 0, 0);
+      const float sv = fmaf(65536.0f, (float)cacc[2], (float)(cacc[0] + (cacc[1] << 8)));
+      const bool valid = (t0 + 16 * sub + r < s_end) && c < G;
+      sc[sub] = valid ? sv * qscale * ksw[16 * sub + r] * inv_sqrt : -INFINITY;
+    }
+    // online softmax of head c over the tile
+    const float tmax = row16_max(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
+    const float m_new = fmaxf(run_m, tmax);
+    float corr = 1.0f, p[4] = {0.f, 0.f, 0.f, 0.f};
+    if (m_new != -INFINITY) {
+      corr = __expf(run_m - m_new);
+#pragma unroll
+      for (int sub = 0; sub < 4; sub++) p[sub] = __expf(sc[sub] - m_new);
+    }
+    run_l = run_l * corr + row16_sum((p[0] + p[1]) + (p[2] + p[3]));
+    run_m = m_new;
+#pragma unroll
+    for (int sub = 0; sub < 4; sub++) pw[(16 * sub + r) * 4 + c] = p[sub] * vsw[16 * sub + r];
+    // rescale the PV accumulators by each head's correction
+#pragma unroll
+    for (int h = 0; h < 4; h++) {
+      const float ch = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, corr), 16 * h));
+      psum[h] *= ch;
+#pragma unroll
+      for (int d = 0; d < VD; d++) acc[h][d] *= ch;
+    }
+    // PV
+#pragma unroll
+    for (int rr = 0; rr < 16; rr++) {
+      const float4 pv = *reinterpret_cast<const float4*>(&pw[(4 * rr + tg) * 4]);
+      const float ph[4] = {pv.x, pv.y, pv.z, pv.w};
+      float f[VD];
+#pragma unroll
+      for (int w = 0; w < VW; w++) {
+        const uint32_t u = opaque(vraw[rr][w] ^ 0x80808080u);  // bytes = code + 128
+#pragma unroll
+        for (int b = 0; b < 4; b++) f[4 * w + b] = (float)byte_of(u, b);
+      }
+#pragma unroll
+      for (int h = 0; h < 4; h++) {
+        psum[h] += ph[h];
+#pragma unroll
+        for (int d = 0; d < VD; d++) acc[h][d] = fmaf(ph[h], f[d], acc[h][d]);
+      }
+    }
+  }
+
+  // remove the +128 code offset, sum the four token groups, write the split's records
+#pragma unroll
+  for (int h = 0; h < 4; h++)
+#pragma unroll
+    for (int d = 0; d < VD; d++) {
+      float a = fmaf(-128.0f, psum[h], acc[h][d]);
+      a += __shfl_xor(a, 16, 64);
+      a += __shfl_xor(a, 32, 64);
+      acc[h][d] = a;
+    }
+  if (tg == 0) {
+#pragma unroll
+    for (int h = 0; h < 4; h++) {
+      if (h < G) {
+        float* rec = partial + (((size_t)seq * n_head + h0 + h) * n_splits + split) * (HD + 2);
+#pragma unroll
+        for (int d = 0; d < VD; d++) rec[2 + VD * dg + d] = acc[h][d];
+      }
+    }
+  }
+  if (r == 0 && c < G) {
+    float* rec = partial + (((size_t)seq * n_head + h0 + c) * n_splits + split) * (HD + 2);
+    rec[0] = run_m;
+    rec[1] = run_l;
+  }
+}
+
 template <int HD>
 __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restrict__ partial,
                                                           int n_splits, int n_head,
@@ -301,18 +555,81 @@ hipError_t run_attn(const float* q, Src src, const int32_t* tables, const int32_
 
 }  // namespace
 
+namespace {
+
+int log2_exact(int v) {
+  if (v <= 0 || (v & (v - 1))) return -1;
+  int l = 0;
+  while ((1 << l) < v) l++;
+  return l;
+}
+
+// The matrix-core kernel needs a power-of-two block size and 16-byte aligned
+// q and code pools (16-byte K / q loads).
+bool paged_mfma_ok(const PagedAttnArgs& a) {
+  return log2_exact(a.block_size) >= 0 && ((uintptr_t)a.k_codes & 15) == 0 &&
+         ((uintptr_t)a.v_codes & 15) == 0 && ((uintptr_t)a.q & 15) == 0;
+}
+
+// Splits of the context for the matrix-core kernel: about 8 wavefronts per CU,
+// whole 64-token tiles.
+void paged_mfma_splits(const PagedAttnArgs& a, int* n_splits, int* split_len) {
+  const int group = a.n_head / a.n_head_kv;
+  const int units = a.n_seq * a.n_head_kv * ((group + 3) / 4);
+  const int target = device_cu_count() * 8;
+  const int want = std::max(1, (target + units - 1) / units);
+  int len = (a.max_ctx + want - 1) / want;
+  len = std::max(kAt, (len + kAt - 1) / kAt * kAt);
+  *split_len = len;
+  *n_splits = std::max(1, (a.max_ctx + len - 1) / len);
+}
+
+}  // namespace
+
 size_t paged_attn_workspace_bytes(const PagedAttnArgs& a, int* n_splits_out) {
-  const int n = pick_splits(a.n_seq * a.n_head_kv, a.max_ctx);
+  int n;
+  if (paged_mfma_ok(a)) {
+    int len;
+    paged_mfma_splits(a, &n, &len);
+  } else {
+    n = pick_splits(a.n_seq * a.n_head_kv, a.max_ctx);
+  }
   if (n_splits_out) *n_splits_out = n;
   return (size_t)a.n_seq * a.n_head * n * (a.head_dim + 2) * sizeof(float);
 }
 
+template <int HD>
+hipError_t run_paged_mfma(const PagedAttnArgs& a, float* part, hipStream_t s) {
+  int n_splits, split_len;
+  paged_mfma_splits(a, &n_splits, &split_len);
+  const int group = a.n_head / a.n_head_kv, n_hchunks = (group + 3) / 4;
+  const dim3 grid((unsigned)((n_splits + 3) / 4), (unsigned)(a.n_head_kv * n_hchunks), (unsigned)a.n_seq);
+  if (grid.y > 65535 || grid.z > 65535) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((paged_attn_mfma_kernel<HD>), grid, dim3(256), 0, s, a.q, a.k_codes,
+                     a.k_scales, a.v_codes, a.v_scales, a.block_tables, a.ctx_lens,
+                     a.max_blocks_per_seq, log2_exact(a.block_size), a.n_head, a.n_head_kv,
+                     n_hchunks, split_len, n_splits, part);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3(a.n_head, a.n_seq), dim3(HD), 0, s, part,
+                     n_splits, a.n_head, a.out);
+  return hipGetLastError();
+}
+
 hipError_t launch_paged_attn(const PagedAttnArgs& a, void* workspace, hipStream_t s) {
+  float* part = static_cast<float*>(workspace);
+  if (paged_mfma_ok(a)) {
+    switch (a.head_dim) {
+      case 64: return run_paged_mfma<64>(a, part, s);
+      case 128: return run_paged_mfma<128>(a, part, s);
+      case 256: return run_paged_mfma<256>(a, part, s);
+      default: return hipErrorInvalidValue;
+    }
+  }
   int n_splits = 0;
   paged_attn_workspace_bytes(a, &n_splits);
   PagedSrc src{a.k_codes, a.k_scales, a.v_codes, a.v_scales, nullptr, a.block_size,
                a.n_head_kv * a.head_dim};
-  float* part = static_cast<float*>(workspace);
   switch (a.head_dim) {
     case 64:
       return run_attn<64>(a.q, src, a.block_tables, a.ctx_lens, a.max_blocks_per_seq, a.n_seq,

@@ -298,7 +298,7 @@ __device__ __forceinline__ float row16_sum(float v) {
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
 template <int HD>
-__global__ __launch_bounds__(256, 2) void paged_attn_mfma_kernel(
+__global__ __launch_bounds__(256, HD == 256 ? 1 : 2) void paged_attn_mfma_kernel(
     const float* __restrict__ q, const int8_t* __restrict__ kc, const float* __restrict__ ks,
     const int8_t* __restrict__ vc, const float* __restrict__ vs, const int32_t* __restrict__ tables,
     const int32_t* __restrict__ ctx_lens, int max_blocks, int bs_log2, int n_head, int n_head_kv,
@@ -306,9 +306,9 @@ __global__ __launch_bounds__(256, 2) void paged_attn_mfma_kernel(
   constexpr int NMI = HD / 64;  // MFMAs per 16-token sub-tile
   constexpr int VD = HD / 16;   // dims per lane in the PV layout
   constexpr int VW = VD / 4;    // V dwords per lane per round
-  __shared__ float p_s[4][kAt * 4];  // per wave: p * v_scale [token][head]
-  __shared__ int row_s[4][kAt];      // per wave: pool row of each token of the tile
-  __shared__ float ks_s[4][kAt], vs_s[4][kAt];
+  __shared__ float p_s[4][kAt * 4];     // per wave: p * v_scale [token][head]
+  __shared__ int row_s[4][2 * kAt];     // per wave, two tiles: pool row of each token
+  __shared__ float ks_s[4][2 * kAt], vs_s[4][2 * kAt];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int split = blockIdx.x * 4 + wave;
@@ -395,37 +395,66 @@ __global__ __launch_bounds__(256, 2) void paged_attn_mfma_kernel(
     for (int d = 0; d < VD; d++) acc[h][d] = 0.f;
   }
 
-  for (int t0 = s_begin; t0 < s_end; t0 += kAt) {
-    // pool rows and scales of the tile's tokens (clamped to the last valid one)
-    {
-      const int t = min(t0 + lane, s_end - 1);
-      const int row = table[t >> bs_log2] * (1 << bs_log2) + (t & bs_mask);
-      rw[lane] = row;
-      ksw[lane] = ks[row];
-      vsw[lane] = vs[row];
-    }
-    // K (B operand): token 16*sub + r, dims 64*mi + 16c .. +16
-    i32x4 kb[4][NMI];
+  // Software pipeline over the split's tiles (two register / LDS slots):
+  // while tile i is computed, the K and V of tile i+1 and the block-table
+  // entries of tile i+2 are in flight.
+  const int n_tiles = s_end > s_begin ? (s_end - s_begin + kAt - 1) / kAt : 0;
+  auto tok_row = [&](int tab, int t) { return tab * (1 << bs_log2) + (t & bs_mask); };
+  auto tile_tok = [&](int i) { return min(s_begin + i * kAt + lane, s_end - 1); };
+  int tab_n = 0, row_n = 0;
+  float ks_n = 0.f, vs_n = 0.f;
+  i32x4 kb[2][4][NMI];
+  uint32_t vraw[2][16][VW];
+  auto issue_kv = [&](auto slot_c) {  // K and V of the tile whose rows sit in rw[slot]
+    constexpr int sl = decltype(slot_c)::value;
+    const int* rws = rw + sl * kAt;
 #pragma unroll
     for (int sub = 0; sub < 4; sub++) {
-      const int8_t* kp = kc + (size_t)rw[16 * sub + r] * kv_dim + (size_t)kvh * HD + 16 * c;
+      const int8_t* kp = kc + (size_t)rws[16 * sub + r] * kv_dim + (size_t)kvh * HD + 16 * c;
 #pragma unroll
-      for (int mi = 0; mi < NMI; mi++) kb[sub][mi] = *reinterpret_cast<const i32x4*>(kp + 64 * mi);
+      for (int mi = 0; mi < NMI; mi++) kb[sl][sub][mi] = *reinterpret_cast<const i32x4*>(kp + 64 * mi);
     }
-    // V (PV layout): round rr covers token 4*rr + tg, dims VD*dg .. +VD
-    uint32_t vraw[16][VW];
 #pragma unroll
     for (int rr = 0; rr < 16; rr++) {
-      const int8_t* vp = vc + (size_t)rw[4 * rr + tg] * kv_dim + (size_t)kvh * HD + VD * dg;
+      const int8_t* vp = vc + (size_t)rws[4 * rr + tg] * kv_dim + (size_t)kvh * HD + VD * dg;
       if constexpr (VW == 1) {
-        vraw[rr][0] = *reinterpret_cast<const uint32_t*>(vp);
+        vraw[sl][rr][0] = *reinterpret_cast<const uint32_t*>(vp);
       } else if constexpr (VW == 2) {
         const uint2 v2 = *reinterpret_cast<const uint2*>(vp);
-        vraw[rr][0] = v2.x; vraw[rr][1] = v2.y;
+        vraw[sl][rr][0] = v2.x; vraw[sl][rr][1] = v2.y;
       } else {
         const uint4 v4 = *reinterpret_cast<const uint4*>(vp);
-        vraw[rr][0] = v4.x; vraw[rr][1] = v4.y; vraw[rr][2] = v4.z; vraw[rr][3] = v4.w;
+        vraw[sl][rr][0] = v4.x; vraw[sl][rr][1] = v4.y; vraw[sl][rr][2] = v4.z; vraw[sl][rr][3] = v4.w;
       }
+    }
+  };
+  if (n_tiles > 0) {  // prologue: rows and K / V of tile 0, table entry of tile 1
+    const int t = tile_tok(0);
+    row_n = tok_row(table[t >> bs_log2], t);
+    rw[lane] = row_n;
+    ks_n = ks[row_n];
+    vs_n = vs[row_n];
+    const int t1 = tile_tok(1);
+    tab_n = table[t1 >> bs_log2];
+    issue_kv(std::integral_constant<int, 0>{});
+  }
+
+  auto tile = [&](auto slot_c, int i) {
+    constexpr int sl = decltype(slot_c)::value;
+    const int t0 = s_begin + i * kAt;
+    float* ksl = ksw + sl * kAt;
+    float* vsl = vsw + sl * kAt;
+    ksl[lane] = ks_n;  // scales of tile i (loaded one iteration ago)
+    vsl[lane] = vs_n;
+    {  // rows of tile i+1, their scales, the table entry of tile i+2, then K and V of tile i+1
+      const int t = tile_tok(i + 1);
+      row_n = tok_row(tab_n, t);
+      rw[(sl ^ 1) * kAt + lane] = row_n;
+      ks_n = ks[row_n];
+      vs_n = vs[row_n];
+      const int t2 = tile_tok(i + 2);
+      tab_n = table[t2 >> bs_log2];
+      issue_kv(std::integral_constant<int, sl ^ 1>{});
     }
     // scores of head c, tokens 16*sub + r
     float sc[4];
@@ -434,10 +463,10 @@ __global__ __launch_bounds__(256, 2) void paged_attn_mfma_kernel(
       i32x4 cacc = i32x4{0, 0, 0, 0};
 #pragma unroll
       for (int mi = 0; mi < NMI; mi++)
-        cacc = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa[mi], kb[sub][mi], cacc, 0, 0, 0);
+        cacc = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa[mi], kb[sl][sub][mi], cacc, 0, 0, 0);
       const float sv = fmaf(65536.0f, (float)cacc[2], (float)(cacc[0] + (cacc[1] << 8)));
       const bool valid = (t0 + 16 * sub + r < s_end) && c < G;
-      sc[sub] = valid ? sv * qscale * ksw[16 * sub + r] * inv_sqrt : -INFINITY;
+      sc[sub] = valid ? sv * qscale * ksl[16 * sub + r] * inv_sqrt : -INFINITY;
     }
     // online softmax of head c over the tile
     const float tmax = row16_max(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
@@ -451,7 +480,7 @@ __global__ __launch_bounds__(256, 2) void paged_attn_mfma_kernel(
     run_l = run_l * corr + row16_sum((p[0] + p[1]) + (p[2] + p[3]));
     run_m = m_new;
 #pragma unroll
-    for (int sub = 0; sub < 4; sub++) pw[(16 * sub + r) * 4 + c] = p[sub] * vsw[16 * sub + r];
+    for (int sub = 0; sub < 4; sub++) pw[(16 * sub + r) * 4 + c] = p[sub] * vsl[16 * sub + r];
     // rescale the PV accumulators by each head's correction
 #pragma unroll
     for (int h = 0; h < 4; h++) {
@@ -468,7 +497,7 @@ __global__ __launch_bounds__(256, 2) void paged_attn_mfma_kernel(
       float f[VD];
 #pragma unroll
       for (int w = 0; w < VW; w++) {
-        const uint32_t u = opaque(vraw[rr][w] ^ 0x80808080u);  // bytes = code + 128
+        const uint32_t u = opaque(vraw[sl][rr][w] ^ 0x80808080u);  // bytes = code + 128
 #pragma unroll
         for (int b = 0; b < 4; b++) f[4 * w + b] = (float)byte_of(u, b);
       }
@@ -479,6 +508,10 @@ __global__ __launch_bounds__(256, 2) void paged_attn_mfma_kernel(
         for (int d = 0; d < VD; d++) acc[h][d] = fmaf(ph[h], f[d], acc[h][d]);
       }
     }
+  };
+  for (int i = 0; i < n_tiles; i += 2) {
+    tile(std::integral_constant<int, 0>{}, i);
+    if (i + 1 < n_tiles) tile(std::integral_constant<int, 1>{}, i + 1);
   }
 
   // remove the +128 code offset, sum the four token groups, write the split's records
@@ -508,25 +541,54 @@ __global__ __launch_bounds__(256, 2) void paged_attn_mfma_kernel(
   }
 }
 
+// Log-sum-exp merge of the split partials of one (sequence, head): the split
+// maxima and weights are reduced once in LDS, then every thread sums its
+// dimension over the splits with independent loads.
+constexpr int kMaxSplits = 1024;
+
 template <int HD>
-__global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restrict__ partial,
-                                                          int n_splits, int n_head,
-                                                          float* __restrict__ out) {
-  const int h = blockIdx.x, seq = blockIdx.y, d = threadIdx.x;
+__global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ partial,
+                                                           int n_splits, int n_head,
+                                                           float* __restrict__ out) {
+  __shared__ float w_s[kMaxSplits];
+  __shared__ float red[256 / 64];
+  const int h = blockIdx.x, seq = blockIdx.y, tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
   const float* rec = partial + ((size_t)seq * n_head + h) * n_splits * (HD + 2);
-  float M = -INFINITY;
-  for (int s = 0; s < n_splits; s++) M = fmaxf(M, rec[(size_t)s * (HD + 2)]);
-  float l = 0.f, a = 0.f;
-  if (M != -INFINITY) {
-    for (int s = 0; s < n_splits; s++) {
-      const float* r = rec + (size_t)s * (HD + 2);
-      if (r[0] == -INFINITY) continue;
-      const float w = __expf(r[0] - M);
-      l = fmaf(w, r[1], l);
-      a = fmaf(w, r[2 + d], a);
-    }
+  // 1. global maximum of the split maxima
+  float m = -INFINITY;
+  for (int s = tid; s < n_splits; s += 256) m = fmaxf(m, rec[(size_t)s * (HD + 2)]);
+  m = wave_max(m);
+  if (lane == 0) red[wave] = m;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  // 2. split weights exp(m_s - M) and the total l
+  float l = 0.f;
+  for (int s = tid; s < n_splits; s += 256) {
+    const float ms = rec[(size_t)s * (HD + 2)];
+    const float w = (M == -INFINITY || ms == -INFINITY) ? 0.f : __expf(ms - M);
+    w_s[s] = w;
+    l = fmaf(w, rec[(size_t)s * (HD + 2) + 1], l);
   }
-  out[((size_t)seq * n_head + h) * HD + d] = l > 0.f ? a * (1.0f / l) : 0.f;
+  l = wave_sum(l);
+  if (lane == 0) red[wave] = l;
+  __syncthreads();
+  const float L = (red[0] + red[1]) + (red[2] + red[3]);
+  // 3. out[d] = sum_s w_s acc_s[d] / L
+  for (int d = tid; d < HD; d += 256) {
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    int s = 0;
+    for (; s + 4 <= n_splits; s += 4) {
+      a0 = fmaf(w_s[s], rec[(size_t)s * (HD + 2) + 2 + d], a0);
+      a1 = fmaf(w_s[s + 1], rec[(size_t)(s + 1) * (HD + 2) + 2 + d], a1);
+      a2 = fmaf(w_s[s + 2], rec[(size_t)(s + 2) * (HD + 2) + 2 + d], a2);
+      a3 = fmaf(w_s[s + 3], rec[(size_t)(s + 3) * (HD + 2) + 2 + d], a3);
+    }
+    for (; s < n_splits; s++) a0 = fmaf(w_s[s], rec[(size_t)s * (HD + 2) + 2 + d], a0);
+    const float a = (a0 + a1) + (a2 + a3);
+    out[((size_t)seq * n_head + h) * HD + d] = L > 0.f ? a * (1.0f / L) : 0.f;
+  }
 }
 
 int pick_splits(int units, int max_len) {
@@ -534,7 +596,7 @@ int pick_splits(int units, int max_len) {
   const int target = device_cu_count() * 4;
   int splits = std::max(1, (target + units - 1) / units);
   const int max_splits = std::max(1, (max_len + kTile - 1) / kTile);
-  return std::min(splits, max_splits);
+  return std::min(std::min(splits, max_splits), kMaxSplits);
 }
 
 template <int HD, class Src>
@@ -548,7 +610,7 @@ hipError_t run_attn(const float* q, Src src, const int32_t* tables, const int32_
                      pe, split_len, n_splits, partial);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3(n_head, n_seq), dim3(HD), 0, s, partial,
+  hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3(n_head, n_seq), dim3(256), 0, s, partial,
                      n_splits, n_head, out);
   return hipGetLastError();
 }
@@ -580,6 +642,8 @@ void paged_mfma_splits(const PagedAttnArgs& a, int* n_splits, int* split_len) {
   const int want = std::max(1, (target + units - 1) / units);
   int len = (a.max_ctx + want - 1) / want;
   len = std::max(kAt, (len + kAt - 1) / kAt * kAt);
+  len = std::max(len, (a.max_ctx + kMaxSplits - 1) / kMaxSplits);
+  len = (len + kAt - 1) / kAt * kAt;
   *split_len = len;
   *n_splits = std::max(1, (a.max_ctx + len - 1) / len);
 }
@@ -611,7 +675,7 @@ hipError_t run_paged_mfma(const PagedAttnArgs& a, float* part, hipStream_t s) {
                      n_hchunks, split_len, n_splits, part);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3(a.n_head, a.n_seq), dim3(HD), 0, s, part,
+  hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3(a.n_head, a.n_seq), dim3(256), 0, s, part,
                      n_splits, a.n_head, a.out);
   return hipGetLastError();
 }

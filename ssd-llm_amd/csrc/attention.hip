@@ -271,9 +271,9 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
 //    reference's is q's 23-bit rounding relative to its head's maximum.
 //  * online softmax per head inside each 16-lane row (DPP reductions).
 //  * PV on the VALU: p * v_scale goes through LDS to a lane layout where each
-//    lane owns head_dim/16 dimensions of one token per round; V codes (xor
-//    0x80, so v_cvt_f32_ubyte gives code + 128) are accumulated for all 4
-//    heads, and 128 * sum(p * v_scale) is subtracted at the end.
+//    lane owns head_dim/16 dimensions of one token per round; each V code is
+//    converted once (v_cvt_f32_i32 of a sign-extended byte) and accumulated
+//    for all 4 heads.
 // Partial records (m, l, acc[head_dim]) per split go to the combine kernel.
 constexpr int kAt = 64;  // tokens per tile
 
@@ -387,13 +387,10 @@ __global__ __launch_bounds__(256, HD == 256 ? 1 : 2) void paged_attn_mfma_kernel
   float run_m = -INFINITY, run_l = 0.f;  // head c, replicated over the 16-lane row
   const int tg = lane >> 4, dg = lane & 15;  // PV layout: token group, dimension group
   float acc[4][VD];
-  float psum[4];
 #pragma unroll
-  for (int h = 0; h < 4; h++) {
-    psum[h] = 0.f;
+  for (int h = 0; h < 4; h++)
 #pragma unroll
     for (int d = 0; d < VD; d++) acc[h][d] = 0.f;
-  }
 
   // Software pipeline over the split's tiles (two register / LDS slots):
   // while tile i is computed, the K and V of tile i+1 and the block-table
@@ -485,7 +482,6 @@ __global__ __launch_bounds__(256, HD == 256 ? 1 : 2) void paged_attn_mfma_kernel
 #pragma unroll
     for (int h = 0; h < 4; h++) {
       const float ch = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, corr), 16 * h));
-      psum[h] *= ch;
 #pragma unroll
       for (int d = 0; d < VD; d++) acc[h][d] *= ch;
     }
@@ -496,17 +492,14 @@ __global__ __launch_bounds__(256, HD == 256 ? 1 : 2) void paged_attn_mfma_kernel
       const float ph[4] = {pv.x, pv.y, pv.z, pv.w};
       float f[VD];
 #pragma unroll
-      for (int w = 0; w < VW; w++) {
-        const uint32_t u = opaque(vraw[sl][rr][w] ^ 0x80808080u);  // bytes = code + 128
+      for (int w = 0; w < VW; w++)
 #pragma unroll
-        for (int b = 0; b < 4; b++) f[4 * w + b] = (float)byte_of(u, b);
-      }
+        for (int b = 0; b < 4; b++)  // one v_cvt_f32_i32 with a sign-extended byte select
+          f[4 * w + b] = (float)(int8_t)(vraw[sl][rr][w] >> (8 * b));
 #pragma unroll
-      for (int h = 0; h < 4; h++) {
-        psum[h] += ph[h];
+      for (int h = 0; h < 4; h++)
 #pragma unroll
         for (int d = 0; d < VD; d++) acc[h][d] = fmaf(ph[h], f[d], acc[h][d]);
-      }
     }
   };
   for (int i = 0; i < n_tiles; i += 2) {
@@ -514,12 +507,12 @@ __global__ __launch_bounds__(256, HD == 256 ? 1 : 2) void paged_attn_mfma_kernel
     if (i + 1 < n_tiles) tile(std::integral_constant<int, 1>{}, i + 1);
   }
 
-  // remove the +128 code offset, sum the four token groups, write the split's records
+  // sum the four token groups, write the split's records
 #pragma unroll
   for (int h = 0; h < 4; h++)
 #pragma unroll
     for (int d = 0; d < VD; d++) {
-      float a = fmaf(-128.0f, psum[h], acc[h][d]);
+      float a = acc[h][d];
       a += __shfl_xor(a, 16, 64);
       a += __shfl_xor(a, 32, 64);
       acc[h][d] = a;

@@ -89,7 +89,8 @@ def test_misaligned_weights_take_generic_path(dtype):
 
 ODD = [
     (Q4_0, 1, 32, 1), (Q4_0, 3, 96, 2), (Q4_0, 257, 4096 + 17, 3), (Q4_0, 70, 32 * 9, 1),
-    (Q8_0, 5, 64, 5), (Q8_0, 129, 32 * 7, 7), (Q8_0, 64, 8192, 16),
+    (Q8_0, 5, 64, 5), (Q8_0, 129, 32 * 7, 7), (Q8_0, 64, 8192, 16), (Q8_0, 1000, 32 * 12, 6),
+    (Q8_0, 17, 32 * 64, 21),
     (Q4_K, 1, 256, 1), (Q4_K, 33, 256 * 3, 6), (Q4_K, 200, 256 * 40 + 100, 2), (Q4_K, 64, 4096, 9),
     (Q6_K, 2, 256, 1), (Q6_K, 31, 256 * 5, 3), (Q6_K, 100, 256 * 7, 8),
 ]

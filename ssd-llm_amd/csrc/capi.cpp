@@ -63,6 +63,11 @@ hipError_t workspace_get(size_t bytes, hipStream_t stream, void** out) {
   std::lock_guard<std::mutex> lk(g_ws_mu);
   Workspace& w = g_ws[{dev, (void*)stream}];
   if (w.bytes < bytes) {
+    // No allocation while the stream is being captured into a graph (it would
+    // invalidate the capture): run the call once on this stream beforehand.
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (stream && hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+      return hipErrorStreamCaptureUnsupported;
     if (w.ptr) {
       e = hipStreamSynchronize(stream);
       if (e != hipSuccess) return e;
@@ -242,10 +247,15 @@ static int matvec_common(int dtype, const void* w, const float* x, float* y, siz
   if (keff > 0 && (!w || !x)) return fail(SSDQ_ERR_INVALID_ARG, "%s: w or x is NULL", fn);
   if (((uintptr_t)x & 3) || ((uintptr_t)y & 3))
     return fail(SSDQ_ERR_INVALID_ARG, "%s: x and y must be 4-byte aligned", fn);
-  hipError_t e = generic ? ssdq::launch_matvec_generic(dtype, (const uint8_t*)w, x, y, out_dim,
-                                                       in_dim, batch, s)
-                         : ssdq::launch_matvec(dtype, (const uint8_t*)w, x, y, out_dim, in_dim,
-                                               batch, s);
+  hipError_t e = hipSuccess;
+  if (generic) {
+    e = ssdq::launch_matvec_generic(dtype, (const uint8_t*)w, x, y, out_dim, in_dim, batch, s);
+  } else {
+    const size_t wsb = ssdq::matvec_workspace_bytes(dtype, w, x, out_dim, in_dim, batch);
+    void* ws = nullptr;
+    if (wsb && (e = workspace_get(wsb, s, &ws)) != hipSuccess) return hip_fail(e, "ssdq_matvec_dev: workspace");
+    e = ssdq::launch_matvec(dtype, (const uint8_t*)w, x, y, out_dim, in_dim, batch, s, ws, wsb);
+  }
   if (e != hipSuccess) return hip_fail(e, fn);
   return ok();
 }

@@ -16,7 +16,11 @@ hipError_t launch_dequant(int dtype, const uint8_t* w, size_t n_blocks, float* o
 // y[b*out_dim + r] = sum_k W[r,k] * x[b*in_dim + k], b < batch, over the
 // whole blocks of each row (k < (in_dim / block) * block).
 hipError_t launch_matvec(int dtype, const uint8_t* w, const float* x, float* y, size_t out_dim,
-                         size_t in_dim, size_t batch, hipStream_t stream);
+                         size_t in_dim, size_t batch, hipStream_t stream, void* workspace = nullptr,
+                         size_t workspace_bytes = 0);
+// Device workspace launch_matvec uses for these operands (batch-1 K slices).
+size_t matvec_workspace_bytes(int dtype, const void* w, const float* x, size_t out_dim,
+                              size_t in_dim, size_t batch);
 // Same, forcing the byte-addressed fallback kernel (used by tests to cover it).
 hipError_t launch_matvec_generic(int dtype, const uint8_t* w, const float* x, float* y,
                                  size_t out_dim, size_t in_dim, size_t batch, hipStream_t stream);

@@ -503,22 +503,32 @@ template <int F> constexpr int loads_per_unit() { return (F == kQ4_K || F == kQ4
 //      straight-line code with clamped addresses, so the compiler's in-order
 //      wait counts stay exact, and the cross-lane sums of all rows are taken
 //      together at the end.
+//
+// Long rows are cut into K slices (blockIdx.y; slice_bpr blocks each, the last
+// one may be shorter): every workgroup stages only its slice of x, and slice z
+// writes its partial dot products to y + z * out_dim, summed by
+// slice_reduce_kernel in slice order.
 template <int F, int UPL, int RMAX, bool FULL, int SIT>
 __global__ __launch_bounds__(768) void mv_b1(const uint8_t* __restrict__ w,
                                              const float* __restrict__ x, float* __restrict__ y,
-                                             int out_dim, int bpr, int ks) {
+                                             int out_dim, int row_bpr, int slice_bpr, int ks) {
   using FU = FastUnit<F>;
   using D = Dig<F>;
   constexpr int NW = FU::NW, US = D::US;
   static_assert(US % 4 == 0, "unit records are read as 16-byte vectors");
   extern __shared__ uint4 lds4[];
   uint32_t* lds = reinterpret_cast<uint32_t*>(lds4);
+  const int blk0 = blockIdx.y * slice_bpr;
+  const int bpr = min(slice_bpr, row_bpr - blk0);  // blocks of this slice
+  w += (size_t)blk0 * Geom<F>::bb;
+  x += (size_t)blk0 * Geom<F>::bs;
+  y += (size_t)blockIdx.y * out_dim;
   const int keff = bpr * Geom<F>::bs;
   const int U = keff / FU::E;
   float* red = reinterpret_cast<float*>(lds + (size_t)U * US);  // [RMAX][ks]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nw = blockDim.x >> 6, kw = wave % ks, stream = wave / ks, rs = nw / ks;
-  const size_t row_bytes = (size_t)bpr * Geom<F>::bb;
+  const size_t row_bytes = (size_t)row_bpr * Geom<F>::bb;
   const long n_streams = (long)gridDim.x * rs, gs = (long)blockIdx.x * rs + stream;
   const int r_begin = (int)(gs * out_dim / n_streams);
   const int n_rows = (int)((gs + 1) * out_dim / n_streams) - r_begin;  // <= RMAX
@@ -594,6 +604,16 @@ __global__ __launch_bounds__(768) void mv_b1(const uint8_t* __restrict__ w,
       y[r_begin + lane] = s;
     }
   }
+}
+
+__global__ __launch_bounds__(256) void slice_reduce_kernel(const float* __restrict__ part,
+                                                           float* __restrict__ y, int n,
+                                                           int slices) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float s = part[i];
+  for (int z = 1; z < slices; z++) s += part[(size_t)z * n + i];
+  y[i] = s;
 }
 
 // ------------------------------------------------------ batched (B > 1) path
@@ -821,23 +841,25 @@ void row_split(int out_dim, int quantum, int target, int* n_wg, int* rows_per_wg
 }
 
 template <int F, int UPL, int RMAX, bool FULL, int SIT>
-hipError_t run_b1_sit(const uint8_t* w, const float* x, float* y, int out_dim, int bpr, int ks,
-                      int rs, size_t lds, hipStream_t s) {
+hipError_t run_b1_sit(const uint8_t* w, const float* x, float* y, int out_dim, int row_bpr,
+                      int slice_bpr, int slices, int ks, int rs, size_t lds, hipStream_t s) {
   auto kern = mv_b1<F, UPL, RMAX, FULL, SIT>;
   hipError_t e = set_lds_attr(kern, lds);
   if (e != hipSuccess) return e;
   const int threads = 64 * ks * rs;
   const long streams_needed = (out_dim + RMAX - 1) / RMAX;
-  long n_wg = std::max<long>(device_cu_count(), (streams_needed + rs - 1) / rs);
+  // about one workgroup per CU over all slices
+  long n_wg = std::max<long>((device_cu_count() + slices - 1) / slices, (streams_needed + rs - 1) / rs);
   n_wg = std::max<long>(1, std::min<long>(n_wg, (out_dim + rs - 1) / rs));
-  hipLaunchKernelGGL(kern, dim3((unsigned)n_wg), dim3(threads), lds, s, w, x, y, out_dim, bpr, ks);
+  hipLaunchKernelGGL(kern, dim3((unsigned)n_wg, (unsigned)slices), dim3(threads), lds, s, w, x, y,
+                     out_dim, row_bpr, slice_bpr, ks);
   return hipGetLastError();
 }
 
 template <int F, int UPL, int RMAX, bool FULL>
-hipError_t run_b1(const uint8_t* w, const float* x, float* y, int out_dim, int bpr, int ks,
-                  hipStream_t s) {
-  const int U = bpr * Geom<F>::bs / FastUnit<F>::E;
+hipError_t run_b1(const uint8_t* w, const float* x, float* y, int out_dim, int row_bpr,
+                  int slice_bpr, int slices, int ks, hipStream_t s) {
+  const int U = slice_bpr * Geom<F>::bs / FastUnit<F>::E;
   const size_t lds = ((size_t)U * Dig<F>::US + (size_t)RMAX * ks) * sizeof(uint32_t);
   if (lds > (size_t)lds_limit()) return hipErrorInvalidValue;
   // One workgroup per CU holding as many waves as fit (ks waves per row
@@ -872,14 +894,14 @@ hipError_t run_b1(const uint8_t* w, const float* x, float* y, int out_dim, int b
     rs_cache[key] = rs;
   }
   const int threads = 64 * ks * rs;
-  const int nchunk = bpr * Geom<F>::bs / 8;
+  const int nchunk = slice_bpr * Geom<F>::bs / 8;
   const int sit = (nchunk + threads - 1) / threads;
   switch (sit) {
     case 0:
-    case 1: return run_b1_sit<F, UPL, RMAX, FULL, 1>(w, x, y, out_dim, bpr, ks, rs, lds, s);
-    case 2: return run_b1_sit<F, UPL, RMAX, FULL, 2>(w, x, y, out_dim, bpr, ks, rs, lds, s);
+    case 1: return run_b1_sit<F, UPL, RMAX, FULL, 1>(w, x, y, out_dim, row_bpr, slice_bpr, slices, ks, rs, lds, s);
+    case 2: return run_b1_sit<F, UPL, RMAX, FULL, 2>(w, x, y, out_dim, row_bpr, slice_bpr, slices, ks, rs, lds, s);
     case 3:
-    case 4: return run_b1_sit<F, UPL, RMAX, FULL, 4>(w, x, y, out_dim, bpr, ks, rs, lds, s);
+    case 4: return run_b1_sit<F, UPL, RMAX, FULL, 4>(w, x, y, out_dim, row_bpr, slice_bpr, slices, ks, rs, lds, s);
     default: return hipErrorNotSupported;  // x too long to stage
   }
 }
@@ -904,47 +926,81 @@ bool fast_aligned(const uint8_t* w, const float* x, int in_dim, int bpr) {
   else return (a & 3u) == 0 && (bpr % 2) == 0;  // Q4_0 / Q8_0 pairs, Q6_K dword rows
 }
 
+// Row geometry of the batch-1 kernel: rows of up to 128 units run whole (one
+// wave per row stream); longer rows are cut into slices of at most 64 units.
+template <int F>
+struct B1Plan {
+  int upl = 1, slice_bpr = 0, slices = 1;
+  bool full = true;
+};
+
+template <int F>
+B1Plan<F> b1_plan(int bpr) {
+  const int U = bpr * Geom<F>::bs / FastUnit<F>::E;
+  B1Plan<F> p;
+  if (U <= 128) {
+    p.upl = U <= 64 ? 1 : 2;
+    p.slice_bpr = bpr;
+    p.full = (U == p.upl * 64);
+    return p;
+  }
+  p.slices = (U + 63) / 64;
+  int sb;
+  if constexpr (Geom<F>::bs == 32) {  // Q4_0 / Q8_0: two blocks per unit
+    sb = (bpr + p.slices - 1) / p.slices;
+    sb += sb & 1;
+  } else {
+    sb = (bpr + p.slices - 1) / p.slices;
+  }
+  p.slice_bpr = sb;
+  p.slices = (bpr + sb - 1) / sb;
+  p.full = (bpr % sb == 0) && sb * Geom<F>::bs / FastUnit<F>::E == 64;
+  return p;
+}
+
+template <int F>
+size_t b1_workspace_floats(int out_dim, int bpr) {
+  const B1Plan<F> p = b1_plan<F>(bpr);
+  return p.slices > 1 ? (size_t)p.slices * out_dim : 0;
+}
+
 template <int F>
 hipError_t b1_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, int bpr,
-                       hipStream_t s, bool* used) {
+                       hipStream_t s, float* ws, size_t ws_floats, bool* used) {
   const int U = bpr * Geom<F>::bs / FastUnit<F>::E;
   if (U == 0) return hipSuccess;
-  int ks, upl;
-  if (U <= 128) {
-    ks = 1;
-    upl = U <= 64 ? 1 : 2;
-  } else if (U <= 512) {
-    ks = (U + 63) / 64;
-    upl = 1;
-  } else {
-    return hipSuccess;  // long rows: batched LDS kernel
-  }
-  const bool full = (U == ks * upl * 64);
+  const B1Plan<F> p = b1_plan<F>(bpr);
+  if (p.slices > 1 && (!ws || ws_floats < (size_t)p.slices * out_dim)) return hipSuccess;
+  float* dst = p.slices > 1 ? ws : y;
   *used = true;
   hipError_t e;
-  if (upl == 1)
-    e = full ? run_b1<F, 1, 5, true>(w, x, y, out_dim, bpr, ks, s)
-             : run_b1<F, 1, 5, false>(w, x, y, out_dim, bpr, ks, s);
+  if (p.upl == 1)
+    e = p.full ? run_b1<F, 1, 5, true>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s)
+               : run_b1<F, 1, 5, false>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s);
   else
-    e = full ? run_b1<F, 2, 3, true>(w, x, y, out_dim, bpr, ks, s)
-             : run_b1<F, 2, 3, false>(w, x, y, out_dim, bpr, ks, s);
+    e = p.full ? run_b1<F, 2, 3, true>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s)
+               : run_b1<F, 2, 3, false>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s);
   if (e == hipErrorNotSupported) {  // not launched: the caller takes the batched path
     *used = false;
     return hipSuccess;
   }
-  return e;
+  if (e != hipSuccess || p.slices == 1) return e;
+  hipLaunchKernelGGL(slice_reduce_kernel, dim3((unsigned)((out_dim + 255) / 256)), dim3(256), 0, s,
+                     ws, y, out_dim, p.slices);
+  return hipGetLastError();
 }
 
 template <int F>
 hipError_t fast_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, int in_dim,
-                         int bpr, int batch, hipStream_t s, bool* used) {
+                         int bpr, int batch, hipStream_t s, float* ws, size_t ws_floats,
+                         bool* used) {
   *used = false;
   if (!fast_aligned<F>(w, x, in_dim, bpr)) return hipSuccess;
   const int keff = bpr * Geom<F>::bs;
   const int U = keff / FastUnit<F>::E;
   const int limit = lds_limit();
   if (batch == 1) {
-    hipError_t e = b1_dispatch<F>(w, x, y, out_dim, bpr, s, used);
+    hipError_t e = b1_dispatch<F>(w, x, y, out_dim, bpr, s, ws, ws_floats, used);
     if (e != hipSuccess || *used) return e;
   }
   if constexpr (F == kQ8_0) {
@@ -993,17 +1049,36 @@ hipError_t launch_matvec_generic(int dtype, const uint8_t* w, const float* x, fl
   }
 }
 
+size_t matvec_workspace_bytes(int dtype, const void* w, const float* x, size_t out_dim,
+                              size_t in_dim, size_t batch) {
+  if (batch != 1 || out_dim == 0) return 0;
+  const uint8_t* wb = (const uint8_t*)w;
+  const int od = (int)out_dim, id = (int)in_dim;
+  size_t n = 0;
+  switch (dtype) {
+    case kQ4_0: if (fast_aligned<kQ4_0>(wb, x, id, id / 32)) n = b1_workspace_floats<kQ4_0>(od, id / 32); break;
+    case kQ8_0: if (fast_aligned<kQ8_0>(wb, x, id, id / 32)) n = b1_workspace_floats<kQ8_0>(od, id / 32); break;
+    case kQ4_K: if (fast_aligned<kQ4_K>(wb, x, id, id / 256)) n = b1_workspace_floats<kQ4_K>(od, id / 256); break;
+    case kQ6_K: if (fast_aligned<kQ6_K>(wb, x, id, id / 256)) n = b1_workspace_floats<kQ6_K>(od, id / 256); break;
+    default: break;
+  }
+  return n * sizeof(float);
+}
+
 hipError_t launch_matvec(int dtype, const uint8_t* w, const float* x, float* y, size_t out_dim,
-                         size_t in_dim, size_t batch, hipStream_t s) {
+                         size_t in_dim, size_t batch, hipStream_t s, void* workspace,
+                         size_t workspace_bytes) {
   if (out_dim == 0 || batch == 0) return hipSuccess;
   bool used = false;
   hipError_t e = hipSuccess;
   const int od = (int)out_dim, id = (int)in_dim, b = (int)batch;
+  float* ws = static_cast<float*>(workspace);
+  const size_t wf = workspace_bytes / sizeof(float);
   switch (dtype) {
-    case kQ4_0: e = fast_dispatch<kQ4_0>(w, x, y, od, id, id / 32, b, s, &used); break;
-    case kQ8_0: e = fast_dispatch<kQ8_0>(w, x, y, od, id, id / 32, b, s, &used); break;
-    case kQ4_K: e = fast_dispatch<kQ4_K>(w, x, y, od, id, id / 256, b, s, &used); break;
-    case kQ6_K: e = fast_dispatch<kQ6_K>(w, x, y, od, id, id / 256, b, s, &used); break;
+    case kQ4_0: e = fast_dispatch<kQ4_0>(w, x, y, od, id, id / 32, b, s, ws, wf, &used); break;
+    case kQ8_0: e = fast_dispatch<kQ8_0>(w, x, y, od, id, id / 32, b, s, ws, wf, &used); break;
+    case kQ4_K: e = fast_dispatch<kQ4_K>(w, x, y, od, id, id / 256, b, s, ws, wf, &used); break;
+    case kQ6_K: e = fast_dispatch<kQ6_K>(w, x, y, od, id, id / 256, b, s, ws, wf, &used); break;
     default: return hipErrorInvalidValue;
   }
   if (e != hipSuccess || used) return e;

@@ -14,6 +14,8 @@
 // One wavefront per row; a row is read once from HBM (kept in registers for
 // rows up to 64*32 floats, re-read from L2 otherwise) and its codes are written
 // as packed dwords.
+#include <algorithm>
+
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -75,6 +77,73 @@ __device__ __forceinline__ void quantize_row(const float* __restrict__ in, int l
   if (lane == 0) *scale = amax == 0.0f ? 0.0f : amax / 127.0f;
 }
 
+// Maximum over the wavefront with DPP only, returned in every lane.
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, dpp_mov<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_mov<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_mov<0x124>(v));  // row_ror:4
+  v = fmaxf(v, dpp_mov<0x128>(v));  // row_ror:8: every lane holds its row's maximum
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                   __builtin_bit_cast(int, v), __builtin_bit_cast(int, v), 0x142, 0xA, 0xF, false)));
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                   __builtin_bit_cast(int, v), __builtin_bit_cast(int, v), 0x143, 0xC, 0xF, false)));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+// Rows of len <= NV*256 floats (len % 4 == 0, 16-byte aligned rows): each
+// wavefront quantizes RPW consecutive rows, with the loads of all of them
+// issued first.  Straight-line code (rows past the end are clamped to the
+// last row, quantized again to the same bits; FULL = len == NV*256 drops the
+// per-lane bounds tests): a loop or a memory access under a branch makes the
+// compiler wait for every outstanding load.
+constexpr int kRowsPerWave = 4;
+
+template <int NV, bool FULL>
+__global__ __launch_bounds__(256) void kv_quantize_pipe_kernel(const float* __restrict__ in,
+                                                               int8_t* __restrict__ codes,
+                                                               float* __restrict__ scales,
+                                                               size_t n_rows, int len) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const size_t w = (size_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const size_t r0 = w * kRowsPerWave;
+  if (r0 >= n_rows) return;
+  float4 rv[kRowsPerWave][NV];
+#pragma unroll
+  for (int k = 0; k < kRowsPerWave; k++) {
+    const size_t row = min(r0 + k, n_rows - 1);
+    const float* src = in + row * (size_t)len;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+      const int e = (i * 64 + lane) * 4;
+      rv[k][i] = (FULL || e < len) ? *reinterpret_cast<const float4*>(src + e)
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kRowsPerWave; k++) {
+    const size_t row = min(r0 + k, n_rows - 1);
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; i++)
+      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(rv[k][i].x), fabsf(rv[k][i].y)),
+                               fmaxf(fabsf(rv[k][i].z), fabsf(rv[k][i].w))));
+    amax = wave_max_dpp(amax);
+    const float inv = amax != 0.0f ? 127.0f / amax : 0.0f;
+    int8_t* dst = codes + row * (size_t)len;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+      const int e = (i * 64 + lane) * 4;
+      // amax == 0 gives inv == 0 and so codes 0 (NaN inputs map to 0 too):
+      // no branch needed
+      if (FULL || e < len)
+        *reinterpret_cast<uint32_t*>(dst + e) =
+            pack4(rv[k][i].x, rv[k][i].y, rv[k][i].z, rv[k][i].w, inv);
+    }
+    if (lane == 0) scales[row] = amax / 127.0f;  // 0 when amax == 0
+  }
+}
+
 template <int NV>
 __global__ __launch_bounds__(256) void kv_quantize_kernel(const float* __restrict__ in,
                                                           int8_t* __restrict__ codes,
@@ -126,6 +195,20 @@ unsigned grid_waves(size_t rows) {
 hipError_t launch_kv_quantize(const float* in, int8_t* codes, float* scales, size_t n_rows,
                               size_t row_len, hipStream_t s) {
   if (n_rows == 0) return hipSuccess;
+  const bool vec = row_len % 4 == 0 && ((uintptr_t)in & 15) == 0 && ((uintptr_t)codes & 3) == 0;
+  if (vec && row_len <= 64 * 4 * 4) {
+    const size_t waves = (n_rows + kRowsPerWave - 1) / kRowsPerWave;
+    const size_t g = (waves + 3) / 4;
+    if (g > 0x7FFFFFFF) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)g);
+    if (row_len == 64 * 4 * 4)
+      hipLaunchKernelGGL((kv_quantize_pipe_kernel<4, true>), grid, dim3(256), 0, s, in, codes, scales,
+                         n_rows, (int)row_len);
+    else
+      hipLaunchKernelGGL((kv_quantize_pipe_kernel<4, false>), grid, dim3(256), 0, s, in, codes, scales,
+                         n_rows, (int)row_len);
+    return hipGetLastError();
+  }
   if (row_len <= 64 * 4 * 4)
     hipLaunchKernelGGL(kv_quantize_kernel<4>, dim3(grid_waves(n_rows)), dim3(256), 0, s, in, codes,
                        scales, n_rows, (int)row_len);

@@ -611,8 +611,17 @@ __global__ __launch_bounds__(256) void slice_reduce_kernel(const float* __restri
                                                            int slices) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  float s = part[i];
-  for (int z = 1; z < slices; z++) s += part[(size_t)z * n + i];
+  // Eight slice loads are in flight together (addresses clamped, so the
+  // loads are unconditional); the sum still runs in slice order.
+  float s = 0.f;
+  for (int z0 = 0; z0 < slices; z0 += 8) {
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) v[k] = part[(size_t)min(z0 + k, slices - 1) * n + i];
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+      if (z0 + k < slices) s = z0 + k == 0 ? v[k] : s + v[k];
+  }
   y[i] = s;
 }
 

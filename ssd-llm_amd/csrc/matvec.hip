@@ -485,6 +485,10 @@ __device__ __forceinline__ void lds_barrier() {
 // Vector memory instructions one load_unit issues.
 template <int F> constexpr int loads_per_unit() { return (F == kQ4_K || F == kQ4_0) ? 3 : 5; }
 
+// rows whose weight loads are in flight at once in a wave (measured at
+// 14336 x 4096 Q4_K: depth 1 9.8 us, 2 8.5 us, 3 9.2 us, 5 11.2 us)
+template <int RMAX> constexpr int kB1Depth = RMAX < 2 ? RMAX : 2;
+
 // Every lane keeps the digit planes of its units in registers.  KS waves split
 // each row's units (KS > 1 for long rows; partial sums meet in LDS); the
 // workgroup's other waves take other rows.  Rows are spread evenly over all
@@ -511,7 +515,8 @@ template <int F> constexpr int loads_per_unit() { return (F == kQ4_K || F == kQ4
 template <int F, int UPL, int RMAX, bool FULL, int SIT>
 __global__ __launch_bounds__(768) void mv_b1(const uint8_t* __restrict__ w,
                                              const float* __restrict__ x, float* __restrict__ y,
-                                             int out_dim, int row_bpr, int slice_bpr, int ks) {
+                                             int out_dim, int row_bpr, int slice_bpr, int ks,
+                                             bool interleave) {
   using FU = FastUnit<F>;
   using D = Dig<F>;
   constexpr int NW = FU::NW, US = D::US;
@@ -530,13 +535,23 @@ __global__ __launch_bounds__(768) void mv_b1(const uint8_t* __restrict__ w,
   const int nw = blockDim.x >> 6, kw = wave % ks, stream = wave / ks, rs = nw / ks;
   const size_t row_bytes = (size_t)row_bpr * Geom<F>::bb;
   const long n_streams = (long)gridDim.x * rs, gs = (long)blockIdx.x * rs + stream;
-  const int r_begin = (int)(gs * out_dim / n_streams);
-  const int n_rows = (int)((gs + 1) * out_dim / n_streams) - r_begin;  // <= RMAX
+  // Rows of a stream are either one contiguous run or, interleaved, rows
+  // gs, gs + n_streams, ... (all waves then sweep the matrix together).
+  int r_begin, r_step, n_rows;  // n_rows <= RMAX either way
+  if (interleave) {
+    r_begin = (int)gs;
+    r_step = (int)n_streams;
+    n_rows = gs < out_dim ? (int)((out_dim - 1 - gs) / n_streams) + 1 : 0;
+  } else {
+    r_begin = (int)(gs * out_dim / n_streams);
+    r_step = 1;
+    n_rows = (int)((gs + 1) * out_dim / n_streams) - r_begin;
+  }
   const int ubase = kw * 64 * UPL + lane;
 
   uint32_t buf[RMAX][UPL][NW];
   auto load_row = [&](int rr) {
-    const int row = max(0, min(r_begin + rr, out_dim - 1));
+    const int row = max(0, min(r_begin + rr * r_step, out_dim - 1));
     const uint8_t* rp = w + (size_t)row * row_bytes;
 #pragma unroll
     for (int i = 0; i < UPL; i++) {
@@ -547,14 +562,14 @@ __global__ __launch_bounds__(768) void mv_b1(const uint8_t* __restrict__ w,
 
   XChunks<SIT> st;
   stage_load<SIT>(x, keff, st, blockDim.x);  // 1.
-  load_row(0);
+#pragma unroll
+  for (int rr = 0; rr < kB1Depth<RMAX>; rr++) load_row(rr);
   {
-    // 2. wait for x only (the row-0 loads issued after it may stay in flight)
-    constexpr int N = UPL * loads_per_unit<F>();
+    // 2. wait for x only (the weight loads issued after it may stay in flight)
+    constexpr int N = kB1Depth<RMAX> * UPL * loads_per_unit<F>();
     static_assert(N < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
   }
-  if (RMAX > 1) load_row(1);
   stage_store<F, SIT>(st, keff, lds, blockDim.x);
   lds_barrier();
 
@@ -573,7 +588,7 @@ __global__ __launch_bounds__(768) void mv_b1(const uint8_t* __restrict__ w,
   float acc[RMAX];
 #pragma unroll
   for (int rr = 0; rr < RMAX; rr++) {  // 3.
-    if (rr >= 1 && rr + 1 < RMAX) load_row(rr + 1);  // rows 0 and 1 are already in flight
+    if (rr >= 1 && rr + kB1Depth<RMAX> - 1 < RMAX) load_row(rr + kB1Depth<RMAX> - 1);
     float a = 0.f;
     if (ks > 1 || rr < n_rows) {  // uniform per wave: padding rows are not computed
 #pragma unroll
@@ -590,7 +605,7 @@ __global__ __launch_bounds__(768) void mv_b1(const uint8_t* __restrict__ w,
     if (ks == 1) {
 #pragma unroll
       for (int rr = 0; rr < RMAX; rr++)
-        if (rr < n_rows) y[r_begin + rr] = acc[rr];
+        if (rr < n_rows) y[r_begin + rr * r_step] = acc[rr];
     } else {
 #pragma unroll
       for (int rr = 0; rr < RMAX; rr++) red[rr * ks + kw] = acc[rr];
@@ -601,7 +616,7 @@ __global__ __launch_bounds__(768) void mv_b1(const uint8_t* __restrict__ w,
     if (wave == 0 && lane < n_rows) {
       float s = 0.f;
       for (int k = 0; k < ks; k++) s += red[lane * ks + k];
-      y[r_begin + lane] = s;
+      y[r_begin + lane * r_step] = s;
     }
   }
 }
@@ -856,12 +871,15 @@ hipError_t run_b1_sit(const uint8_t* w, const float* x, float* y, int out_dim, i
   hipError_t e = set_lds_attr(kern, lds);
   if (e != hipSuccess) return e;
   const int threads = 64 * ks * rs;
+  // Q8_0 rows (68 bytes per unit) run faster with interleaved rows (11008 x
+  // 4096: 11.0 us vs 11.5 us); the other formats with contiguous runs.
+  const bool interleave = F == kQ8_0;
   const long streams_needed = (out_dim + RMAX - 1) / RMAX;
   // about one workgroup per CU over all slices
   long n_wg = std::max<long>((device_cu_count() + slices - 1) / slices, (streams_needed + rs - 1) / rs);
   n_wg = std::max<long>(1, std::min<long>(n_wg, (out_dim + rs - 1) / rs));
   hipLaunchKernelGGL(kern, dim3((unsigned)n_wg, (unsigned)slices), dim3(threads), lds, s, w, x, y,
-                     out_dim, row_bpr, slice_bpr, ks);
+                     out_dim, row_bpr, slice_bpr, ks, interleave);
   return hipGetLastError();
 }
 

@@ -111,10 +111,14 @@ __device__ __forceinline__ h8 codes_times_s(uint32_t qd, uint32_t s2) {
   return r;
 }
 
-// 4 bytes (values < 64) -> 4 fp16 values
-__device__ __forceinline__ void bytes_to_f16(uint32_t b, _Float16* dst) {
+// 4 bytes (values < 1024) -> fp16 values: bytes 0, 1 -> r[0], bytes 2, 3 -> r[1]
+__device__ __forceinline__ void bytes_to_f16(uint32_t b, uint32_t* r) {
 #pragma unroll
-  for (int i = 0; i < 4; i++) dst[i] = (_Float16)(float)byte_of(b, i);
+  for (int i = 0; i < 2; i++) {
+    const uint32_t u = __builtin_amdgcn_perm(0u, b, (uint32_t)(2 * i) | 0x0C00u | ((uint32_t)(2 * i + 1) << 16) | 0x0C000000u);
+    const h2 hv = __builtin_bit_cast(h2, u | 0x64006400u) - (h2){(_Float16)1024.f, (_Float16)1024.f};
+    r[i] = __builtin_bit_cast(uint32_t, hv);
+  }
 }
 
 // blockIdx.z selects split z of the K range (split = gridDim.z); split z
@@ -126,7 +130,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_mfma(const uint8_t* __restric
                                                         float* __restrict__ y, int M, int N, int K) {
   constexpr int BM = 16 * MT;
   constexpr int XCH = BM * 4 / 256;  // 16-byte X chunks per thread per step
-  constexpr int SS = 24;                   // LDS row stride (halves) of the sub-block sums
+  constexpr int SS = 32;                   // LDS row stride (halves) of the sub-block sums
   constexpr int SCH = BM * 4 / 256;        // 8-byte pieces of sub-block sums per thread
   __shared__ __align__(16) _Float16 xs[2][BM * XS];
   __shared__ __align__(16) _Float16 xsum[BM * SS];
@@ -218,6 +222,10 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_mfma(const uint8_t* __restric
 #pragma unroll
     for (int j = 0; j < NT; j++) tot[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
+  // halves 16..31 of every sub-block-sum row stay zero: lanes 32-63 read them
+  // as their part of the min-term A operand
+  for (int r = threadIdx.x; r < BM; r += 256)
+    *reinterpret_cast<u32x4*>(&xsum[r * SS + 16]) = *reinterpret_cast<u32x4*>(&xsum[r * SS + 24]) = u32x4{0u, 0u, 0u, 0u};
   fetch_head(0);
   fetch_x(0, std::integral_constant<int, 0>{});
   fetch_x(1, std::integral_constant<int, 1>{});
@@ -301,25 +309,22 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_mfma(const uint8_t* __restric
     step(std::integral_constant<int, 5>{}, s + 5, b, s2);
     step(std::integral_constant<int, 6>{}, s + 6, b, s2);
     step(std::integral_constant<int, 7>{}, s + 7, b, s2);
-    // min term: A = XS hi (lanes 0-15) / lo (16-31), B = m (lanes 0-31); lanes
-    // 32-63 carry zeros in both
+    // min term: A = XS hi (lanes 0-15) / lo (16-31) / zeros (32-63), B = the
+    // 8 mins m in every lane group (finite, so the zero A lanes add 0)
     h8 bmin[NT];
     float dd[NT], dm[NT];
 #pragma unroll
     for (int j = 0; j < NT; j++) {
-      _Float16 mv[8];
+      uint32_t mv[4];
       bytes_to_f16(mlo[j], mv);
-      bytes_to_f16(mhi[j], mv + 4);
-#pragma unroll
-      for (int i = 0; i < 8; i++) bmin[j][i] = c < 2 ? mv[i] : (_Float16)0.f;
+      bytes_to_f16(mhi[j], mv + 2);
+      bmin[j] = __builtin_bit_cast(h8, u32x4{mv[0], mv[1], mv[2], mv[3]});
       dd[j] = f16_to_f32(dbits[j] & 0xFFFFu);
       dm[j] = f16_to_f32(dbits[j] >> 16);
     }
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
-      h8 amin = *reinterpret_cast<const h8*>(&xsum[(mt * 16 + (lane & 15)) * SS + 8 * (c & 1)]);
-#pragma unroll
-      for (int i = 0; i < 8; i++) amin[i] = c < 2 ? amin[i] : (_Float16)0.f;
+      const h8 amin = *reinterpret_cast<const h8*>(&xsum[(mt * 16 + (lane & 15)) * SS + 8 * c]);
 #pragma unroll
       for (int j = 0; j < NT; j++) {
         const f4 qm = __builtin_amdgcn_mfma_f32_16x16x32_f16(amin, bmin[j], f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);

@@ -192,28 +192,23 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_mfma(const uint8_t* __restric
     }
   };
 
-  // Weights, loaded half a super-block ahead: the header (d|dmin, scale bytes
-  // 0-3, 4-7, 8-11) and the 16 code bytes of sub-block c (code0) at step 4 of
-  // the previous super-block, the 16 code bytes of sub-block 4+c (code1) at
-  // step 0 of its own.
-  uint32_t hdr[NT][4];
-  u32x4a4 code0[NT], code1[NT];
+  // Weights, loaded a whole super-block (8 steps) ahead into queue registers:
+  // the header (d|dmin, scale bytes 0-3, 4-7, 8-11) with the 16 code bytes of
+  // sub-block c (used in steps 0-3) at step 0 of the previous super-block, the
+  // 16 code bytes of sub-block 4+c (steps 4-7) at its step 4.
+  u32x4a4 hdrq[NT], code0q[NT], code1q[NT], code0[NT], code1[NT];
   auto wptr = [&](int j, int b) { return wrow[j] + (size_t)(b_begin + min(b, b_end - b_begin - 1)) * 144; };
   auto fetch_head = [&](int b) {
 #pragma unroll
     for (int j = 0; j < NT; j++) {
       const uint8_t* p = wptr(j, b);
-      const u32x4a4 h = *reinterpret_cast<const u32x4a4*>(p);
-      hdr[j][0] = h.x;
-      hdr[j][1] = h.y;
-      hdr[j][2] = h.z;
-      hdr[j][3] = h.w;
-      code0[j] = *reinterpret_cast<const u32x4a4*>(p + 16 + 16 * c);
+      hdrq[j] = *reinterpret_cast<const u32x4a4*>(p);
+      code0q[j] = *reinterpret_cast<const u32x4a4*>(p + 16 + 16 * c);
     }
   };
   auto fetch_tail = [&](int b) {
 #pragma unroll
-    for (int j = 0; j < NT; j++) code1[j] = *reinterpret_cast<const u32x4a4*>(wptr(j, b) + 16 + 16 * (4 + c));
+    for (int j = 0; j < NT; j++) code1q[j] = *reinterpret_cast<const u32x4a4*>(wptr(j, b) + 16 + 16 * (4 + c));
   };
 
   f4 acc[MT][NT], tot[MT][NT];
@@ -227,6 +222,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_mfma(const uint8_t* __restric
   for (int r = threadIdx.x; r < BM; r += 256)
     *reinterpret_cast<u32x4*>(&xsum[r * SS + 16]) = *reinterpret_cast<u32x4*>(&xsum[r * SS + 24]) = u32x4{0u, 0u, 0u, 0u};
   fetch_head(0);
+  fetch_tail(0);
   fetch_x(0, std::integral_constant<int, 0>{});
   fetch_x(1, std::integral_constant<int, 1>{});
   fetch_x(2, std::integral_constant<int, 2>{});
@@ -242,6 +238,11 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_mfma(const uint8_t* __restric
   // buffer t % 2; queue slot t holds X of step s until step s-1 stored it.
   auto step = [&](auto t_c, int s, int b, const uint32_t (&s2)[NT][2]) {
     constexpr int t = decltype(t_c)::value, slot = t & 1;
+    if (t == 4) {  // sub-block 4+c codes arrive for steps 4-7; queue the next ones
+#pragma unroll
+      for (int j = 0; j < NT; j++) code1[j] = code1q[j];
+      fetch_tail(b + 1);
+    }
     h8 bf[NT];
 #pragma unroll
     for (int j = 0; j < NT; j++) {
@@ -249,11 +250,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_mfma(const uint8_t* __restric
       const uint32_t qd = (t & 3) == 0 ? cw.x : (t & 3) == 1 ? cw.y : (t & 3) == 2 ? cw.z : cw.w;
       bf[j] = codes_times_s(qd, s2[j][t >> 2]);
     }
-    if (t == 0) {
-      fetch_tail(b);
-      fetch_sums(b);
-    }
-    if (t == 4) fetch_head(b + 1);
+    if (t == 0) fetch_sums(b);
     if (t == 6) store_sums();
     // X of step s+1 goes to the other LDS buffer (its readers finished at the
     // barrier that ended step s-1; after the last step it is never read, and
@@ -289,9 +286,16 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_mfma(const uint8_t* __restric
     // s[0..3] = sc[0..3] & 63, s[4..7] = sc[0..3] >> 6 | (sc[8..11] & 15) << 2,
     // m[0..3] = sc[4..7] & 63, m[4..7] = sc[4..7] >> 6 | (sc[8..11] >> 4) << 2
     uint32_t s2[NT][2], mlo[NT], mhi[NT], dbits[NT];
+    u32x4a4 hdr[NT];
 #pragma unroll
     for (int j = 0; j < NT; j++) {
-      const uint32_t h1 = hdr[j][1], h2v = hdr[j][2], h3 = hdr[j][3];
+      hdr[j] = hdrq[j];
+      code0[j] = code0q[j];
+    }
+    fetch_head(b + 1);
+#pragma unroll
+    for (int j = 0; j < NT; j++) {
+      const uint32_t h1 = hdr[j].y, h2v = hdr[j].z, h3 = hdr[j].w;
       const uint32_t slo = h1 & 0x3F3F3F3Fu;
       const uint32_t shi = ((h1 >> 6) & 0x03030303u) | ((h3 & 0x0F0F0F0Fu) << 2);
       mlo[j] = h2v & 0x3F3F3F3Fu;
@@ -299,7 +303,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_mfma(const uint8_t* __restric
       const uint32_t sa = (slo >> (8 * c)) & 0xFFu, sb = (shi >> (8 * c)) & 0xFFu;
       s2[j][0] = sa | (sa << 16);
       s2[j][1] = sb | (sb << 16);
-      dbits[j] = hdr[j][0];
+      dbits[j] = hdr[j].x;
     }
     step(std::integral_constant<int, 0>{}, s, b, s2);
     step(std::integral_constant<int, 1>{}, s + 1, b, s2);

@@ -22,9 +22,13 @@
 // plus XS: in a super-block, MFMA step t (32 k values) gives lane group c
 // (lanes 16c .. 16c+15) the 8 values of sub-block 4*(t/4) + c at offset
 // 8*(t%4), so one 16-byte load hands a lane the codes of a whole sub-block.
-// Tiling: a workgroup of 4 waves computes a (16*MT) x 128 tile; X tiles are
-// staged through LDS (double-buffered), each wave owns 32 columns and builds
-// its B fragments from the codes in registers.
+// Tiling: a workgroup of 4 waves computes a (16*MT) x 128 tile, two
+// workgroups per CU.  X tiles are staged through LDS (double-buffered, fed
+// from a register ring one super-block deep); weights are prefetched a
+// super-block ahead; each wave owns 32 columns and builds its B fragments from
+// the codes in registers.  Every global load is consumed outside branches, so
+// the compiler's waits stay partial (a load consumed under a branch costs a
+// full vmcnt(0) drain).
 #include <algorithm>
 #include <type_traits>
 
@@ -375,18 +379,15 @@ bool gemm_q4k_mfma_ok(const void* w, const void* x) {
 
 namespace {
 
-// M rows per workgroup tile: 128 when that still gives two workgroups per CU
-// without splitting K, else 64
-int gemm_mt(size_t M, size_t N) {
-  const size_t tiles128 = ((N + BN - 1) / BN) * ((M + 127) / 128);
-  (void)tiles128;
-  return 4;
-}
+// Workgroup tiles are 64 (M) x 128 (N): 16 x 4 = 64 rows per wave.  128-row
+// tiles would halve the B-fragment work per MFMA but need more than the 256
+// registers two waves per SIMD allow (measured: 31 spilled).
+constexpr int kMT = 4;
 
 // K splits for a GEMM: enough workgroups for two per CU, at most 8 splits and
 // never more than one split per 256-element block.
-int gemm_split(size_t M, size_t N, size_t K, int mt) {
-  const size_t bm = 16 * (size_t)mt;
+int gemm_split(size_t M, size_t N, size_t K) {
+  const size_t bm = 16 * (size_t)kMT;
   const size_t tiles = ((N + BN - 1) / BN) * ((M + bm - 1) / bm);
   const size_t want = 2 * (size_t)device_cu_count();
   size_t split = tiles >= want ? 1 : (want + tiles - 1) / tiles;
@@ -403,7 +404,7 @@ size_t prep_bytes(size_t M, size_t K) { return M * K * 2 + M * (K / 256) * 32; }
 
 size_t gemm_q4k_workspace_bytes(const void* w, const void* x, size_t M, size_t N, size_t K) {
   if (!gemm_q4k_mfma_ok(w, x)) return M * K * sizeof(float);
-  const int split = gemm_split(M, N, K, gemm_mt(M, N));
+  const int split = gemm_split(M, N, K);
   return prep_bytes(M, K) + (split > 1 ? (size_t)split * M * N * sizeof(float) : 0);
 }
 
@@ -412,8 +413,7 @@ hipError_t launch_gemm_q4k(const uint8_t* w, const uint16_t* x, float* y, size_t
   if (M == 0 || N == 0) return hipSuccess;
   if (K % 256 != 0) return hipErrorInvalidValue;
   if (gemm_q4k_mfma_ok(w, x)) {
-    const int mt = gemm_mt(M, N);
-    const int split = gemm_split(M, N, K, mt);
+    const int split = gemm_split(M, N, K);
     const size_t need = prep_bytes(M, K) + (split > 1 ? (size_t)split * M * N * sizeof(float) : 0);
     if (workspace_bytes < need) return hipErrorInvalidValue;
     _Float16* xp = static_cast<_Float16*>(workspace);
@@ -424,14 +424,11 @@ hipError_t launch_gemm_q4k(const uint8_t* w, const uint16_t* x, float* y, size_t
                        (int)M, (int)K);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int bm = 16 * mt;
+    const int bm = 16 * kMT;
     const dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + bm - 1) / bm), (unsigned)split);
     if (grid.y > 65535) return hipErrorInvalidValue;
     float* dst = split > 1 ? part : y;
-    if (mt == 8)
-      hipLaunchKernelGGL(gemm_q4k_mfma<8>, grid, dim3(256), 0, s, w, xp, xsp, dst, (int)M, (int)N, (int)K);
-    else
-      hipLaunchKernelGGL(gemm_q4k_mfma<4>, grid, dim3(256), 0, s, w, xp, xsp, dst, (int)M, (int)N, (int)K);
+    hipLaunchKernelGGL(gemm_q4k_mfma<kMT>, grid, dim3(256), 0, s, w, xp, xsp, dst, (int)M, (int)N, (int)K);
     e = hipGetLastError();
     if (e != hipSuccess || split == 1) return e;
     const size_t mn = M * N;

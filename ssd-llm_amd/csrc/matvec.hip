@@ -290,16 +290,21 @@ struct XChunks {
   float v[SIT][8];
 };
 
+// rows > 1: the chunks of rows x rows of x (row stride x_stride floats) form
+// one sequence (a row's chunk count is a multiple of 4, so no 32-element group
+// straddles two rows).
 template <int SIT>
 __device__ __forceinline__ void stage_load(const float* __restrict__ x, int keff, XChunks<SIT>& st,
-                                           int nthreads) {
-  const int nchunk = keff >> 3;
+                                           int nthreads, int rows = 1, size_t x_stride = 0) {
+  const int nchunk = keff >> 3, total = rows * nchunk;
 #pragma unroll
   for (int it = 0; it < SIT; it++) {
     const int c = it * nthreads + threadIdx.x;
-    if (c < nchunk) {
-      const float4 a = *reinterpret_cast<const float4*>(x + 8 * c);
-      const float4 b = *reinterpret_cast<const float4*>(x + 8 * c + 4);
+    if (c < total) {
+      const int r = rows > 1 ? c / nchunk : 0, cc = c - r * nchunk;
+      const float* xp = x + (size_t)r * x_stride + 8 * cc;
+      const float4 a = *reinterpret_cast<const float4*>(xp);
+      const float4 b = *reinterpret_cast<const float4*>(xp + 4);
       st.v[it][0] = a.x; st.v[it][1] = a.y; st.v[it][2] = a.z; st.v[it][3] = a.w;
       st.v[it][4] = b.x; st.v[it][5] = b.y; st.v[it][6] = b.z; st.v[it][7] = b.w;
     } else {
@@ -309,15 +314,18 @@ __device__ __forceinline__ void stage_load(const float* __restrict__ x, int keff
   }
 }
 
+// rows > 1: row r's planes start lds_stride dwords after row r-1's.
 template <int F, int SIT>
-__device__ __forceinline__ void stage_store(const XChunks<SIT>& st, int keff, uint32_t* lds, int nthreads) {
+__device__ __forceinline__ void stage_store(const XChunks<SIT>& st, int keff, uint32_t* lds, int nthreads,
+                                            int rows = 1, int lds_stride = 0) {
   using D = Dig<F>;
-  const int nchunk = keff >> 3;
+  const int nchunk = keff >> 3, total = rows * nchunk;
 #pragma unroll
   for (int it = 0; it < SIT; it++) {
-    if (it * nthreads >= nchunk) break;  // uniform across the staging waves
-    const int c = it * nthreads + threadIdx.x;
-    const bool live = c < nchunk;
+    if (it * nthreads >= total) break;  // uniform across the staging waves
+    const int c0 = it * nthreads + threadIdx.x;
+    const bool live = c0 < total;
+    const int r = rows > 1 ? c0 / nchunk : 0, c = c0 - r * nchunk;
     const float* v = st.v[it];
     float m = 0.f, s = 0.f;
     bool bad = false;
@@ -346,7 +354,7 @@ __device__ __forceinline__ void stage_store(const XChunks<SIT>& st, int keff, ui
     gbad |= __shfl_xor(gbad ? 1 : 0, 2, 64) != 0;
     if (live) {
       const int g = c >> 2;
-      uint32_t* rec = lds + (size_t)(g / D::NG) * D::US + (g % D::NG) * D::GW;
+      uint32_t* rec = lds + (size_t)r * lds_stride + (size_t)(g / D::NG) * D::US + (g % D::NG) * D::GW;
       uint32_t* pl = rec + 6 * k;
 #pragma unroll
       for (int d = 0; d < 3; d++) {
@@ -638,6 +646,105 @@ __global__ __launch_bounds__(256) void slice_reduce_kernel(const float* __restri
       if (z0 + k < slices) s = z0 + k == 0 ? v[k] : s + v[k];
   }
   y[i] = s;
+}
+
+// Small batches (NB = 2..8 activation rows) on the digit-plane scheme.  The
+// planes of all NB rows of x sit in LDS (row b at b * U * US dwords); each
+// wave streams its weight rows through registers once, as mv_b1 does, and
+// applies every row to all NB activations, so W is read once per call.  One
+// unit per lane (rows longer than 64 units are cut into K slices; slice z
+// writes partials [z][NB][out_dim]).
+template <int F, int NB, int RMAX, int RG, bool FULL, int SIT>
+__global__ __launch_bounds__(512) void mv_bn(const uint8_t* __restrict__ w,
+                                             const float* __restrict__ x, float* __restrict__ y,
+                                             int out_dim, int in_dim, int row_bpr, int slice_bpr,
+                                             bool interleave) {
+  using FU = FastUnit<F>;
+  using D = Dig<F>;
+  constexpr int NW = FU::NW, US = D::US;
+  static_assert(US % 4 == 0, "unit records are read as 16-byte vectors");
+  extern __shared__ uint4 lds4[];
+  uint32_t* lds = reinterpret_cast<uint32_t*>(lds4);
+  const int blk0 = blockIdx.y * slice_bpr;
+  const int bpr = min(slice_bpr, row_bpr - blk0);
+  w += (size_t)blk0 * Geom<F>::bb;
+  x += (size_t)blk0 * Geom<F>::bs;
+  y += (size_t)blockIdx.y * NB * out_dim;
+  const int keff = bpr * Geom<F>::bs;
+  const int U = keff / FU::E;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const size_t row_bytes = (size_t)row_bpr * Geom<F>::bb;
+  const long n_streams = (long)gridDim.x * nw, gs = (long)blockIdx.x * nw + wave;
+  int r_begin, r_step, n_rows;  // n_rows <= RMAX
+  if (interleave) {
+    r_begin = (int)gs;
+    r_step = (int)n_streams;
+    n_rows = gs < out_dim ? (int)((out_dim - 1 - gs) / n_streams) + 1 : 0;
+  } else {
+    r_begin = (int)(gs * out_dim / n_streams);
+    r_step = 1;
+    n_rows = (int)((gs + 1) * out_dim / n_streams) - r_begin;
+  }
+  const int u = lane;
+  const bool ok = FULL || u < U;
+
+  uint32_t buf[RMAX][NW];
+  auto load_row = [&](int rr) {
+    const int row = max(0, min(r_begin + rr * r_step, out_dim - 1));
+    if (ok) load_unit<F>(w + (size_t)row * row_bytes, u, buf[rr]);
+  };
+
+  static_assert(RMAX % RG == 0, "rows come in groups of RG");
+  XChunks<SIT> st;
+  stage_load<SIT>(x, keff, st, blockDim.x, NB, (size_t)in_dim);
+#pragma unroll
+  for (int rr = 0; rr < RG; rr++) load_row(rr);
+  {
+    constexpr int N = RG * loads_per_unit<F>();
+    static_assert(N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+  }
+  stage_store<F, SIT>(st, keff, lds, blockDim.x, NB, U * US);
+  lds_barrier();
+
+  // Groups of RG rows: the next group's rows are requested before this one is
+  // computed; each activation row's planes are read from LDS once per group.
+  float acc[RMAX][NB];
+#pragma unroll
+  for (int g0 = 0; g0 < RMAX; g0 += RG) {
+    if (g0 + RG < RMAX) {
+#pragma unroll
+      for (int r = 0; r < RG; r++) load_row(g0 + RG + r);
+    }
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+      uint32_t pr[US];
+#pragma unroll
+      for (int t = 0; t < US; t += 4) {
+        const uint4 v = lds4[((size_t)b * U + u) * (US / 4) + t / 4];
+        pr[t] = v.x; pr[t + 1] = v.y; pr[t + 2] = v.z; pr[t + 3] = v.w;
+      }
+#pragma unroll
+      for (int r = 0; r < RG; r++) {
+        float a = 0.f;
+        if (g0 + r < n_rows && ok)  // uniform per wave except the last units of a partial row
+          accumulate_dig<F>(buf[g0 + r], u, [&](int t) { return pr[t]; }, a);
+        acc[g0 + r][b] = a;
+      }
+    }
+  }
+#pragma unroll
+  for (int rr = 0; rr < RMAX; rr++)
+#pragma unroll
+    for (int b = 0; b < NB; b++) acc[rr][b] = wave_sum_l63(acc[rr][b]);
+  if (lane == 63) {
+#pragma unroll
+    for (int rr = 0; rr < RMAX; rr++)
+      if (rr < n_rows) {
+#pragma unroll
+        for (int b = 0; b < NB; b++) y[(size_t)b * out_dim + r_begin + rr * r_step] = acc[rr][b];
+      }
+  }
 }
 
 // ------------------------------------------------------ batched (B > 1) path
@@ -1017,6 +1124,105 @@ hipError_t b1_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, 
   return hipGetLastError();
 }
 
+// K slices of the small-batch kernel: one unit per lane, at most 64 per slice.
+template <int F>
+B1Plan<F> bn_plan(int bpr) {
+  const int U = bpr * Geom<F>::bs / FastUnit<F>::E;
+  B1Plan<F> p;
+  p.slices = (U + 63) / 64;
+  int sb = (bpr + p.slices - 1) / p.slices;
+  if constexpr (Geom<F>::bs == 32) sb += sb & 1;  // Q4_0 / Q8_0: two blocks per unit
+  p.slice_bpr = sb;
+  p.slices = (bpr + sb - 1) / sb;
+  p.full = (bpr % sb == 0) && sb * Geom<F>::bs / FastUnit<F>::E == 64;
+  return p;
+}
+
+template <int F>
+size_t bn_workspace_floats(int out_dim, int bpr, int nb) {
+  const B1Plan<F> p = bn_plan<F>(bpr);
+  return p.slices > 1 ? (size_t)p.slices * nb * out_dim : 0;
+}
+
+// Rows per wave of mv_bn and rows per group (planes read once per group)
+template <int NB> constexpr int kBnRows = 6;
+template <int NB> constexpr int kBnGroup = NB >= 4 ? 3 : 2;
+
+template <int F, int NB, int RMAX, int RG, bool FULL>
+hipError_t run_bn(const uint8_t* w, const float* x, float* dst, int out_dim, int in_dim, int row_bpr,
+                  int slice_bpr, int slices, hipStream_t s) {
+  const int U = slice_bpr * Geom<F>::bs / FastUnit<F>::E;
+  const size_t lds = (size_t)NB * U * Dig<F>::US * sizeof(uint32_t);
+  if (lds > (size_t)lds_limit()) return hipErrorNotSupported;
+  // waves per workgroup: as many as fit with one workgroup per CU (cached per
+  // device and LDS size, probed on the deepest staging instantiation)
+  static std::mutex mu;
+  static std::map<std::pair<int, size_t>, int> rs_cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+  int rs = 0;
+  {
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = rs_cache.find({dev, lds});
+    if (it != rs_cache.end()) rs = it->second;
+  }
+  if (rs == 0) {
+    auto probe = mv_bn<F, NB, RMAX, RG, FULL, 8>;
+    hipError_t e = set_lds_attr(probe, lds);
+    if (e != hipSuccess) return e;
+    rs = 1;
+    for (int cand = 8; cand >= 1; cand--) {  // launch bounds: 512 threads
+      int per_cu = 0;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, probe, 64 * cand, lds) == hipSuccess && per_cu >= 1) {
+        rs = cand;
+        break;
+      }
+    }
+    std::lock_guard<std::mutex> lk(mu);
+    rs_cache[{dev, lds}] = rs;
+  }
+  const int threads = 64 * rs;
+  const int nchunk = NB * (slice_bpr * Geom<F>::bs / 8);
+  const int sit = (nchunk + threads - 1) / threads;
+  const long streams_needed = (out_dim + RMAX - 1) / RMAX;
+  long n_wg = std::max<long>((device_cu_count() + slices - 1) / slices, (streams_needed + rs - 1) / rs);
+  n_wg = std::max<long>(1, std::min<long>(n_wg, (out_dim + rs - 1) / rs));
+  const bool interleave = F == kQ8_0;
+  auto launch = [&](auto kern) {
+    hipError_t e = set_lds_attr(kern, lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kern, dim3((unsigned)n_wg, (unsigned)slices), dim3(threads), lds, s, w, x, dst,
+                       out_dim, in_dim, row_bpr, slice_bpr, interleave);
+    return hipGetLastError();
+  };
+  if (sit <= 1) return launch(mv_bn<F, NB, RMAX, RG, FULL, 1>);
+  if (sit <= 2) return launch(mv_bn<F, NB, RMAX, RG, FULL, 2>);
+  if (sit <= 4) return launch(mv_bn<F, NB, RMAX, RG, FULL, 4>);
+  if (sit <= 8) return launch(mv_bn<F, NB, RMAX, RG, FULL, 8>);
+  return hipErrorNotSupported;
+}
+
+// One chunk of NB activation rows; *used = false when the kernel cannot take it.
+template <int F, int NB>
+hipError_t bn_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, int in_dim, int bpr,
+                       hipStream_t s, float* ws, size_t ws_floats, bool* used) {
+  const B1Plan<F> p = bn_plan<F>(bpr);
+  *used = false;
+  if (p.slices > 1 && (!ws || ws_floats < (size_t)p.slices * NB * out_dim)) return hipSuccess;
+  float* dst = p.slices > 1 ? ws : y;
+  constexpr int R = kBnRows<NB>, G = kBnGroup<NB>;
+  hipError_t e = p.full ? run_bn<F, NB, R, G, true>(w, x, dst, out_dim, in_dim, bpr, p.slice_bpr, p.slices, s)
+                        : run_bn<F, NB, R, G, false>(w, x, dst, out_dim, in_dim, bpr, p.slice_bpr, p.slices, s);
+  if (e == hipErrorNotSupported) return hipSuccess;
+  if (e != hipSuccess) return e;
+  *used = true;
+  if (p.slices == 1) return hipSuccess;
+  const int n = NB * out_dim;
+  hipLaunchKernelGGL(slice_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, ws, y, n,
+                     p.slices);
+  return hipGetLastError();
+}
+
 template <int F>
 hipError_t fast_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, int in_dim,
                          int bpr, int batch, hipStream_t s, float* ws, size_t ws_floats,
@@ -1029,6 +1235,32 @@ hipError_t fast_dispatch(const uint8_t* w, const float* x, float* y, int out_dim
   if (batch == 1) {
     hipError_t e = b1_dispatch<F>(w, x, y, out_dim, bpr, s, ws, ws_floats, used);
     if (e != hipSuccess || *used) return e;
+  } else {
+    // chunks of 8 / 4 / 2 activation rows on mv_bn, a last single row on mv_b1
+    // (the first chunk decides: every chunk has the same row geometry)
+    int b0 = 0;
+    while (b0 < batch) {
+      const int left = batch - b0;
+      const float* xb = x + (size_t)b0 * in_dim;
+      float* yb = y + (size_t)b0 * out_dim;
+      bool u = false;
+      hipError_t e;
+      int take;
+      if (left >= 8) { take = 8; e = bn_dispatch<F, 8>(w, xb, yb, out_dim, in_dim, bpr, s, ws, ws_floats, &u); }
+      else if (left >= 4) { take = 4; e = bn_dispatch<F, 4>(w, xb, yb, out_dim, in_dim, bpr, s, ws, ws_floats, &u); }
+      else if (left >= 2) { take = 2; e = bn_dispatch<F, 2>(w, xb, yb, out_dim, in_dim, bpr, s, ws, ws_floats, &u); }
+      else { take = 1; e = b1_dispatch<F>(w, xb, yb, out_dim, bpr, s, ws, ws_floats, &u); }
+      if (e != hipSuccess) return e;
+      if (!u) {
+        if (b0 == 0) break;  // nothing launched: the paths below take the whole batch
+        return hipErrorInvalidValue;
+      }
+      b0 += take;
+    }
+    if (b0 == batch) {
+      *used = true;
+      return hipSuccess;
+    }
   }
   if constexpr (F == kQ8_0) {
     // the matrix-core kernel wins from 5 activation rows on (measured at
@@ -1076,17 +1308,24 @@ hipError_t launch_matvec_generic(int dtype, const uint8_t* w, const float* x, fl
   }
 }
 
+template <int F>
+size_t ws_floats_for(int od, int bpr, size_t batch) {
+  size_t n = b1_workspace_floats<F>(od, bpr);  // batch 1, or the last single row of a batch
+  if (batch > 1) n = std::max(n, bn_workspace_floats<F>(od, bpr, (int)std::min<size_t>(batch, 8)));
+  return n;
+}
+
 size_t matvec_workspace_bytes(int dtype, const void* w, const float* x, size_t out_dim,
                               size_t in_dim, size_t batch) {
-  if (batch != 1 || out_dim == 0) return 0;
+  if (batch == 0 || out_dim == 0) return 0;
   const uint8_t* wb = (const uint8_t*)w;
   const int od = (int)out_dim, id = (int)in_dim;
   size_t n = 0;
   switch (dtype) {
-    case kQ4_0: if (fast_aligned<kQ4_0>(wb, x, id, id / 32)) n = b1_workspace_floats<kQ4_0>(od, id / 32); break;
-    case kQ8_0: if (fast_aligned<kQ8_0>(wb, x, id, id / 32)) n = b1_workspace_floats<kQ8_0>(od, id / 32); break;
-    case kQ4_K: if (fast_aligned<kQ4_K>(wb, x, id, id / 256)) n = b1_workspace_floats<kQ4_K>(od, id / 256); break;
-    case kQ6_K: if (fast_aligned<kQ6_K>(wb, x, id, id / 256)) n = b1_workspace_floats<kQ6_K>(od, id / 256); break;
+    case kQ4_0: if (fast_aligned<kQ4_0>(wb, x, id, id / 32)) n = ws_floats_for<kQ4_0>(od, id / 32, batch); break;
+    case kQ8_0: if (fast_aligned<kQ8_0>(wb, x, id, id / 32)) n = ws_floats_for<kQ8_0>(od, id / 32, batch); break;
+    case kQ4_K: if (fast_aligned<kQ4_K>(wb, x, id, id / 256)) n = ws_floats_for<kQ4_K>(od, id / 256, batch); break;
+    case kQ6_K: if (fast_aligned<kQ6_K>(wb, x, id, id / 256)) n = ws_floats_for<kQ6_K>(od, id / 256, batch); break;
     default: break;
   }
   return n * sizeof(float);

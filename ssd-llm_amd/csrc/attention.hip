@@ -297,23 +297,28 @@ __device__ __forceinline__ float row16_sum(float v) {
 
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
-template <int HD>
-__global__ __launch_bounds__(256, HD == 256 ? 1 : 2) void paged_attn_mfma_kernel(
+template <int HD, int NWV>
+__global__ __launch_bounds__(64 * NWV, HD == 256 ? 1 : 8 / NWV) void paged_attn_mfma_kernel(
     const float* __restrict__ q, const int8_t* __restrict__ kc, const float* __restrict__ ks,
     const int8_t* __restrict__ vc, const float* __restrict__ vs, const int32_t* __restrict__ tables,
     const int32_t* __restrict__ ctx_lens, int max_blocks, int bs_log2, int n_head, int n_head_kv,
-    int n_hchunks, int split_len, int n_splits, float* __restrict__ partial) {
+    int n_hchunks, int split_len, int n_splits, bool kv_major, float* __restrict__ partial) {
   constexpr int NMI = HD / 64;  // MFMAs per 16-token sub-tile
   constexpr int VD = HD / 16;   // dims per lane in the PV layout
   constexpr int VW = VD / 4;    // V dwords per lane per round
-  __shared__ float p_s[4][kAt * 4];     // per wave: p * v_scale [token][head]
-  __shared__ int row_s[4][2 * kAt];     // per wave, two tiles: pool row of each token
-  __shared__ float ks_s[4][2 * kAt], vs_s[4][2 * kAt];
+  __shared__ float p_s[NWV][kAt * 4];     // per wave: p * v_scale [token][head]
+  __shared__ int row_s[NWV][2 * kAt];     // per wave, two tiles: pool row of each token
+  __shared__ float ks_s[NWV][2 * kAt], vs_s[NWV][2 * kAt];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int split = blockIdx.x * 4 + wave;
-  if (split >= n_splits) return;  // no barriers follow: the wave can leave
-  const int hc = blockIdx.y % n_hchunks, kvh = blockIdx.y / n_hchunks, seq = blockIdx.z;
+  // kv_major: the NWV waves take NWV KV heads of one split, so the slices of
+  // each token row they read (adjacent in the pool row) are fetched together
+  // (measured at config 5b: 129 us with 4 splits of one KV head per workgroup,
+  // 110 us with 4 KV heads); otherwise NWV splits of one KV head
+  const int split = kv_major ? blockIdx.x : blockIdx.x * NWV + wave;
+  const int hc = blockIdx.y % n_hchunks, seq = blockIdx.z;
+  const int kvh = kv_major ? (blockIdx.y / n_hchunks) * NWV + wave : blockIdx.y / n_hchunks;
+  if (split >= n_splits || kvh >= n_head_kv) return;  // no barriers follow: the wave can leave
   const int group = n_head / n_head_kv;
   const int h0 = kvh * group + hc * 4;
   const int G = min(4, group - hc * 4);
@@ -660,14 +665,27 @@ hipError_t run_paged_mfma(const PagedAttnArgs& a, float* part, hipStream_t s) {
   int n_splits, split_len;
   paged_mfma_splits(a, &n_splits, &split_len);
   const int group = a.n_head / a.n_head_kv, n_hchunks = (group + 3) / 4;
-  const dim3 grid((unsigned)((n_splits + 3) / 4), (unsigned)(a.n_head_kv * n_hchunks), (unsigned)a.n_seq);
-  if (grid.y > 65535 || grid.z > 65535) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((paged_attn_mfma_kernel<HD>), grid, dim3(256), 0, s, a.q, a.k_codes,
-                     a.k_scales, a.v_codes, a.v_scales, a.block_tables, a.ctx_lens,
-                     a.max_blocks_per_seq, log2_exact(a.block_size), a.n_head, a.n_head_kv,
-                     n_hchunks, split_len, n_splits, part);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  // one workgroup per split over 8 (else 4) KV heads when they divide n_head_kv
+  auto go = [&](auto nwv_c, bool kv_major) {
+    constexpr int NWV = decltype(nwv_c)::value;
+    const dim3 grid = kv_major
+        ? dim3((unsigned)n_splits, (unsigned)(a.n_head_kv / NWV * n_hchunks), (unsigned)a.n_seq)
+        : dim3((unsigned)((n_splits + NWV - 1) / NWV), (unsigned)(a.n_head_kv * n_hchunks), (unsigned)a.n_seq);
+    if (grid.y > 65535 || grid.z > 65535) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((paged_attn_mfma_kernel<HD, NWV>), grid, dim3(64 * NWV), 0, s, a.q, a.k_codes,
+                       a.k_scales, a.v_codes, a.v_scales, a.block_tables, a.ctx_lens,
+                       a.max_blocks_per_seq, log2_exact(a.block_size), a.n_head, a.n_head_kv,
+                       n_hchunks, split_len, n_splits, kv_major, part);
+    return hipGetLastError();
+  };
+  hipError_t e0;
+  if constexpr (HD < 256) {  // head_dim 256 fits one wave per SIMD only: 4 waves
+    e0 = a.n_head_kv % 8 == 0 ? go(std::integral_constant<int, 8>{}, true)
+                              : go(std::integral_constant<int, 4>{}, a.n_head_kv % 4 == 0);
+  } else {
+    e0 = go(std::integral_constant<int, 4>{}, a.n_head_kv % 4 == 0);
+  }
+  if (e0 != hipSuccess) return e0;
   hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3(a.n_head, a.n_seq), dim3(256), 0, s, part,
                      n_splits, a.n_head, a.out);
   return hipGetLastError();

@@ -57,6 +57,7 @@ CASES = [
     (2, 8, 2, 256, 32, [700, 33]),       # head_dim 256, block 32
     (1, 48, 4, 128, 16, [257]),          # group 12 > 8 heads per pass
     (2, 4, 2, 128, 1, [50, 3]),          # block size 1
+    (2, 48, 16, 64, 16, [200, 1500]),    # 16 KV heads (two 8-head workgroups), group 3
 ]
 
 

@@ -62,11 +62,6 @@ hipError_t launch_gemm_q4k(const uint8_t* w, const uint16_t* x, float* y, size_t
                            size_t K, void* workspace, size_t workspace_bytes, hipStream_t stream);
 size_t gemm_q4k_workspace_bytes(const void* w, const void* x, size_t M, size_t N, size_t K);
 
-// Q8_0 small batch (up to 16 rows per launch) on the matrix cores.
-bool mv_q8_0_mfma_ok(const void* w, const float* x, int in_dim, int bpr);
-hipError_t launch_mv_q8_0_mfma(const uint8_t* w, const float* x, float* y, int out_dim, int in_dim,
-                               int bpr, int batch, hipStream_t s);
-
 int device_cu_count();
 
 }  // namespace ssdq

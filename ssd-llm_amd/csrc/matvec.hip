@@ -1129,6 +1129,11 @@ template <int F>
 B1Plan<F> bn_plan(int bpr) {
   const int U = bpr * Geom<F>::bs / FastUnit<F>::E;
   B1Plan<F> p;
+  if (U == 0) {  // rows shorter than one unit: one empty slice
+    p.slice_bpr = bpr;
+    p.full = false;
+    return p;
+  }
   p.slices = (U + 63) / 64;
   int sb = (bpr + p.slices - 1) / p.slices;
   if constexpr (Geom<F>::bs == 32) sb += sb & 1;  // Q4_0 / Q8_0: two blocks per unit
@@ -1228,7 +1233,8 @@ hipError_t fast_dispatch(const uint8_t* w, const float* x, float* y, int out_dim
                          int bpr, int batch, hipStream_t s, float* ws, size_t ws_floats,
                          bool* used) {
   *used = false;
-  if (!fast_aligned<F>(w, x, in_dim, bpr)) return hipSuccess;
+  // rows shorter than one block: the generic path writes the (zero) sums
+  if (bpr == 0 || !fast_aligned<F>(w, x, in_dim, bpr)) return hipSuccess;
   const int keff = bpr * Geom<F>::bs;
   const int U = keff / FastUnit<F>::E;
   const int limit = lds_limit();
@@ -1260,14 +1266,6 @@ hipError_t fast_dispatch(const uint8_t* w, const float* x, float* y, int out_dim
     if (b0 == batch) {
       *used = true;
       return hipSuccess;
-    }
-  }
-  if constexpr (F == kQ8_0) {
-    // the matrix-core kernel wins from 5 activation rows on (measured at
-    // 11008 x 4096: B=4 35 us LDS kernel vs 37 us, B=8 76 us vs 41 us)
-    if (batch >= 5 && mv_q8_0_mfma_ok(w, x, in_dim, bpr)) {
-      *used = true;
-      return launch_mv_q8_0_mfma(w, x, y, out_dim, in_dim, bpr, batch, s);
     }
   }
   // LDS-resident x; batch processed in chunks of 8/4/2/1 that each fit LDS

@@ -90,7 +90,8 @@ def test_misaligned_weights_take_generic_path(dtype):
 ODD = [
     (Q4_0, 1, 32, 1), (Q4_0, 3, 96, 2), (Q4_0, 257, 4096 + 17, 3), (Q4_0, 70, 32 * 9, 1),
     (Q8_0, 5, 64, 5), (Q8_0, 129, 32 * 7, 7), (Q8_0, 64, 8192, 16), (Q8_0, 1000, 32 * 12, 6),
-    (Q8_0, 17, 32 * 64, 21),
+    (Q8_0, 17, 32 * 64, 21), (Q8_0, 7, 16, 4),  # the last: rows shorter than one block
+    (Q8_0, 40, 32 * 2, 3), (Q8_0, 300, 4096, 2),
     (Q4_K, 1, 256, 1), (Q4_K, 33, 256 * 3, 6), (Q4_K, 200, 256 * 40 + 100, 2), (Q4_K, 64, 4096, 9),
     (Q6_K, 2, 256, 1), (Q6_K, 31, 256 * 5, 3), (Q6_K, 100, 256 * 7, 8),
 ]
@@ -163,3 +164,40 @@ def test_repeat_is_deterministic():
     a, _ = run(Q4_K, None, x, 14336, 4096, w_dev=wd)
     b, _ = run(Q4_K, None, x, 14336, 4096, w_dev=wd)
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype,batch", [(Q8_0, 4), (Q4_K, 4), (Q8_0, 1), (Q4_K, 1)])
+def test_extreme_and_nonfinite_activations(dtype, batch):
+    # row 0 normal; row 1 with one NaN (the reference's serial sum is NaN for
+    # every output); row 2 with a whole 32-element block scaled by 1e30 and a
+    # 1e3 outlier in another block; row 3 scaled to ~1e-30.  Batch 1 takes
+    # the rows one call at a time.  (x is carried relative to the largest
+    # value of its 32-element block, so values more than ~7 orders below it
+    # are not: the outlier stays within that range.)
+    out_dim, in_dim = 300, 4096
+    w = synth.quant_weights(dtype, out_dim, in_dim, 71)
+    x = synth.normal_f32((4, in_dim), 72)
+    x[1, 1000] = np.nan
+    x[2, 64:96] *= np.float32(1e30)
+    x[2, 200] = np.float32(1e3)
+    x[3] *= np.float32(1e-30)
+    announce("matvec extreme activations", ssdq.TYPE_NAMES[dtype], batch)
+    if batch == 4:
+        y, rc = run(dtype, w, x, out_dim, in_dim, 4)
+        assert rc == 0
+        y = y.reshape(4, out_dim)
+    else:
+        rows = []
+        for b in range(4):
+            yb, rc = run(dtype, w, x[b], out_dim, in_dim, 1)
+            assert rc == 0
+            rows.append(yb)
+        y = np.stack(rows)
+    ref, exact = reference(dtype, w, x, out_dim, in_dim, 4)
+    ref, exact = ref.reshape(4, out_dim), exact.reshape(4, out_dim)
+    assert np.all(np.isnan(ref[1])) and np.all(np.isnan(y[1]))
+    for b in (0, 2):
+        assert_close_attributed(y[b], ref[b], exact[b], f"row {b}")
+    # row 3: relative agreement (the absolute 1e-4 term says nothing at 1e-30)
+    scale = np.abs(exact[3]).max()
+    assert np.all(np.abs(y[3] - exact[3]) <= 1e-3 * scale)

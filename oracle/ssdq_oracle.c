@@ -20,8 +20,9 @@ size_t ssdo_block_size(int dtype) {
     /* src/model/gguf.rs:87-105 */
     switch (dtype) {
         case SSDO_F32: case SSDO_F16: case SSDO_BF16: return 1;
-        case SSDO_Q4_0: case SSDO_Q8_0: return 32;
-        case SSDO_Q4_K: case SSDO_Q6_K: return 256;
+        case SSDO_Q4_0: case SSDO_Q8_0: case SSDO_IQ4_NL: return 32;
+        case SSDO_Q2_K: case SSDO_Q3_K: case SSDO_Q4_K: case SSDO_Q5_K: case SSDO_Q6_K:
+        case SSDO_Q8_K: case SSDO_IQ4_XS: return 256;
         default: return 0;
     }
 }
@@ -35,6 +36,13 @@ size_t ssdo_type_size(int dtype) {
         case SSDO_Q8_0: return 34;                      /* 2 + 32 */
         case SSDO_Q4_K: return 2 + 2 + 12 + 256 / 2;    /* 144 */
         case SSDO_Q6_K: return 256 / 2 + 256 / 4 + 256 / 16 + 2; /* 210 */
+        case SSDO_Q2_K: return 2 + 2 + 16 + 64;         /* 84 */
+        case SSDO_Q3_K: return 256 / 8 + 256 / 4 + 12 + 2; /* 110: the block matvec_q3_k_cpu
+                                  reads (compute.rs:798); gguf.rs:127 writes 256/8*3 (174) */
+        case SSDO_Q5_K: return 2 + 2 + 12 + 256 / 8 + 256 / 2; /* 176 */
+        case SSDO_Q8_K: return 4 + 256 + 16 * 2;        /* 292 */
+        case SSDO_IQ4_NL: return 2 + 16;                /* 18 */
+        case SSDO_IQ4_XS: return 2 + 2 + 128 + 16;      /* 148 */
         default: return 0;
     }
 }
@@ -316,6 +324,218 @@ static void mv_q8_0(const uint8_t* w, const float* x, size_t r0, size_t r1, size
     }
 }
 
+/* The reference's other matvec types (compute.rs:796-1077, 2256-2285). Each
+ * keeps the reference's block layout, element order and expression order. */
+
+static void mv_q3_k(const uint8_t* w, const float* x, size_t r0, size_t r1, size_t in_dim,
+                    float* y) {
+    /* src/metal/compute.rs:796-840: hmask[32] @0, qs[64] @32, sc[12] @96, d f16 @108 */
+    const size_t bs = 256, bb = 110, bpr = in_dim / bs;
+    for (size_t row = r0; row < r1; row++) {
+        size_t row_off = row * bpr * bb;
+        float sum = 0.0f;
+        for (size_t b = 0; b < bpr; b++) {
+            size_t boff = row_off + b * bb;
+            const uint8_t* hmask = w + boff;
+            const uint8_t* qs = w + boff + 32;
+            const uint8_t* sc = w + boff + 96;
+            float d = le_f16(w + boff + 108);
+            size_t xb = b * bs;
+            for (size_t sb = 0; sb < 16; sb++) {
+                unsigned low4 = (sc[sb / 2] >> ((sb & 1) * 4)) & 0x0Fu;
+                unsigned hi2 = (sc[8 + sb / 4] >> ((sb % 4) * 2)) & 0x03u;
+                int scale_val = (int)(low4 | (hi2 << 4));
+                if (scale_val >= 32) scale_val -= 64;
+                float sc_f = d * (float)scale_val;
+                for (size_t j = 0; j < 16; j++) {
+                    size_t idx = sb * 16 + j;
+                    unsigned low2 = (qs[idx / 4] >> ((idx % 4) * 2)) & 0x03u;
+                    unsigned hbit = (hmask[idx / 8] >> (idx % 8)) & 1u;
+                    int q = (int)(low2 | (hbit << 2)) - 4;
+                    sum += sc_f * (float)q * x[xb + idx];
+                }
+            }
+        }
+        y[row] = sum;
+    }
+}
+
+static void mv_q5_k(const uint8_t* w, const float* x, size_t r0, size_t r1, size_t in_dim,
+                    float* y) {
+    /* src/metal/compute.rs:845-902: d @0, dmin @2, sc[12] @4 (Q4_K packing),
+     * qh[32] @16, ql[128] @48 */
+    const size_t bs = 256, bb = 176, bpr = in_dim / bs;
+    for (size_t row = r0; row < r1; row++) {
+        size_t row_off = row * bpr * bb;
+        float sum = 0.0f;
+        for (size_t b = 0; b < bpr; b++) {
+            size_t boff = row_off + b * bb;
+            float d = le_f16(w + boff);
+            float dmin = le_f16(w + boff + 2);
+            const uint8_t* sc = w + boff + 4;
+            const uint8_t* qh = w + boff + 16;
+            const uint8_t* ql = w + boff + 48;
+            size_t xb = b * bs;
+            for (unsigned sb = 0; sb < 8; sb++) {
+                unsigned s, m;
+                q4k_scale_min(sc, sb, &s, &m);
+                float scale = d * (float)s;
+                float min_val = dmin * (float)m;
+                size_t qs_off = sb * 16;
+                for (size_t j = 0; j < 16; j++) {
+                    size_t idx0 = sb * 32 + j * 2, idx1 = idx0 + 1;
+                    uint8_t bv = ql[qs_off + j];
+                    unsigned low0 = bv & 0x0Fu, low1 = (bv >> 4) & 0x0Fu;
+                    unsigned hbit0 = (qh[idx0 / 8] >> (idx0 % 8)) & 1u;
+                    unsigned hbit1 = (qh[idx1 / 8] >> (idx1 % 8)) & 1u;
+                    float v0 = scale * (float)(low0 | (hbit0 << 4)) - min_val;
+                    float v1 = scale * (float)(low1 | (hbit1 << 4)) - min_val;
+                    sum += v0 * x[xb + idx0] + v1 * x[xb + idx1];
+                }
+            }
+        }
+        y[row] = sum;
+    }
+}
+
+static void mv_q2_k(const uint8_t* w, const float* x, size_t r0, size_t r1, size_t in_dim,
+                    float* y) {
+    /* src/metal/compute.rs:930-966: d @0, dmin @2, sc[16] @4 (low nibble scale,
+     * high nibble min), qs[64] @20 (2 bits, 4 per byte) */
+    const size_t bs = 256, bb = 84, bpr = in_dim / bs;
+    for (size_t row = r0; row < r1; row++) {
+        size_t row_off = row * bpr * bb;
+        float sum = 0.0f;
+        for (size_t b = 0; b < bpr; b++) {
+            size_t boff = row_off + b * bb;
+            float d = le_f16(w + boff);
+            float dmin = le_f16(w + boff + 2);
+            const uint8_t* sc = w + boff + 4;
+            const uint8_t* qs = w + boff + 20;
+            size_t xb = b * bs;
+            for (size_t sb = 0; sb < 16; sb++) {
+                float scale = d * (float)(sc[sb] & 0x0F);
+                float min_val = dmin * (float)((sc[sb] >> 4) & 0x0F);
+                for (size_t j = 0; j < 16; j++) {
+                    size_t idx = sb * 16 + j;
+                    float q = (float)((qs[idx / 4] >> ((idx % 4) * 2)) & 0x03);
+                    sum += (scale * q - min_val) * x[xb + idx];
+                }
+            }
+        }
+        y[row] = sum;
+    }
+}
+
+static inline float le_f32(const uint8_t* p) {
+    uint32_t bits = (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) |
+                    ((uint32_t)p[3] << 24);
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+static void mv_q8_k(const uint8_t* w, const float* x, size_t r0, size_t r1, size_t in_dim,
+                    float* y) {
+    /* src/metal/compute.rs:971-993: d f32 @0, int8 qs[256] @4, bsums unused */
+    const size_t bs = 256, bb = 292, bpr = in_dim / bs;
+    for (size_t row = r0; row < r1; row++) {
+        size_t row_off = row * bpr * bb;
+        float sum = 0.0f;
+        for (size_t b = 0; b < bpr; b++) {
+            size_t boff = row_off + b * bb;
+            float d = le_f32(w + boff);
+            size_t xb = b * bs;
+            for (size_t j = 0; j < 256; j++) sum += d * (float)(int8_t)w[boff + 4 + j] * x[xb + j];
+        }
+        y[row] = sum;
+    }
+}
+
+/* IQ4_NL non-linear code book, src/metal/compute.rs:997-999 (a format constant) */
+static const int8_t kIq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                  1,    13,   25,  38,  53,  69,  89,  113};
+
+static void mv_iq4_nl(const uint8_t* w, const float* x, size_t r0, size_t r1, size_t in_dim,
+                      float* y) {
+    /* src/metal/compute.rs:1004-1028: d f16 @0, qs[16] @2, elements 2j / 2j+1
+     * from the low / high nibble of qs[j] through the code book */
+    const size_t bs = 32, bb = 18, bpr = in_dim / bs;
+    for (size_t row = r0; row < r1; row++) {
+        size_t row_off = row * bpr * bb;
+        float sum = 0.0f;
+        for (size_t b = 0; b < bpr; b++) {
+            size_t boff = row_off + b * bb;
+            float d = le_f16(w + boff);
+            size_t xb = b * bs;
+            for (size_t j = 0; j < 16; j++) {
+                uint8_t bv = w[boff + 2 + j];
+                sum += d * (float)kIq4nl[bv & 0x0F] * x[xb + 2 * j];
+                sum += d * (float)kIq4nl[(bv >> 4) & 0x0F] * x[xb + 2 * j + 1];
+            }
+        }
+        y[row] = sum;
+    }
+}
+
+static void mv_iq4_xs(const uint8_t* w, const float* x, size_t r0, size_t r1, size_t in_dim,
+                      float* y) {
+    /* src/metal/compute.rs:1034-1077: d f16 @0, scales_h u16 @2, scales_l u16[8]
+     * @4 (sub-block sb: nibble sb%2 of word sb/2), qs[128] @20; scale =
+     * (sl | sh << 4) - 32 */
+    const size_t bs = 256, bb = 148, bpr = in_dim / bs;
+    for (size_t row = r0; row < r1; row++) {
+        size_t row_off = row * bpr * bb;
+        float sum = 0.0f;
+        for (size_t b = 0; b < bpr; b++) {
+            size_t boff = row_off + b * bb;
+            float d = le_f16(w + boff);
+            unsigned scales_h = (unsigned)w[boff + 2] | ((unsigned)w[boff + 3] << 8);
+            for (size_t sb = 0; sb < 8; sb++) {
+                size_t sl_idx = sb / 2;
+                unsigned sl_word = (unsigned)w[boff + 4 + sl_idx * 2] |
+                                   ((unsigned)w[boff + 5 + sl_idx * 2] << 8);
+                int sl = (sb % 2 == 0) ? (int)(sl_word & 0x0F) : (int)((sl_word >> 4) & 0x0F);
+                int sh = (int)((scales_h >> (2 * sb)) & 0x03);
+                float scale = (float)(sl | (sh << 4)) - 32.0f;
+                size_t qs_off = boff + 20 + sb * 16;
+                size_t xb = b * bs + sb * 32;
+                for (size_t j = 0; j < 16; j++) {
+                    uint8_t bv = w[qs_off + j];
+                    sum += d * scale * (float)kIq4nl[bv & 0x0F] * x[xb + 2 * j];
+                    sum += d * scale * (float)kIq4nl[(bv >> 4) & 0x0F] * x[xb + 2 * j + 1];
+                }
+            }
+        }
+        y[row] = sum;
+    }
+}
+
+static void mv_f16(const uint8_t* w, const float* x, size_t r0, size_t r1, size_t in_dim,
+                   float* y) {
+    /* src/metal/compute.rs:2272-2285 */
+    for (size_t row = r0; row < r1; row++) {
+        size_t row_off = row * in_dim * 2;
+        float sum = 0.0f;
+        for (size_t col = 0; col < in_dim; col++) sum += le_f16(w + row_off + col * 2) * x[col];
+        y[row] = sum;
+    }
+}
+
+static void mv_bf16(const uint8_t* w, const float* x, size_t r0, size_t r1, size_t in_dim,
+                    float* y) {
+    /* src/metal/compute.rs:2249-2269 */
+    for (size_t row = r0; row < r1; row++) {
+        size_t row_off = row * in_dim * 2;
+        float sum = 0.0f;
+        for (size_t col = 0; col < in_dim; col++) {
+            const uint8_t* p = w + row_off + col * 2;
+            sum += ssdo_bf16_to_f32((uint16_t)(p[0] | ((uint16_t)p[1] << 8))) * x[col];
+        }
+        y[row] = sum;
+    }
+}
+
 typedef void (*mv_fn)(const uint8_t*, const float*, size_t, size_t, size_t, float*);
 
 static mv_fn pick_mv(int dtype) {
@@ -325,6 +545,14 @@ static mv_fn pick_mv(int dtype) {
         case SSDO_Q4_K: return mv_q4_k;
         case SSDO_Q6_K: return mv_q6_k;
         case SSDO_Q8_0: return mv_q8_0;
+        case SSDO_Q3_K: return mv_q3_k;
+        case SSDO_Q5_K: return mv_q5_k;
+        case SSDO_Q2_K: return mv_q2_k;
+        case SSDO_Q8_K: return mv_q8_k;
+        case SSDO_IQ4_NL: return mv_iq4_nl;
+        case SSDO_IQ4_XS: return mv_iq4_xs;
+        case SSDO_BF16: return mv_bf16;
+        case SSDO_F16: return mv_f16;
         default: return NULL;
     }
 }
@@ -377,6 +605,110 @@ int ssdo_matvec_quantized_mt(const uint8_t* w, const float* x, size_t out_dim, s
     return 0;
 }
 
+/* Element values of one row as the matvec functions above form them before the
+ * multiply by x (for the exact sums; the dequant path covers the other types). */
+static void row_elements(int dtype, const uint8_t* r, size_t row_bytes, size_t k, float* e) {
+    size_t bpr = k / 256;
+    switch (dtype) {
+        case SSDO_Q3_K:
+            for (size_t b = 0; b < bpr; b++) {
+                const uint8_t* p = r + b * 110;
+                float d = le_f16(p + 108);
+                for (size_t sb = 0; sb < 16; sb++) {
+                    unsigned low4 = (p[96 + sb / 2] >> ((sb & 1) * 4)) & 0x0Fu;
+                    unsigned hi2 = (p[104 + sb / 4] >> ((sb % 4) * 2)) & 0x03u;
+                    int sv = (int)(low4 | (hi2 << 4));
+                    if (sv >= 32) sv -= 64;
+                    float sc_f = d * (float)sv;
+                    for (size_t j = 0; j < 16; j++) {
+                        size_t idx = sb * 16 + j;
+                        unsigned low2 = (p[32 + idx / 4] >> ((idx % 4) * 2)) & 0x03u;
+                        unsigned hbit = (p[idx / 8] >> (idx % 8)) & 1u;
+                        e[b * 256 + idx] = sc_f * (float)((int)(low2 | (hbit << 2)) - 4);
+                    }
+                }
+            }
+            return;
+        case SSDO_Q5_K:
+            for (size_t b = 0; b < bpr; b++) {
+                const uint8_t* p = r + b * 176;
+                float d = le_f16(p), dmin = le_f16(p + 2);
+                for (unsigned sb = 0; sb < 8; sb++) {
+                    unsigned sv, mv;
+                    q4k_scale_min(p + 4, sb, &sv, &mv);
+                    float scale = d * (float)sv, min_val = dmin * (float)mv;
+                    for (size_t j = 0; j < 32; j++) {
+                        size_t idx = sb * 32 + j;
+                        uint8_t bv = p[48 + sb * 16 + j / 2];
+                        unsigned lo = (j & 1) ? ((bv >> 4) & 0x0Fu) : (bv & 0x0Fu);
+                        unsigned hb = (p[16 + idx / 8] >> (idx % 8)) & 1u;
+                        e[b * 256 + idx] = scale * (float)(lo | (hb << 4)) - min_val;
+                    }
+                }
+            }
+            return;
+        case SSDO_Q2_K:
+            for (size_t b = 0; b < bpr; b++) {
+                const uint8_t* p = r + b * 84;
+                float d = le_f16(p), dmin = le_f16(p + 2);
+                for (size_t sb = 0; sb < 16; sb++) {
+                    float scale = d * (float)(p[4 + sb] & 0x0F);
+                    float min_val = dmin * (float)((p[4 + sb] >> 4) & 0x0F);
+                    for (size_t j = 0; j < 16; j++) {
+                        size_t idx = sb * 16 + j;
+                        float q = (float)((p[20 + idx / 4] >> ((idx % 4) * 2)) & 0x03);
+                        e[b * 256 + idx] = scale * q - min_val;
+                    }
+                }
+            }
+            return;
+        case SSDO_Q8_K:
+            for (size_t b = 0; b < bpr; b++) {
+                float d = le_f32(r + b * 292);
+                for (size_t j = 0; j < 256; j++) e[b * 256 + j] = d * (float)(int8_t)r[b * 292 + 4 + j];
+            }
+            return;
+        case SSDO_IQ4_NL:
+            for (size_t b = 0; b < k / 32; b++) {
+                const uint8_t* p = r + b * 18;
+                float d = le_f16(p);
+                for (size_t j = 0; j < 16; j++) {
+                    e[b * 32 + 2 * j] = d * (float)kIq4nl[p[2 + j] & 0x0F];
+                    e[b * 32 + 2 * j + 1] = d * (float)kIq4nl[(p[2 + j] >> 4) & 0x0F];
+                }
+            }
+            return;
+        case SSDO_IQ4_XS:
+            for (size_t b = 0; b < bpr; b++) {
+                const uint8_t* p = r + b * 148;
+                float d = le_f16(p);
+                unsigned sh_all = (unsigned)p[2] | ((unsigned)p[3] << 8);
+                for (size_t sb = 0; sb < 8; sb++) {
+                    unsigned slw = (unsigned)p[4 + (sb / 2) * 2] | ((unsigned)p[5 + (sb / 2) * 2] << 8);
+                    int sl = (sb % 2 == 0) ? (int)(slw & 0x0F) : (int)((slw >> 4) & 0x0F);
+                    int sh = (int)((sh_all >> (2 * sb)) & 0x03);
+                    float scale = (float)(sl | (sh << 4)) - 32.0f;
+                    for (size_t j = 0; j < 16; j++) {
+                        uint8_t bv = p[20 + sb * 16 + j];
+                        e[b * 256 + sb * 32 + 2 * j] = d * scale * (float)kIq4nl[bv & 0x0F];
+                        e[b * 256 + sb * 32 + 2 * j + 1] = d * scale * (float)kIq4nl[(bv >> 4) & 0x0F];
+                    }
+                }
+            }
+            return;
+        default:
+            ssdo_dequantize_to_f32(dtype, r, row_bytes, k, e);
+    }
+}
+
+int ssdo_matvec_elements(const uint8_t* w, size_t out_dim, size_t in_dim, int dtype, float* e) {
+    size_t bs = ssdo_block_size(dtype), tb = ssdo_type_size(dtype);
+    if (!pick_mv(dtype)) return 1;
+    size_t bpr = in_dim / bs, k = bpr * bs, row_bytes = bpr * tb;
+    for (size_t r = 0; r < out_dim; r++) row_elements(dtype, w + r * row_bytes, row_bytes, k, e + r * k);
+    return 0;
+}
+
 int ssdo_matvec_exact(const uint8_t* w, const float* x, size_t out_dim, size_t in_dim, int dtype,
                       double* y) {
     size_t bs = ssdo_block_size(dtype), tb = ssdo_type_size(dtype);
@@ -387,7 +719,7 @@ int ssdo_matvec_exact(const uint8_t* w, const float* x, size_t out_dim, size_t i
     size_t bpr = in_dim / bs, k = bpr * bs, row_bytes = bpr * tb;
     float* e = (float*)malloc(k * sizeof(float));
     for (size_t r = 0; r < out_dim; r++) {
-        ssdo_dequantize_to_f32(dtype, w + r * row_bytes, row_bytes, k, e);
+        row_elements(dtype, w + r * row_bytes, row_bytes, k, e);
         double s = 0.0;
         for (size_t i = 0; i < k; i++) s += (double)e[i] * (double)x[i];
         y[r] = s;

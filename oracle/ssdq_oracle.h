@@ -25,7 +25,8 @@ extern "C" {
 /* GgmlType ids, src/model/gguf.rs:17-48 */
 enum {
     SSDO_F32 = 0, SSDO_F16 = 1, SSDO_Q4_0 = 2, SSDO_Q8_0 = 8,
-    SSDO_Q4_K = 12, SSDO_Q6_K = 14, SSDO_BF16 = 30
+    SSDO_Q2_K = 10, SSDO_Q3_K = 11, SSDO_Q4_K = 12, SSDO_Q5_K = 13, SSDO_Q6_K = 14,
+    SSDO_Q8_K = 15, SSDO_IQ4_NL = 20, SSDO_IQ4_XS = 23, SSDO_BF16 = 30
 };
 
 /* block_size / type_size, src/model/gguf.rs:87-135 (0 for unknown ids) */
@@ -65,6 +66,9 @@ int ssdo_matvec_quantized_mt(const uint8_t* w, const float* x, size_t out_dim, s
  * (double)elem * (double)x in double precision, where elem is the reference's
  * bit-exact fp32 element value.  Used only to tell apart the reference's own
  * fp32 rounding error from a device error. */
+/* The element values each matvec multiplies by x, [out_dim][whole blocks of in_dim]
+ * (1 and nothing written for types the matvec does not support). */
+int ssdo_matvec_elements(const uint8_t* w, size_t out_dim, size_t in_dim, int dtype, float* e);
 int ssdo_matvec_exact(const uint8_t* w, const float* x, size_t out_dim, size_t in_dim, int dtype,
                       double* y);
 

@@ -33,6 +33,7 @@ def lib():
             "ssdo_matvec_quantized": (_i, [_vp, _vp, _sz, _sz, _i, _vp]),
             "ssdo_matvec_quantized_mt": (_i, [_vp, _vp, _sz, _sz, _i, _vp, _i]),
             "ssdo_matvec_exact": (_i, [_vp, _vp, _sz, _sz, _i, _vp]),
+            "ssdo_matvec_elements": (_i, [_vp, _sz, _sz, _i, _vp]),
             "ssdo_quantize_rows_int8": (None, [_vp, _sz, _sz, _vp, _vp]),
             "ssdo_dequantize_rows_int8": (None, [_vp, _vp, _sz, _sz, _vp]),
             "ssdo_flash_attention_f32": (None, [_vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _vp]),
@@ -94,6 +95,15 @@ def matvec_exact(dtype, w, x, out_dim, in_dim):
     y = np.empty(out_dim, np.float64)
     lib().ssdo_matvec_exact(w.ctypes.data, x.ctypes.data, out_dim, in_dim, dtype, y.ctypes.data)
     return y
+
+
+def matvec_elements(dtype, w, out_dim, in_dim):
+    """The element values each matvec multiplies by x, [out_dim, whole blocks of in_dim]."""
+    w = _c(w, np.uint8)
+    k = (in_dim // block_size(dtype)) * block_size(dtype)
+    e = np.zeros((out_dim, k), np.float32)
+    rc = lib().ssdo_matvec_elements(w.ctypes.data, out_dim, in_dim, dtype, e.ctypes.data)
+    return e, rc
 
 
 def quantize_rows(data, n_rows, dim):

@@ -9,6 +9,12 @@ Distributions follow the benchmark configurations of the reference path:
         code bytes
   Q6_K  d ~ U[0.001, 0.01] -> f16, random ql / qh bytes, int8 scales uniform in
         [-32, 31] (6-bit range)
+  Q2_K / Q3_K / Q5_K / IQ4_NL / IQ4_XS  f16 scales ~ U[0.001, 0.01]
+        (IQ4_NL U[0.002, 0.02], IQ4_XS U[0.0001, 0.001]), every other byte
+        uniform random (scale fields included)
+  Q8_K  f32 d ~ U[0.001, 0.01], int8 codes uniform in [-127, 127], bsums the
+        16-element code sums
+  F16 / BF16  N(0, 0.05) rounded to the type
   activations / K / V / Q  ~ N(0, 1) f32; bf16 activations are the f32 draws
         rounded to nearest even.
 Both the device path and the CPU oracle consume the same bytes, so any seeded
@@ -18,9 +24,11 @@ from __future__ import annotations
 
 import numpy as np
 
-from . import Q4_0, Q8_0, Q4_K, Q6_K
+from . import BF16, F16, IQ4_NL, IQ4_XS, Q2_K, Q3_K, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, Q8_K
 
-BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
+BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210), Q2_K: (256, 84),
+         Q3_K: (256, 110), Q5_K: (256, 176), Q8_K: (256, 292), IQ4_NL: (32, 18),
+         IQ4_XS: (256, 148), F16: (1, 2), BF16: (1, 2)}
 
 
 def rng(seed: int) -> np.random.Generator:
@@ -51,6 +59,26 @@ def quant_weights(dtype: int, out_dim: int, in_dim: int, seed: int) -> np.ndarra
         blk[:, 0:192] = g.integers(0, 256, (nb, 192), dtype=np.uint8)
         blk[:, 192:208] = g.integers(-32, 32, (nb, 16), dtype=np.int16).astype(np.int8).view(np.uint8)
         blk[:, 208:210] = _f16_bytes(g.uniform(0.001, 0.01, nb).astype(np.float32))
+    elif dtype in (Q2_K, Q5_K):  # d, dmin first
+        blk[:, 0:2] = _f16_bytes(g.uniform(0.001, 0.01, nb).astype(np.float32))
+        blk[:, 2:4] = _f16_bytes(g.uniform(0.001, 0.01, nb).astype(np.float32))
+        blk[:, 4:] = g.integers(0, 256, (nb, bb - 4), dtype=np.uint8)
+    elif dtype == Q3_K:  # d last
+        blk[:, 0:108] = g.integers(0, 256, (nb, 108), dtype=np.uint8)
+        blk[:, 108:110] = _f16_bytes(g.uniform(0.001, 0.01, nb).astype(np.float32))
+    elif dtype == Q8_K:
+        blk[:, 0:4] = g.uniform(0.001, 0.01, nb).astype(np.float32).view(np.uint8).reshape(-1, 4)
+        q = g.integers(-127, 128, (nb, 256), dtype=np.int16)
+        blk[:, 4:260] = q.astype(np.int8).view(np.uint8)
+        blk[:, 260:292] = q.reshape(nb, 16, 16).sum(axis=2).astype(np.int16).view(np.uint8)
+    elif dtype in (IQ4_NL, IQ4_XS):
+        lo, hi = (0.002, 0.02) if dtype == IQ4_NL else (0.0001, 0.001)
+        blk[:, 0:2] = _f16_bytes(g.uniform(lo, hi, nb).astype(np.float32))
+        blk[:, 2:] = g.integers(0, 256, (nb, bb - 2), dtype=np.uint8)
+    elif dtype in (F16, BF16):
+        v = (g.standard_normal(nb, dtype=np.float32) * np.float32(0.05)).astype(np.float32)
+        bits = v.astype(np.float16).view(np.uint16) if dtype == F16 else f32_to_bf16_bits(v)
+        return bits.view(np.uint8).reshape(-1)
     else:
         raise ValueError(f"unsupported dtype {dtype}")
     return blk.reshape(-1)

@@ -52,8 +52,14 @@ extern "C" {
 #define SSDQ_TYPE_F16 1
 #define SSDQ_TYPE_Q4_0 2
 #define SSDQ_TYPE_Q8_0 8
+#define SSDQ_TYPE_Q2_K 10
+#define SSDQ_TYPE_Q3_K 11
 #define SSDQ_TYPE_Q4_K 12
+#define SSDQ_TYPE_Q5_K 13
 #define SSDQ_TYPE_Q6_K 14
+#define SSDQ_TYPE_Q8_K 15
+#define SSDQ_TYPE_IQ4_NL 20
+#define SSDQ_TYPE_IQ4_XS 23
 #define SSDQ_TYPE_BF16 30
 
 typedef void* ssdq_stream_t; /* a hipStream_t; NULL = default stream */
@@ -63,7 +69,9 @@ typedef struct ssdq_ctx ssdq_ctx;
 int ssdq_abi_version(void);
 /* Message of the last failing call on this thread ("" if none). */
 const char* ssdq_last_error(void);
-/* GgmlType::block_size / type_size, src/model/gguf.rs:87-135 (0 if unknown). */
+/* GgmlType::block_size / type_size, src/model/gguf.rs:87-135 (0 if unknown),
+ * except Q3_K: 110 bytes, the block matvec_q3_k_cpu reads (compute.rs:798),
+ * where gguf.rs:127 computes 174. */
 size_t ssdq_block_size(int dtype);
 size_t ssdq_type_size(int dtype);
 /* Bytes of one weight row of in_dim elements: (in_dim / block) * type_size,
@@ -106,8 +114,10 @@ int ssdq_dequantize_to_f32(ssdq_ctx* ctx, int dtype, const uint8_t* data, size_t
  * Replaces MetalCompute::matvec_quantized (compute.rs:157-191), MetalGpu::
  * matvec_q4_0/q4_k/q6_k/q8_0 (gpu.rs:396-428) and matvec_quantized_cpu
  * (compute.rs:648-677); batch > 1 replaces the per-row loop of
- * batch_scheduler.rs:242-276. Unsupported dtypes zero-fill y and return
- * SSDQ_WARN_UNSUPPORTED_ZEROED. */
+ * batch_scheduler.rs:242-276. Types: Q4_0, Q8_0, Q4_K, Q6_K and the other
+ * matvec_quantized types Q2_K, Q3_K, Q5_K, Q8_K, IQ4_NL, IQ4_XS, F16, BF16
+ * (matvec_*_cpu, compute.rs:796-1077, 2249-2285). Other dtypes (F32 included,
+ * as in compute.rs:672-675) zero-fill y and return SSDQ_WARN_UNSUPPORTED_ZEROED. */
 int ssdq_matvec_dev(int dtype, const void* w, const float* x, float* y, size_t out_dim,
                     size_t in_dim, size_t batch, ssdq_stream_t stream);
 /* Host twin with the MetalCompute::matvec_quantized contract

@@ -41,6 +41,9 @@ bool supported_quant(int dtype) {
          dtype == SSDQ_TYPE_Q6_K;
 }
 
+// matvec_quantized_cpu's match arms (compute.rs:655-671)
+bool supported_matvec(int dtype) { return supported_quant(dtype) || ssdq::matvec_ext_type(dtype); }
+
 bool float_type(int dtype) {
   return dtype == SSDQ_TYPE_F32 || dtype == SSDQ_TYPE_F16 || dtype == SSDQ_TYPE_BF16;
 }
@@ -138,8 +141,9 @@ const char* ssdq_last_error(void) { return g_err; }
 size_t ssdq_block_size(int dtype) {
   switch (dtype) {
     case SSDQ_TYPE_F32: case SSDQ_TYPE_F16: case SSDQ_TYPE_BF16: return 1;
-    case SSDQ_TYPE_Q4_0: case SSDQ_TYPE_Q8_0: return 32;
-    case SSDQ_TYPE_Q4_K: case SSDQ_TYPE_Q6_K: return 256;
+    case SSDQ_TYPE_Q4_0: case SSDQ_TYPE_Q8_0: case SSDQ_TYPE_IQ4_NL: return 32;
+    case SSDQ_TYPE_Q2_K: case SSDQ_TYPE_Q3_K: case SSDQ_TYPE_Q4_K: case SSDQ_TYPE_Q5_K:
+    case SSDQ_TYPE_Q6_K: case SSDQ_TYPE_Q8_K: case SSDQ_TYPE_IQ4_XS: return 256;
     default: return 0;
   }
 }
@@ -152,6 +156,12 @@ size_t ssdq_type_size(int dtype) {
     case SSDQ_TYPE_Q8_0: return 34;
     case SSDQ_TYPE_Q4_K: return 144;
     case SSDQ_TYPE_Q6_K: return 210;
+    case SSDQ_TYPE_Q2_K: return 84;
+    case SSDQ_TYPE_Q3_K: return 110;  // the matvec's block; gguf.rs:127 computes 174
+    case SSDQ_TYPE_Q5_K: return 176;
+    case SSDQ_TYPE_Q8_K: return 292;
+    case SSDQ_TYPE_IQ4_NL: return 18;
+    case SSDQ_TYPE_IQ4_XS: return 148;
     default: return 0;
   }
 }
@@ -237,7 +247,7 @@ static int matvec_common(int dtype, const void* w, const float* x, float* y, siz
       !fits_int(out_dim * batch) || !fits_int(in_dim * batch))
     return fail(SSDQ_ERR_INVALID_ARG, "%s: dimensions exceed 2^31", fn);
   hipStream_t s = (hipStream_t)stream;
-  if (!supported_quant(dtype)) {
+  if (!supported_matvec(dtype)) {
     hipError_t e = ssdq::launch_fill_zero(y, out_dim * batch, s);
     if (e != hipSuccess) return hip_fail(e, fn);
     fail(SSDQ_WARN_UNSUPPORTED_ZEROED, "%s: dtype %d unsupported, zero-filled", fn, dtype);
@@ -248,7 +258,9 @@ static int matvec_common(int dtype, const void* w, const float* x, float* y, siz
   if (((uintptr_t)x & 3) || ((uintptr_t)y & 3))
     return fail(SSDQ_ERR_INVALID_ARG, "%s: x and y must be 4-byte aligned", fn);
   hipError_t e = hipSuccess;
-  if (generic) {
+  if (ssdq::matvec_ext_type(dtype)) {
+    e = ssdq::launch_matvec_ext(dtype, (const uint8_t*)w, x, y, out_dim, in_dim, batch, s, generic);
+  } else if (generic) {
     e = ssdq::launch_matvec_generic(dtype, (const uint8_t*)w, x, y, out_dim, in_dim, batch, s);
   } else {
     const size_t wsb = ssdq::matvec_workspace_bytes(dtype, w, x, out_dim, in_dim, batch);
@@ -275,7 +287,7 @@ int ssdq_matvec_quantized(ssdq_ctx* c, const uint8_t* w_raw, size_t w_len, const
   if (!c) return fail(SSDQ_ERR_INVALID_ARG, "ssdq_matvec_quantized: ctx is NULL");
   if (out_dim == 0) return ok();
   if (!y) return fail(SSDQ_ERR_INVALID_ARG, "ssdq_matvec_quantized: y is NULL");
-  if (!supported_quant(dtype)) {
+  if (!supported_matvec(dtype)) {
     memset(y, 0, out_dim * sizeof(float));
     fail(SSDQ_WARN_UNSUPPORTED_ZEROED, "ssdq_matvec_quantized: dtype %d unsupported, zeros", dtype);
     return SSDQ_WARN_UNSUPPORTED_ZEROED;

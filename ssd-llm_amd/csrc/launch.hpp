@@ -25,6 +25,13 @@ size_t matvec_workspace_bytes(int dtype, const void* w, const float* x, size_t o
 hipError_t launch_matvec_generic(int dtype, const uint8_t* w, const float* x, float* y,
                                  size_t out_dim, size_t in_dim, size_t batch, hipStream_t stream);
 
+// The reference's other matvec_quantized types (Q2_K, Q3_K, Q5_K, Q8_K, IQ4_NL,
+// IQ4_XS, F16, BF16), same contract as launch_matvec; generic forces the
+// byte-addressed kernel.
+bool matvec_ext_type(int dtype);
+hipError_t launch_matvec_ext(int dtype, const uint8_t* w, const float* x, float* y, size_t out_dim,
+                             size_t in_dim, size_t batch, hipStream_t stream, bool generic);
+
 hipError_t launch_kv_quantize(const float* in, int8_t* codes, float* scales, size_t n_rows,
                               size_t row_len, hipStream_t stream);
 hipError_t launch_kv_dequantize(const int8_t* codes, const float* scales, float* out,

@@ -44,6 +44,11 @@ def test_type_helpers():
         assert ssdq.row_bytes(dt, 4096) == 4096 // bs * ts
         assert ssdq.row_bytes(dt, 4096 + bs - 1) == 4096 // bs * ts  # partial block ignored
     assert ssdq.block_size(99) == 0 and ssdq.row_bytes(99, 4096) == 0
+    # the other matvec types agree with the oracle's table (Q3_K: 110-byte blocks)
+    import ssdq_oracle as o
+    for dt in ssdq.MATVEC_EXTRA_TYPES:
+        assert (ssdq.block_size(dt), ssdq.type_size(dt)) == (o.block_size(dt), o.type_size(dt)), dt
+    assert ssdq.type_size(ssdq.Q3_K) == 110
 
 
 def test_null_arguments_are_rejected_without_a_device():

@@ -223,6 +223,9 @@ def extras(torch, ssdq, synth, timer, np):
         ("q8_0_matvec_11008x4096_b8", ssdq.Q8_0, 11008, 4096, 8, 2),
         ("q6_k_matvec_4096x14336_b1", ssdq.Q6_K, 4096, 14336, 1, 3),
     ]
+    # the reference's other matvec_quantized types at the north-star shape
+    for k, dt in enumerate(ssdq.MATVEC_EXTRA_TYPES):
+        cases.append((f"{ssdq.TYPE_NAMES[dt].lower()}_matvec_14336x4096_b1", dt, 14336, 4096, 1, 6 + k))
     for name, dt, od, idim, b, cfg in cases:
         step, nbytes, _ = matvec_case(torch, ssdq, synth, dt, od, idim, b, cfg)
         t, _, n = timer.run(step, 200, 20)

@@ -129,10 +129,12 @@ __device__ __forceinline__ void load_group(const uint8_t* __restrict__ row, int 
 template <int F>
 __device__ __forceinline__ void decode_group(const uint32_t* raw, int g, float* u, float* S, float* O) {
   if constexpr (F == kF16) {
+    // converted explicitly: left to itself the compiler folds the widening
+    // into v_fma_mix_f32, which measured 2.5x slower here than cvt + fmac
 #pragma unroll
     for (int i = 0; i < 16; i++) {
-      u[2 * i] = f16_to_f32(raw[i] & 0xFFFFu);
-      u[2 * i + 1] = f16_to_f32(raw[i] >> 16);
+      u[2 * i] = __uint_as_float(opaque(__float_as_uint(f16_to_f32(raw[i] & 0xFFFFu))));
+      u[2 * i + 1] = __uint_as_float(opaque(__float_as_uint(f16_to_f32(raw[i] >> 16))));
     }
     S[0] = S[1] = 1.f;
     O[0] = O[1] = 0.f;

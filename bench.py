@@ -234,6 +234,45 @@ def extras(torch, ssdq, synth, timer, np):
                      "us": round(t / n * 1e6, 3)}
         torch.cuda.empty_cache()
 
+    # decode-layer ops on quantized weights (Llama-3-8B shapes, batch 1): the
+    # fused launch against the same projections as separate matvec launches
+    def layer_case(name, dts_rows, fused, n_embd=4096):
+        base = []
+        nbytes = 4 * n_embd
+        for i, (dt, rows) in enumerate(dts_rows):
+            w = torch.from_numpy(synth.quant_weights(dt, rows, n_embd, synth.seed(5, 8 + i))).cuda()
+            base.append((dt, w, rows, torch.empty(rows, device="cuda")))
+            nbytes += w.numel() + 4 * rows
+        n = copies_for(nbytes)  # weights rotated over copies larger than 2x the last-level cache
+        sets = [base] + [[(dt, w.clone(), r, y) for dt, w, r, y in base] for _ in range(n - 1)]
+        x = torch.randn(n_embd, device="cuda")
+        tf, _, nf = timer.run(lambda i: fused(sets[i % n], x), 200, 20)
+        ts, _, ns = timer.run(lambda i: [ssdq.matvec(dt, w, x, y, r, n_embd) for dt, w, r, y in sets[i % n]],
+                              200, 20)
+        del sets, base
+        out[name] = {"us": round(tf / nf * 1e6, 3), "GB/s": round(nbytes / (tf / nf) / 1e9, 1),
+                     "pct_hbm_peak": round(100 * nbytes / (tf / nf) / 1e9 / HBM_PEAK_GBS, 2),
+                     "separate_matvecs_us": round(ts / ns * 1e6, 3)}
+        torch.cuda.empty_cache()
+
+    def qkv(m, x):
+        (dq, wq, rq, q), (_, wk, rk, k), (_, wv, rv, v) = m
+        ssdq.qkv_rope((dq,) * 3, (wq, wk, wv), x, q, k, v, rq, rk, 4096, 128, 4000, 500000.0)
+
+    def swi(m, x):
+        (dt, wg, r, h), (_, wu, _, _) = m
+        ssdq.swiglu(dt, wg, wu, x, h, r, 4096)
+
+    gnorm = torch.rand(4096, device="cuda") + 0.5
+
+    def head(m, x):
+        (dt, w, r, y), = m
+        ssdq.rmsnorm_matvec(dt, w, x, gnorm, 1e-5, y, r, 4096)
+
+    layer_case("decode_qkv_rope_q4k_4096", [(ssdq.Q4_K, 4096), (ssdq.Q4_K, 1024), (ssdq.Q4_K, 1024)], qkv)
+    layer_case("decode_swiglu_q4k_14336x4096", [(ssdq.Q4_K, 14336), (ssdq.Q4_K, 14336)], swi)
+    layer_case("decode_output_head_rmsnorm_q6k_128256x4096", [(ssdq.Q6_K, 128256)], head)
+
     # the synchronous host-pointer twin (MetalCompute::matvec_quantized contract):
     # W and x cross PCIe on every call, so this is the PCIe-inclusive rate
     w_host = synth.quant_weights(ssdq.Q4_K, 14336, 4096, synth.seed(3, 0))

@@ -126,6 +126,40 @@ int ssdq_matvec_dev(int dtype, const void* w, const float* x, float* y, size_t o
 int ssdq_matvec_quantized(ssdq_ctx* ctx, const uint8_t* w_raw, size_t w_len, const float* x,
                           size_t x_len, size_t out_dim, size_t in_dim, int dtype, float* y);
 
+/* ------------------------------------------------- decode-layer ops */
+/* The projections of one decode step on quantized weights, QKV+RoPE and
+ * SwiGLU each one kernel launch where the shapes allow it (one matrix type, whole rows of at most 128
+ * 64-element units of Q4_0 / Q8_0 / Q4_K / Q6_K, i.e. n_embd up to 8192 for
+ * Q4_K; otherwise the same result from separate launches).  Batch 1.
+ *
+ * q = Wq x, k = Wk x, v = Wv x, then RoPE on q and k (pairs (2i, 2i+1) of each
+ * head rotated by position * theta_base^(-2i/head_dim); head_dim 0: no RoPE).
+ * Replaces fused_qkv_rope_f32 / fused_qkv_f32 (compute.rs:273-326, gpu.rs:917,
+ * 997; CPU fused_qkv_rope_f32_cpu 509-534, rope_f32_multi_head 482-507) on
+ * quantized weights. q_dim, kv_dim even; head_dim even and dividing both. */
+int ssdq_qkv_rope_dev(int dtype_q, const void* wq, int dtype_k, const void* wk, int dtype_v,
+                      const void* wv, const float* x, float* q, float* k, float* v, size_t q_dim,
+                      size_t kv_dim, size_t n_embd, size_t head_dim, size_t position, float theta_base,
+                      ssdq_stream_t stream);
+/* h = silu(W_gate x) * (W_up x), silu(v) = v / (1 + exp(-v)): the gate / up
+ * half of the SwiGLU feed-forward (src/inference/feed_forward.rs:28-40,
+ * silu_f32 compute.rs:641-645; the reference's fused Metal kernel
+ * gpu.rs feed_forward_f32) on quantized weights. h has n_ff floats. */
+int ssdq_swiglu_dev(int dtype, const void* w_gate, const void* w_up, const float* x, float* h,
+                    size_t n_ff, size_t n_embd, ssdq_stream_t stream);
+/* y = W (x * inv_rms * norm_weight), inv_rms = 1 / sqrt(mean(x^2) + eps): the
+ * output head of fused_rmsnorm_linear_f32 (compute.rs:348-372, CPU 557-578,
+ * which fixes eps = 1e-5) on quantized weights, which the reference
+ * re-dequantizes every token (src/inference/transformer.rs:688-706). */
+int ssdq_rmsnorm_matvec_dev(int dtype, const void* w, const float* x, const float* norm_weight, float eps,
+                            float* y, size_t out_dim, size_t n_embd, ssdq_stream_t stream);
+/* h = x + residual (residual may be NULL; written to hidden_out unless NULL),
+ * out = h * inv_rms * weight: fused_post_attn_norm_f32 (compute.rs:328-346,
+ * CPU 536-555); with residual NULL, rmsnorm_f32 (compute.rs:193-202). out and
+ * hidden_out may alias x. */
+int ssdq_rmsnorm_dev(const float* x, const float* residual, const float* weight, float eps,
+                     float* hidden_out, float* out, size_t n, ssdq_stream_t stream);
+
 /* ------------------------------------------------------- prefill GEMM */
 /* Y[M, N] f32 = X[M, K] bf16 (row-major) times Q4_K W[N rows, K] (reference
  * layout), fp32 accumulate.  The reference has no GEMM: prefill is one matvec

@@ -990,3 +990,64 @@ void ssdo_gemm_q4k_bf16_exact(const uint8_t* w, const uint16_t* x, size_t M, siz
                               double* y, int nthreads) {
     gemm_run(w, x, M, N, K, NULL, y, nthreads);
 }
+
+/* ------------------------------------------------- decode-layer f32 ops */
+
+void ssdo_rope_multi_head(float* x, size_t len, size_t head_dim, size_t n_heads, size_t position,
+                          float theta_base) {
+    /* rope_f32_multi_head, src/metal/compute.rs:482-507 (f32 powf / sin_cos
+     * are libm's on this platform, as for the reference's Rust build) */
+    size_t half_dim = head_dim / 2;
+    for (size_t h = 0; h < n_heads; h++) {
+        size_t base = h * head_dim;
+        for (size_t i = 0; i < half_dim; i++) {
+            float freq = 1.0f / powf(theta_base, 2.0f * (float)i / (float)head_dim);
+            float angle = (float)position * freq;
+            float sin_val = sinf(angle), cos_val = cosf(angle);
+            size_t idx0 = base + i * 2, idx1 = idx0 + 1;
+            if (idx1 < len) {
+                float x0 = x[idx0], x1 = x[idx1];
+                x[idx0] = x0 * cos_val - x1 * sin_val;
+                x[idx1] = x0 * sin_val + x1 * cos_val;
+            }
+        }
+    }
+}
+
+void ssdo_silu(float* x, size_t n) {
+    /* silu_f32, src/metal/compute.rs:641-645 */
+    for (size_t i = 0; i < n; i++) x[i] = x[i] / (1.0f + expf(-x[i]));
+}
+
+static float sum_sq(const float* x, size_t n) {
+    float s = 0.0f; /* Iterator::sum: a serial fold from 0 */
+    for (size_t i = 0; i < n; i++) s += x[i] * x[i];
+    return s;
+}
+
+void ssdo_rmsnorm(float* x, const float* w, size_t n, float eps) {
+    /* rmsnorm_f32_fast_scalar, src/metal/compute.rs:580-589: x *= inv_rms * w */
+    float inv_rms = 1.0f / sqrtf(sum_sq(x, n) / (float)n + eps);
+    for (size_t i = 0; i < n; i++) x[i] *= inv_rms * w[i];
+}
+
+void ssdo_fused_post_attn_norm(float* hidden, const float* attn, const float* w, size_t n,
+                               float eps, float* out) {
+    /* fused_post_attn_norm_f32_cpu, src/metal/compute.rs:536-555:
+     * hidden += attn; out = hidden * inv_rms * w */
+    for (size_t i = 0; i < n; i++) hidden[i] += attn[i];
+    float inv_rms = 1.0f / sqrtf(sum_sq(hidden, n) / (float)n + eps);
+    for (size_t i = 0; i < n; i++) out[i] = hidden[i] * inv_rms * w[i];
+}
+
+int ssdo_fused_rmsnorm_linear(int dtype, const uint8_t* w, const float* x, const float* norm_w,
+                              size_t vocab, size_t n_embd, float* y) {
+    /* fused_rmsnorm_linear_f32_cpu, src/metal/compute.rs:557-578, with the
+     * projection through matvec_quantized_cpu: eps is fixed at 1e-5 there */
+    float inv_rms = 1.0f / sqrtf(sum_sq(x, n_embd) / (float)n_embd + 1e-5f);
+    float* xn = (float*)malloc((n_embd ? n_embd : 1) * sizeof(float));
+    for (size_t i = 0; i < n_embd; i++) xn[i] = x[i] * inv_rms * norm_w[i];
+    int rc = ssdo_matvec_quantized(w, xn, vocab, n_embd, dtype, y);
+    free(xn);
+    return rc;
+}

@@ -120,6 +120,19 @@ void ssdo_gemm_q4k_bf16(const uint8_t* w, const uint16_t* x, size_t M, size_t N,
 void ssdo_gemm_q4k_bf16_exact(const uint8_t* w, const uint16_t* x, size_t M, size_t N, size_t K,
                               double* y, int nthreads);
 
+/* Decode-layer f32 ops: rope_f32_multi_head (compute.rs:482-507), silu_f32
+ * (641-645), rmsnorm_f32_fast_scalar (580-589), fused_post_attn_norm_f32_cpu
+ * (536-555) and fused_rmsnorm_linear_f32_cpu (557-578, projection through
+ * matvec_quantized_cpu). */
+void ssdo_rope_multi_head(float* x, size_t len, size_t head_dim, size_t n_heads, size_t position,
+                          float theta_base);
+void ssdo_silu(float* x, size_t n);
+void ssdo_rmsnorm(float* x, const float* w, size_t n, float eps);
+void ssdo_fused_post_attn_norm(float* hidden, const float* attn, const float* w, size_t n,
+                               float eps, float* out);
+int ssdo_fused_rmsnorm_linear(int dtype, const uint8_t* w, const float* x, const float* norm_w,
+                              size_t vocab, size_t n_embd, float* y);
+
 #ifdef __cplusplus
 }
 #endif

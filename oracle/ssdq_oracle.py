@@ -34,6 +34,11 @@ def lib():
             "ssdo_matvec_quantized_mt": (_i, [_vp, _vp, _sz, _sz, _i, _vp, _i]),
             "ssdo_matvec_exact": (_i, [_vp, _vp, _sz, _sz, _i, _vp]),
             "ssdo_matvec_elements": (_i, [_vp, _sz, _sz, _i, _vp]),
+            "ssdo_rope_multi_head": (None, [_vp, _sz, _sz, _sz, _sz, ctypes.c_float]),
+            "ssdo_silu": (None, [_vp, _sz]),
+            "ssdo_rmsnorm": (None, [_vp, _vp, _sz, ctypes.c_float]),
+            "ssdo_fused_post_attn_norm": (None, [_vp, _vp, _vp, _sz, ctypes.c_float, _vp]),
+            "ssdo_fused_rmsnorm_linear": (_i, [_i, _vp, _vp, _vp, _sz, _sz, _vp]),
             "ssdo_quantize_rows_int8": (None, [_vp, _sz, _sz, _vp, _vp]),
             "ssdo_dequantize_rows_int8": (None, [_vp, _vp, _sz, _sz, _vp]),
             "ssdo_flash_attention_f32": (None, [_vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _vp]),
@@ -154,3 +159,63 @@ def gemm_q4k_bf16(w, x_bf16, M, N, K, threads=1, exact=False):
         y = np.empty(M * N, np.float32)
         lib().ssdo_gemm_q4k_bf16(w.ctypes.data, x.ctypes.data, M, N, K, y.ctypes.data, threads)
     return y
+
+
+def rope_multi_head(x, head_dim, n_heads, position, theta_base):
+    x = np.array(x, np.float32)
+    lib().ssdo_rope_multi_head(x.ctypes.data, x.size, head_dim, n_heads, position, theta_base)
+    return x
+
+
+def silu(x):
+    x = np.array(x, np.float32)
+    lib().ssdo_silu(x.ctypes.data, x.size)
+    return x
+
+
+def rmsnorm(x, w, eps):
+    x = np.array(x, np.float32)
+    w = _c(w, np.float32)
+    lib().ssdo_rmsnorm(x.ctypes.data, w.ctypes.data, x.size, eps)
+    return x
+
+
+def fused_post_attn_norm(hidden, attn, w, eps):
+    """(hidden after the residual add, normalized output)"""
+    hidden = np.array(hidden, np.float32)
+    attn = _c(attn, np.float32)
+    w = _c(w, np.float32)
+    out = np.empty_like(hidden)
+    lib().ssdo_fused_post_attn_norm(hidden.ctypes.data, attn.ctypes.data, w.ctypes.data, hidden.size,
+                                    eps, out.ctypes.data)
+    return hidden, out
+
+
+def fused_rmsnorm_linear(dtype, w, x, norm_w, vocab, n_embd):
+    w = _c(w, np.uint8)
+    x = _c(x, np.float32)
+    norm_w = _c(norm_w, np.float32)
+    y = np.empty(vocab, np.float32)
+    rc = lib().ssdo_fused_rmsnorm_linear(dtype, w.ctypes.data, x.ctypes.data, norm_w.ctypes.data,
+                                         vocab, n_embd, y.ctypes.data)
+    return y, rc
+
+
+def qkv_rope(dq, wq, dk, wk, dv, wv, x, q_dim, kv_dim, n_embd, head_dim, position, theta):
+    """fused_qkv_rope_f32_cpu (compute.rs:509-534) with the projections through
+    matvec_quantized_cpu; head_dim 0 leaves out the rotation (fused_qkv_f32_cpu)."""
+    q, _ = matvec(dq, wq, x, q_dim, n_embd)
+    k, _ = matvec(dk, wk, x, kv_dim, n_embd)
+    v, _ = matvec(dv, wv, x, kv_dim, n_embd)
+    if head_dim:
+        q = rope_multi_head(q, head_dim, q_dim // head_dim, position, theta)
+        k = rope_multi_head(k, head_dim, kv_dim // head_dim, position, theta)
+    return q, k, v
+
+
+def swiglu(dtype, w_gate, w_up, x, n_ff, n_embd):
+    """silu(W_gate x) * (W_up x), feed_forward.rs:28-40 with matvec_quantized_cpu."""
+    g, _ = matvec(dtype, w_gate, x, n_ff, n_embd)
+    g = silu(g)
+    u, _ = matvec(dtype, w_up, x, n_ff, n_embd)
+    return (g * u).astype(np.float32)

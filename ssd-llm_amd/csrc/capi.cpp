@@ -3,10 +3,12 @@
 #include <hip/hip_runtime.h>
 
 #include <climits>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
 #include <map>
+#include <tuple>
 #include <mutex>
 #include <utility>
 
@@ -56,15 +58,17 @@ struct Workspace {
   void* ptr = nullptr;
   size_t bytes = 0;
 };
+// slot 0: the kernels' own scratch; slot 1: intermediates of the unfused
+// decode-layer paths, which call kernels that use slot 0.
 std::mutex g_ws_mu;
-std::map<std::pair<int, void*>, Workspace> g_ws;
+std::map<std::tuple<int, void*, int>, Workspace> g_ws;
 
-hipError_t workspace_get(size_t bytes, hipStream_t stream, void** out) {
+hipError_t workspace_get(size_t bytes, hipStream_t stream, void** out, int slot = 0) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   std::lock_guard<std::mutex> lk(g_ws_mu);
-  Workspace& w = g_ws[{dev, (void*)stream}];
+  Workspace& w = g_ws[std::make_tuple(dev, (void*)stream, slot)];
   if (w.bytes < bytes) {
     // No allocation while the stream is being captured into a graph (it would
     // invalidate the capture): run the call once on this stream beforehand.
@@ -322,6 +326,136 @@ int ssdq_matvec_quantized(ssdq_ctx* c, const uint8_t* w_raw, size_t w_len, const
   if ((e = hipStreamSynchronize(c->stream)) != hipSuccess)
     return hip_fail(e, "ssdq_matvec_quantized: sync");
   return ok();
+}
+
+/* ------------------------------------------------- decode-layer ops */
+
+namespace {
+// 1 / theta^(2i/head_dim) with the C library's powf, the call the reference's
+// rope_f32_multi_head makes (compute.rs:494)
+void rope_freqs(ssdq::RopeFreq* r, int head_dim, float theta) {
+  for (int i = 0; i < 128; i++)
+    r->f[i] = i < head_dim / 2 ? 1.0f / powf(theta, 2.0f * (float)i / (float)head_dim) : 0.0f;
+}
+}  // namespace
+
+int ssdq_rmsnorm_dev(const float* x, const float* residual, const float* weight, float eps,
+                     float* hidden_out, float* out, size_t n, ssdq_stream_t stream) {
+  if (n == 0) return ok();
+  if (!x || !weight || !out) return fail(SSDQ_ERR_INVALID_ARG, "ssdq_rmsnorm_dev: NULL pointer");
+  if (!fits_int(n)) return fail(SSDQ_ERR_INVALID_ARG, "ssdq_rmsnorm_dev: n exceeds 2^31");
+  hipError_t e = ssdq::launch_rmsnorm(x, residual, weight, eps, hidden_out, out, (int)n, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "ssdq_rmsnorm_dev");
+  return ok();
+}
+
+int ssdq_qkv_rope_dev(int dtype_q, const void* wq, int dtype_k, const void* wk, int dtype_v,
+                      const void* wv, const float* x, float* q, float* k, float* v, size_t q_dim,
+                      size_t kv_dim, size_t n_embd, size_t head_dim, size_t position, float theta_base,
+                      ssdq_stream_t stream) {
+  const char* fn = "ssdq_qkv_rope_dev";
+  if (!wq || !wk || !wv || !x || !q || !k || !v) return fail(SSDQ_ERR_INVALID_ARG, "%s: NULL pointer", fn);
+  if (q_dim == 0 || kv_dim == 0 || (q_dim & 1) || (kv_dim & 1) || !fits_int(q_dim + 2 * kv_dim) ||
+      !fits_int(n_embd) || !fits_int(position))
+    return fail(SSDQ_ERR_INVALID_ARG, "%s: q_dim / kv_dim must be positive and even", fn);
+  if (head_dim && ((head_dim & 1) || head_dim > 256 || q_dim % head_dim || kv_dim % head_dim))
+    return fail(SSDQ_ERR_INVALID_ARG, "%s: head_dim must be even, at most 256 and divide q_dim and kv_dim", fn);
+  hipStream_t s = (hipStream_t)stream;
+  ssdq::RopeFreq freq;
+  rope_freqs(&freq, head_dim ? (int)head_dim : 2, theta_base);
+  if (dtype_q == dtype_k && dtype_k == dtype_v && supported_quant(dtype_q)) {
+    ssdq::MatvecFuse f{};
+    f.w0 = (const uint8_t*)wq; f.w1 = (const uint8_t*)wk; f.w2 = (const uint8_t*)wv;
+    f.y0 = q; f.y1 = k; f.y2 = v;
+    f.start1 = (int)q_dim;
+    f.start2 = (int)(q_dim + kv_dim);
+    f.rope_mask = head_dim ? 3u : 0u;
+    f.head_dim = head_dim ? (int)head_dim : 2;
+    f.position = (int)position;
+    f.freq = freq;
+    bool used = false;
+    hipError_t e = ssdq::launch_matvec_fused(dtype_q, f, (int)(q_dim + 2 * kv_dim), x, n_embd, s, &used);
+    if (e != hipSuccess) return hip_fail(e, fn);
+    if (used) return ok();
+  }
+  // unfused: three projections, then the rotation of q and k
+  int worst = SSDQ_OK;
+  const int dts[3] = {dtype_q, dtype_k, dtype_v};
+  const void* ws[3] = {wq, wk, wv};
+  float* ys[3] = {q, k, v};
+  const size_t rows[3] = {q_dim, kv_dim, kv_dim};
+  for (int i = 0; i < 3; i++) {
+    int rc = ssdq_matvec_dev(dts[i], ws[i], x, ys[i], rows[i], n_embd, 1, stream);
+    if (rc < 0) return rc;
+    if (rc > worst) worst = rc;
+  }
+  if (head_dim) {
+    hipError_t e = ssdq::launch_rope(q, (int)q_dim, (int)head_dim, (int)position, freq, s);
+    if (e == hipSuccess) e = ssdq::launch_rope(k, (int)kv_dim, (int)head_dim, (int)position, freq, s);
+    if (e != hipSuccess) return hip_fail(e, fn);
+  }
+  if (worst != SSDQ_OK) {
+    fail(worst, "%s: a projection dtype is unsupported, its output zero-filled", fn);
+    return worst;
+  }
+  return ok();
+}
+
+int ssdq_swiglu_dev(int dtype, const void* w_gate, const void* w_up, const float* x, float* h,
+                    size_t n_ff, size_t n_embd, ssdq_stream_t stream) {
+  const char* fn = "ssdq_swiglu_dev";
+  if (n_ff == 0) return ok();
+  if (!w_gate || !w_up || !x || !h) return fail(SSDQ_ERR_INVALID_ARG, "%s: NULL pointer", fn);
+  if (!fits_int(2 * n_ff) || !fits_int(n_embd)) return fail(SSDQ_ERR_INVALID_ARG, "%s: dimensions exceed 2^31", fn);
+  hipStream_t s = (hipStream_t)stream;
+  if (supported_quant(dtype)) {
+    ssdq::MatvecFuse f{};
+    f.w0 = (const uint8_t*)w_gate; f.w1 = (const uint8_t*)w_up;
+    f.y0 = h;
+    f.start1 = f.start2 = INT_MAX;
+    f.swiglu = 1;
+    f.head_dim = 2;
+    bool used = false;
+    hipError_t e = ssdq::launch_matvec_fused(dtype, f, (int)(2 * n_ff), x, n_embd, s, &used);
+    if (e != hipSuccess) return hip_fail(e, fn);
+    if (used) return ok();
+  }
+  void* tmp = nullptr;
+  hipError_t e = workspace_get(2 * n_ff * sizeof(float), s, &tmp, 1);
+  if (e != hipSuccess) return hip_fail(e, "ssdq_swiglu_dev: workspace");
+  float* g = (float*)tmp;
+  float* u = g + n_ff;
+  int rc = ssdq_matvec_dev(dtype, w_gate, x, g, n_ff, n_embd, 1, stream);
+  if (rc < 0) return rc;
+  rc = ssdq_matvec_dev(dtype, w_up, x, u, n_ff, n_embd, 1, stream);
+  if (rc < 0) return rc;
+  e = ssdq::launch_swiglu(g, u, h, (int)n_ff, s);
+  if (e != hipSuccess) return hip_fail(e, fn);
+  if (rc != SSDQ_OK) {
+    fail(rc, "%s: dtype %d unsupported, zeros", fn, dtype);
+    return rc;
+  }
+  return ok();
+}
+
+int ssdq_rmsnorm_matvec_dev(int dtype, const void* w, const float* x, const float* norm_weight, float eps,
+                            float* y, size_t out_dim, size_t n_embd, ssdq_stream_t stream) {
+  const char* fn = "ssdq_rmsnorm_matvec_dev";
+  if (out_dim == 0) return ok();
+  if (!w || !x || !norm_weight || !y) return fail(SSDQ_ERR_INVALID_ARG, "%s: NULL pointer", fn);
+  if (!fits_int(out_dim) || !fits_int(n_embd)) return fail(SSDQ_ERR_INVALID_ARG, "%s: dimensions exceed 2^31", fn);
+  hipStream_t s = (hipStream_t)stream;
+  // A separate norm kernel and the plain matvec: folding the norm into the
+  // matvec's staging of x measured slower (the norm weights queue ahead of
+  // every workgroup's first weight rows).
+  void* tmp = nullptr;
+  hipError_t e = workspace_get((n_embd ? n_embd : 1) * sizeof(float), s, &tmp, 1);
+  if (e != hipSuccess) return hip_fail(e, "ssdq_rmsnorm_matvec_dev: workspace");
+  if (n_embd) {
+    e = ssdq::launch_rmsnorm(x, nullptr, norm_weight, eps, nullptr, (float*)tmp, (int)n_embd, s);
+    if (e != hipSuccess) return hip_fail(e, fn);
+  }
+  return ssdq_matvec_dev(dtype, w, (const float*)tmp, y, out_dim, n_embd, 1, stream);
 }
 
 int ssdq_gemm_q4k_bf16_dev(const void* w, const uint16_t* x, float* y, size_t M, size_t N,

@@ -32,6 +32,45 @@ bool matvec_ext_type(int dtype);
 hipError_t launch_matvec_ext(int dtype, const uint8_t* w, const float* x, float* y, size_t out_dim,
                              size_t in_dim, size_t batch, hipStream_t stream, bool generic);
 
+// Decode-layer fusion of the batch-1 matvec: up to three matrices of one type
+// and row length sharing x ("segments", virtual rows concatenated; with swiglu
+// the rows of gate (w0) and up (w1) alternate and silu(g) * u goes to y0),
+// and RoPE on the output pairs of the segments in rope_mask.  Every segment
+// has an even row count.
+// RoPE frequencies theta^(-2i/head_dim), i < head_dim / 2, computed on the
+// host with the C library's powf (what the reference's f32::powf calls), so
+// the fp32 angle position * freq matches the reference bit for bit.
+struct RopeFreq {
+  float f[128];
+};
+
+struct MatvecFuse {
+  const uint8_t* w0;
+  const uint8_t* w1;
+  const uint8_t* w2;
+  float* y0;
+  float* y1;
+  float* y2;
+  int start1, start2;  // first virtual row of segments 1 and 2 (INT_MAX: absent)
+  int swiglu;
+  unsigned rope_mask;
+  int head_dim, position;
+  RopeFreq freq;
+};
+// One fused launch when the shapes allow it (Q4_0 / Q8_0 / Q4_K / Q6_K, whole
+// rows of at most 128 units, aligned operands); *used = false otherwise.
+hipError_t launch_matvec_fused(int dtype, const MatvecFuse& f, int total_rows, const float* x,
+                               size_t in_dim, hipStream_t stream, bool* used);
+// Pieces of the unfused decode layer.
+// RoPE on n values (heads of head_dim), pairs (2i, 2i+1): rope_f32_multi_head.
+hipError_t launch_rope(float* v, int n, int head_dim, int position, const RopeFreq& freq, hipStream_t stream);
+// h = silu(g) * u
+hipError_t launch_swiglu(const float* g, const float* u, float* h, int n, hipStream_t stream);
+// hsum = x + residual (residual may be null; hidden_out may be null), then
+// out = hsum * inv_rms * w with inv_rms = 1 / sqrt(mean(hsum^2) + eps).
+hipError_t launch_rmsnorm(const float* x, const float* residual, const float* w, float eps,
+                          float* hidden_out, float* out, int n, hipStream_t stream);
+
 hipError_t launch_kv_quantize(const float* in, int8_t* codes, float* scales, size_t n_rows,
                               size_t row_len, hipStream_t stream);
 hipError_t launch_kv_dequantize(const int8_t* codes, const float* scales, float* out,

@@ -26,9 +26,11 @@
 // Results agree with the reference to fp32 rounding (different summation
 // order); the element values themselves are bit-exact in dequant.hip.
 #include <algorithm>
+#include <climits>
 #include <map>
 #include <mutex>
 #include <tuple>
+#include <type_traits>
 
 #include "common.hpp"
 #include "launch.hpp"
@@ -497,6 +499,28 @@ template <int F> constexpr int loads_per_unit() { return (F == kQ4_K || F == kQ4
 // 14336 x 4096 Q4_K: depth 1 9.8 us, 2 8.5 us, 3 9.2 us, 5 11.2 us)
 template <int RMAX> constexpr int kB1Depth = RMAX < 2 ? RMAX : 2;
 
+// Decode-layer fusion of the batch-1 kernel (FUSE = true).  Up to three
+// weight matrices of one type and row length share x ("segments", virtual
+// rows concatenated; for SwiGLU the rows of gate and up alternate).  Row runs
+// are handed out in pairs so each wave finishes both rows of a RoPE pair or of
+// a (gate, up) pair in its epilogue.  (An RMSNorm of x folded into the staging
+// measured slower than a separate norm kernel: the norm weights queue ahead of
+// every workgroup's first weight rows.)
+// The plain kernel takes an empty argument in the fuse descriptor's place.
+struct NoFuse {};
+// FUSE: 0 plain; 2 segments in row pairs with the RoPE / SwiGLU epilogue.
+template <int FUSE> using FuseArg = typename std::conditional<FUSE != 0, MatvecFuse, NoFuse>::type;
+
+__device__ __forceinline__ int fuse_seg(const MatvecFuse& f, int v, int& r) {
+  if (f.swiglu) {
+    r = v >> 1;
+    return v & 1;
+  }
+  const int sg = (v >= f.start1 ? 1 : 0) + (v >= f.start2 ? 1 : 0);
+  r = v - (sg == 0 ? 0 : sg == 1 ? f.start1 : f.start2);
+  return sg;
+}
+
 // Every lane keeps the digit planes of its units in registers.  KS waves split
 // each row's units (KS > 1 for long rows; partial sums meet in LDS); the
 // workgroup's other waves take other rows.  Rows are spread evenly over all
@@ -520,11 +544,12 @@ template <int RMAX> constexpr int kB1Depth = RMAX < 2 ? RMAX : 2;
 // one may be shorter): every workgroup stages only its slice of x, and slice z
 // writes its partial dot products to y + z * out_dim, summed by
 // slice_reduce_kernel in slice order.
-template <int F, int UPL, int RMAX, bool FULL, int SIT>
+template <int F, int UPL, int RMAX, bool FULL, int SIT, int FUSE = 0>
 __global__ __launch_bounds__(768) void mv_b1(const uint8_t* __restrict__ w,
                                              const float* __restrict__ x, float* __restrict__ y,
                                              int out_dim, int row_bpr, int slice_bpr, int ks,
-                                             bool interleave) {
+                                             bool interleave, FuseArg<FUSE> fu) {
+  static_assert(FUSE != 2 || RMAX % 2 == 0, "fused rows come in pairs");
   using FU = FastUnit<F>;
   using D = Dig<F>;
   constexpr int NW = FU::NW, US = D::US;
@@ -546,7 +571,13 @@ __global__ __launch_bounds__(768) void mv_b1(const uint8_t* __restrict__ w,
   // Rows of a stream are either one contiguous run or, interleaved, rows
   // gs, gs + n_streams, ... (all waves then sweep the matrix together).
   int r_begin, r_step, n_rows;  // n_rows <= RMAX either way
-  if (interleave) {
+  if (FUSE == 2) {  // runs of row pairs
+    const long P = out_dim / 2;
+    const long p0 = gs * P / n_streams, p1 = (gs + 1) * P / n_streams;
+    r_begin = (int)(2 * p0);
+    r_step = 1;
+    n_rows = (int)(2 * (p1 - p0));
+  } else if (interleave) {
     r_begin = (int)gs;
     r_step = (int)n_streams;
     n_rows = gs < out_dim ? (int)((out_dim - 1 - gs) / n_streams) + 1 : 0;
@@ -560,7 +591,14 @@ __global__ __launch_bounds__(768) void mv_b1(const uint8_t* __restrict__ w,
   uint32_t buf[RMAX][UPL][NW];
   auto load_row = [&](int rr) {
     const int row = max(0, min(r_begin + rr * r_step, out_dim - 1));
-    const uint8_t* rp = w + (size_t)row * row_bytes;
+    const uint8_t* rp;
+    if constexpr (FUSE == 2) {
+      int r;
+      const int sg = fuse_seg(fu, row, r);
+      rp = (sg == 0 ? fu.w0 : sg == 1 ? fu.w1 : fu.w2) + (size_t)r * row_bytes;
+    } else {
+      rp = w + (size_t)row * row_bytes;
+    }
 #pragma unroll
     for (int i = 0; i < UPL; i++) {
       const int u = ubase + 64 * i;
@@ -609,6 +647,35 @@ __global__ __launch_bounds__(768) void mv_b1(const uint8_t* __restrict__ w,
   }
 #pragma unroll
   for (int rr = 0; rr < RMAX; rr++) acc[rr] = wave_sum_l63(acc[rr]);
+  if constexpr (FUSE == 2) {
+    if (lane == 63) {
+#pragma unroll
+      for (int rr = 0; rr < RMAX; rr += 2) {
+        if (rr < n_rows) {
+          const float a0 = acc[rr], a1 = acc[rr + 1];
+          int r;
+          const int sg = fuse_seg(fu, r_begin + rr, r);
+          if (fu.swiglu) {
+            fu.y0[r] = (a0 / (1.0f + expf(-a0))) * a1;  // silu(gate) * up
+          } else {
+            float o0 = a0, o1 = a1;
+            if ((fu.rope_mask >> sg) & 1u) {  // rows r, r+1: pair i of a head
+              const int i = (r % fu.head_dim) >> 1;
+              const float ang = (float)fu.position * fu.freq.f[i];
+              // sin / cos of the fp32 angle, rounded once from double
+              const float sn = (float)sin((double)ang), cs = (float)cos((double)ang);
+              o0 = a0 * cs - a1 * sn;
+              o1 = a0 * sn + a1 * cs;
+            }
+            float* yo = sg == 0 ? fu.y0 : sg == 1 ? fu.y1 : fu.y2;
+            yo[r] = o0;
+            yo[r + 1] = o1;
+          }
+        }
+      }
+    }
+    return;
+  }
   if (lane == 63) {
     if (ks == 1) {
 #pragma unroll
@@ -986,7 +1053,7 @@ hipError_t run_b1_sit(const uint8_t* w, const float* x, float* y, int out_dim, i
   long n_wg = std::max<long>((device_cu_count() + slices - 1) / slices, (streams_needed + rs - 1) / rs);
   n_wg = std::max<long>(1, std::min<long>(n_wg, (out_dim + rs - 1) / rs));
   hipLaunchKernelGGL(kern, dim3((unsigned)n_wg, (unsigned)slices), dim3(threads), lds, s, w, x, y,
-                     out_dim, row_bpr, slice_bpr, ks, interleave);
+                     out_dim, row_bpr, slice_bpr, ks, interleave, NoFuse{});
   return hipGetLastError();
 }
 
@@ -1122,6 +1189,90 @@ hipError_t b1_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, 
   hipLaunchKernelGGL(slice_reduce_kernel, dim3((unsigned)((out_dim + 255) / 256)), dim3(256), 0, s,
                      ws, y, out_dim, p.slices);
   return hipGetLastError();
+}
+
+// Fused decode-layer launch: whole rows (one slice), pairs of rows per wave.
+template <int F, int UPL, int RMAX, int SIT, int MODE>
+hipError_t run_fused_sit(const MatvecFuse& f, const float* x, int vrows, int bpr, int rs, size_t lds,
+                         hipStream_t s) {
+  auto kern = mv_b1<F, UPL, RMAX, true, SIT, MODE>;
+  hipError_t e = set_lds_attr(kern, lds);
+  if (e != hipSuccess) return e;
+  // streams of row pairs, at most RMAX rows each
+  const long units = vrows / 2, per = RMAX / 2;
+  const long streams_needed = (units + per - 1) / per;
+  long n_wg = std::max<long>(device_cu_count(), (streams_needed + rs - 1) / rs);
+  n_wg = std::max<long>(1, std::min<long>(n_wg, (units + rs - 1) / rs));
+  if (n_wg > device_cu_count()) {
+    // paired rows in more than one round of workgroups measured slower than
+    // the separate launches (one row chain per wave grows too long)
+    return hipErrorNotSupported;
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)n_wg), dim3(64 * rs), lds, s, nullptr, x, nullptr, vrows, bpr,
+                     bpr, 1, false, f);
+  return hipGetLastError();
+}
+
+template <int F, int UPL, int RMAX, int MODE>
+hipError_t run_fused(const MatvecFuse& f, const float* x, int vrows, int bpr, hipStream_t s, bool* used) {
+  const int U = bpr * Geom<F>::bs / FastUnit<F>::E;
+  const size_t lds = ((size_t)U * Dig<F>::US + RMAX) * sizeof(uint32_t);
+  if (lds > (size_t)lds_limit()) return hipSuccess;
+  static std::mutex mu;
+  static std::map<std::pair<int, size_t>, int> rs_cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+  int rs = 0;
+  {
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = rs_cache.find({dev, lds});
+    if (it != rs_cache.end()) rs = it->second;
+  }
+  if (rs == 0) {
+    auto probe = mv_b1<F, UPL, RMAX, true, 2, MODE>;
+    hipError_t e = set_lds_attr(probe, lds);
+    if (e != hipSuccess) return e;
+    rs = 1;
+    for (int cand = 12; cand >= 1; cand--) {  // launch bounds: 768 threads
+      int per_cu = 0;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, probe, 64 * cand, lds) == hipSuccess && per_cu >= 1) {
+        rs = cand;
+        break;
+      }
+    }
+    std::lock_guard<std::mutex> lk(mu);
+    rs_cache[{dev, lds}] = rs;
+  }
+  const int nchunk = bpr * Geom<F>::bs / 8;
+  const int sit = (nchunk + 64 * rs - 1) / (64 * rs);
+  hipError_t e;
+  if (sit <= 1) e = run_fused_sit<F, UPL, RMAX, 1, MODE>(f, x, vrows, bpr, rs, lds, s);
+  else if (sit <= 2) e = run_fused_sit<F, UPL, RMAX, 2, MODE>(f, x, vrows, bpr, rs, lds, s);
+  else return hipSuccess;  // x too long to stage in two chunks per thread
+  if (e == hipErrorNotSupported) return hipSuccess;  // more rows than one round: not fused
+  *used = (e == hipSuccess);
+  return e;
+}
+
+template <int F>
+hipError_t fused_dispatch(const MatvecFuse& f, int vrows, const float* x, int in_dim, hipStream_t s,
+                          bool* used) {
+  *used = false;
+  if (in_dim % Geom<F>::bs) return hipSuccess;
+  const int bpr = in_dim / Geom<F>::bs;
+  const int U = bpr * Geom<F>::bs / FastUnit<F>::E;
+  if (U == 0 || (U != 64 && U != 128)) return hipSuccess;  // whole units per lane, one slice
+  for (const uint8_t* w : {f.w0, f.w1, f.w2})
+    if (w && !fast_aligned<F>(w, x, in_dim, bpr)) return hipSuccess;
+  if (U == 64) {
+    hipError_t e = run_fused<F, 1, 6, 2>(f, x, vrows, bpr, s, used);
+    if (e != hipSuccess || *used) return e;
+    return run_fused<F, 1, 12, 2>(f, x, vrows, bpr, s, used);  // up to 12 rows per wave
+  }
+  // two units per lane: Q4_K / Q8_0 (12 / 17 raw dwords per unit) would spill
+  // in the fused form, so those rows take the separate launches
+  if constexpr (F == kQ6_K || F == kQ4_0) return run_fused<F, 2, 4, 2>(f, x, vrows, bpr, s, used);
+  return hipSuccess;
 }
 
 // K slices of the small-batch kernel: one unit per lane, at most 64 per slice.
@@ -1293,6 +1444,19 @@ hipError_t fast_dispatch(const uint8_t* w, const float* x, float* y, int out_dim
 }
 
 }  // namespace
+
+hipError_t launch_matvec_fused(int dtype, const MatvecFuse& f, int total_rows, const float* x,
+                               size_t in_dim, hipStream_t s, bool* used) {
+  *used = false;
+  if (total_rows <= 0 || (total_rows & 1) || in_dim > (size_t)INT_MAX) return hipSuccess;
+  switch (dtype) {
+    case kQ4_0: return fused_dispatch<kQ4_0>(f, total_rows, x, (int)in_dim, s, used);
+    case kQ8_0: return fused_dispatch<kQ8_0>(f, total_rows, x, (int)in_dim, s, used);
+    case kQ4_K: return fused_dispatch<kQ4_K>(f, total_rows, x, (int)in_dim, s, used);
+    case kQ6_K: return fused_dispatch<kQ6_K>(f, total_rows, x, (int)in_dim, s, used);
+    default: return hipSuccess;
+  }
+}
 
 hipError_t launch_matvec_generic(int dtype, const uint8_t* w, const float* x, float* y,
                                  size_t out_dim, size_t in_dim, size_t batch, hipStream_t s) {

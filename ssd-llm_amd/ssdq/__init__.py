@@ -53,6 +53,11 @@ SIGNATURES = {
     "ssdq_matvec_generic_dev": (_i, [_i, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     "ssdq_matvec_quantized": (_i, [_vp, _vp, _sz, _vp, _sz, _sz, _sz, _i, _vp]),
     "ssdq_gemm_q4k_bf16_dev": (_i, [_vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    "ssdq_qkv_rope_dev": (_i, [_i, _vp, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz,
+                               _c.c_float, _vp]),
+    "ssdq_swiglu_dev": (_i, [_i, _vp, _vp, _vp, _vp, _sz, _sz, _vp]),
+    "ssdq_rmsnorm_matvec_dev": (_i, [_i, _vp, _vp, _vp, _c.c_float, _vp, _sz, _sz, _vp]),
+    "ssdq_rmsnorm_dev": (_i, [_vp, _vp, _vp, _c.c_float, _vp, _vp, _sz, _vp]),
     "ssdq_kv_quantize_rows_dev": (_i, [_vp, _vp, _vp, _sz, _sz, _vp]),
     "ssdq_kv_dequantize_rows_dev": (_i, [_vp, _vp, _vp, _sz, _sz, _vp]),
     "ssdq_paged_kv_append_dev": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _vp]),
@@ -130,6 +135,32 @@ def matvec(dtype, w, x, y, out_dim, in_dim, batch=1, stream=None, generic=False)
     f = lib().ssdq_matvec_generic_dev if generic else lib().ssdq_matvec_dev
     return check("ssdq_matvec_dev",
                  f(dtype, _ptr(w), _ptr(x), _ptr(y), out_dim, in_dim, batch, _stream(stream)))
+
+
+def qkv_rope(dtypes, ws, x, q, k, v, q_dim, kv_dim, n_embd, head_dim, position, theta, stream=None):
+    (dq, dk, dv), (wq, wk, wv) = dtypes, ws
+    return check("ssdq_qkv_rope_dev",
+                 lib().ssdq_qkv_rope_dev(dq, _ptr(wq), dk, _ptr(wk), dv, _ptr(wv), _ptr(x), _ptr(q),
+                                         _ptr(k), _ptr(v), q_dim, kv_dim, n_embd, head_dim, position,
+                                         theta, _stream(stream)))
+
+
+def swiglu(dtype, w_gate, w_up, x, h, n_ff, n_embd, stream=None):
+    return check("ssdq_swiglu_dev",
+                 lib().ssdq_swiglu_dev(dtype, _ptr(w_gate), _ptr(w_up), _ptr(x), _ptr(h), n_ff, n_embd,
+                                       _stream(stream)))
+
+
+def rmsnorm_matvec(dtype, w, x, norm_w, eps, y, out_dim, n_embd, stream=None):
+    return check("ssdq_rmsnorm_matvec_dev",
+                 lib().ssdq_rmsnorm_matvec_dev(dtype, _ptr(w), _ptr(x), _ptr(norm_w), eps, _ptr(y),
+                                               out_dim, n_embd, _stream(stream)))
+
+
+def rmsnorm(x, residual, weight, eps, hidden_out, out, n, stream=None):
+    return check("ssdq_rmsnorm_dev",
+                 lib().ssdq_rmsnorm_dev(_ptr(x), _ptr(residual), _ptr(weight), eps, _ptr(hidden_out),
+                                        _ptr(out), n, _stream(stream)))
 
 
 def gemm_q4k_bf16(w, x_bf16, y, M, N, K, stream=None):

@@ -273,6 +273,28 @@ def extras(torch, ssdq, synth, timer, np):
     layer_case("decode_swiglu_q4k_14336x4096", [(ssdq.Q4_K, 14336), (ssdq.Q4_K, 14336)], swi)
     layer_case("decode_output_head_rmsnorm_q6k_128256x4096", [(ssdq.Q6_K, 128256)], head)
 
+    # INT8 KV swap slots: 1024 blocks of 16 tokens x 1024 (one layer of a 16k-token
+    # context) gathered into the reference's slot format and scattered back
+    bs_, kv_, nb_, npool_ = 16, 1024, 1024, 4096
+    kc_ = torch.randint(-127, 128, (npool_ * bs_ * kv_,), dtype=torch.int8, device="cuda")
+    vc_ = torch.randint(-127, 128, (npool_ * bs_ * kv_,), dtype=torch.int8, device="cuda")
+    ks_, vs_ = torch.rand(npool_ * bs_, device="cuda"), torch.rand(npool_ * bs_, device="cuda")
+    ids_ = torch.randperm(npool_, device="cuda")[:nb_].to(torch.int32)
+    nf_ = torch.full((nb_,), bs_, dtype=torch.int32, device="cuda")
+    sb_ = ssdq.kv_slot_bytes(bs_, kv_)
+    for where, slots_ in (("device", torch.empty(nb_ * sb_, dtype=torch.uint8, device="cuda")),
+                          ("pinned_host", torch.empty(nb_ * sb_, dtype=torch.uint8).pin_memory())):
+        t, _, n = timer.run(lambda i: ssdq.kv_swap_out(kc_, ks_, vc_, vs_, ids_, nf_, nb_, bs_, kv_, npool_,
+                                                        slots_), 50, 5)
+        ti, _, ni = timer.run(lambda i: ssdq.kv_swap_in(slots_, ids_, nb_, bs_, kv_, npool_, kc_, ks_, vc_, vs_,
+                                                         None), 50, 5)
+        out[f"kv_swap_out_int8_1024x16x1024_to_{where}"] = {
+            "GB/s": round(nb_ * sb_ / (t / n) / 1e9, 1), "us": round(t / n * 1e6, 2),
+            "swap_in_GB/s": round(nb_ * sb_ / (ti / ni) / 1e9, 1), "swap_in_us": round(ti / ni * 1e6, 2),
+            "bytes": nb_ * sb_}
+    del kc_, vc_, ks_, vs_
+    torch.cuda.empty_cache()
+
     # the synchronous host-pointer twin (MetalCompute::matvec_quantized contract):
     # W and x cross PCIe on every call, so this is the PCIe-inclusive rate
     w_host = synth.quant_weights(ssdq.Q4_K, 14336, 4096, synth.seed(3, 0))

@@ -126,6 +126,33 @@ int ssdq_matvec_dev(int dtype, const void* w, const float* x, float* y, size_t o
 int ssdq_matvec_quantized(ssdq_ctx* ctx, const uint8_t* w_raw, size_t w_len, const float* x,
                           size_t x_len, size_t out_dim, size_t in_dim, int dtype, float* y);
 
+/* ------------------------------------------- INT8 KV swap slots */
+/* Bytes of one swap slot: the reference's SwapQuantMode::Int8 slot
+ * (src/ssd/block_swap.rs:148-170): K codes, V codes (block_size * kv_dim i8
+ * each), K scales, V scales (block_size f32 each), num_filled (u32). */
+size_t ssdq_kv_slot_bytes(size_t block_size, size_t kv_dim);
+/* Swap-out of paged INT8 KV blocks: slot i (at slots + i * slot_bytes) gets
+ * physical block block_ids[i] of the pools (rows block_id * block_size ..,
+ * as ssdq_paged_kv_append_dev writes them) and num_filled[i] (NULL: 0).  The
+ * bytes are those SwapFile::write_block writes in Int8 mode
+ * (block_swap.rs:187-252) for the f32 rows the pool was quantized from.
+ * slots may be device memory or mapped pinned host memory (hipHostMalloc);
+ * ids outside [0, n_pool_blocks) give zero slots. At most 65535 blocks per
+ * call; kv_dim % 4 == 0; pointers 4-byte aligned. Replaces the extract +
+ * write half of try_swap_out_blocks (paged_attention.rs:755-786). */
+int ssdq_kv_swap_out_dev(const int8_t* k_codes, const float* k_scales, const int8_t* v_codes,
+                         const float* v_scales, const int32_t* block_ids, const uint32_t* num_filled,
+                         size_t n_blocks, size_t block_size, size_t kv_dim, size_t n_pool_blocks, void* slots,
+                         ssdq_stream_t stream);
+/* Swap-in: the inverse scatter (read_block + restore_block_data,
+ * block_swap.rs:283-370, paged_attention.rs:624-630, 788-815); the codes and
+ * scales are restored exactly (the reference dequantizes them to f32 on
+ * read). num_filled (NULL: not returned) gets each slot's count; ids outside
+ * [0, n_pool_blocks) are skipped. */
+int ssdq_kv_swap_in_dev(const void* slots, const int32_t* block_ids, size_t n_blocks, size_t block_size,
+                        size_t kv_dim, size_t n_pool_blocks, int8_t* k_codes, float* k_scales, int8_t* v_codes,
+                        float* v_scales, uint32_t* num_filled, ssdq_stream_t stream);
+
 /* ------------------------------------------------- decode-layer ops */
 /* The projections of one decode step on quantized weights, QKV+RoPE and
  * SwiGLU each one kernel launch where the shapes allow it (one matrix type, whole rows of at most 128

@@ -1051,3 +1051,46 @@ int ssdo_fused_rmsnorm_linear(int dtype, const uint8_t* w, const float* x, const
     free(xn);
     return rc;
 }
+
+/* ------------------------------------------------ INT8 KV swap slots */
+
+size_t ssdo_kv_slot_bytes(size_t block_size, size_t kv_dim) {
+    /* SwapFile::with_quant_mode, Int8 (src/ssd/block_swap.rs:148-170):
+     * keys + values i8, one f32 scale per key row and per value row, num_filled u32 */
+    return block_size * kv_dim * 2 + block_size * 2 * 4 + 4;
+}
+
+void ssdo_kv_swap_write(const float* keys, const float* values, size_t block_size, size_t kv_dim,
+                        uint32_t num_filled, uint8_t* slot) {
+    /* SwapFile::write_block, Int8 (block_swap.rs:187-252): quantize_vectors_int8
+     * of keys and of values (rows of kv_dim), then codes K, codes V, scales K,
+     * scales V, num_filled little-endian */
+    size_t n = block_size * kv_dim;
+    int8_t* kc = (int8_t*)slot;
+    int8_t* vc = (int8_t*)(slot + n);
+    float* ks = (float*)malloc(block_size * sizeof(float));
+    float* vs = (float*)malloc(block_size * sizeof(float));
+    ssdo_quantize_rows_int8(keys, block_size, kv_dim, kc, ks);
+    ssdo_quantize_rows_int8(values, block_size, kv_dim, vc, vs);
+    memcpy(slot + 2 * n, ks, block_size * 4);
+    memcpy(slot + 2 * n + block_size * 4, vs, block_size * 4);
+    for (int i = 0; i < 4; i++) slot[2 * n + block_size * 8 + i] = (uint8_t)(num_filled >> (8 * i));
+    free(ks);
+    free(vs);
+}
+
+void ssdo_kv_swap_read(const uint8_t* slot, size_t block_size, size_t kv_dim, float* keys, float* values,
+                       uint32_t* num_filled) {
+    /* SwapFile::read_block, Int8 (block_swap.rs:283-370): dequantize_vectors_int8 */
+    size_t n = block_size * kv_dim;
+    float* ks = (float*)malloc(block_size * sizeof(float));
+    float* vs = (float*)malloc(block_size * sizeof(float));
+    memcpy(ks, slot + 2 * n, block_size * 4);
+    memcpy(vs, slot + 2 * n + block_size * 4, block_size * 4);
+    ssdo_dequantize_rows_int8((const int8_t*)slot, ks, block_size, kv_dim, keys);
+    ssdo_dequantize_rows_int8((const int8_t*)(slot + n), vs, block_size, kv_dim, values);
+    const uint8_t* p = slot + 2 * n + block_size * 8;
+    *num_filled = (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+    free(ks);
+    free(vs);
+}

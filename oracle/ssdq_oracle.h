@@ -133,6 +133,14 @@ void ssdo_fused_post_attn_norm(float* hidden, const float* attn, const float* w,
 int ssdo_fused_rmsnorm_linear(int dtype, const uint8_t* w, const float* x, const float* norm_w,
                               size_t vocab, size_t n_embd, float* y);
 
+/* INT8 swap-file slots of the paged KV cache: slot size, write_block and
+ * read_block of SwapFile in SwapQuantMode::Int8 (src/ssd/block_swap.rs:148-370). */
+size_t ssdo_kv_slot_bytes(size_t block_size, size_t kv_dim);
+void ssdo_kv_swap_write(const float* keys, const float* values, size_t block_size, size_t kv_dim,
+                        uint32_t num_filled, uint8_t* slot);
+void ssdo_kv_swap_read(const uint8_t* slot, size_t block_size, size_t kv_dim, float* keys, float* values,
+                       uint32_t* num_filled);
+
 #ifdef __cplusplus
 }
 #endif

@@ -35,6 +35,9 @@ def lib():
             "ssdo_matvec_exact": (_i, [_vp, _vp, _sz, _sz, _i, _vp]),
             "ssdo_matvec_elements": (_i, [_vp, _sz, _sz, _i, _vp]),
             "ssdo_rope_multi_head": (None, [_vp, _sz, _sz, _sz, _sz, ctypes.c_float]),
+            "ssdo_kv_slot_bytes": (_sz, [_sz, _sz]),
+            "ssdo_kv_swap_write": (None, [_vp, _vp, _sz, _sz, ctypes.c_uint32, _vp]),
+            "ssdo_kv_swap_read": (None, [_vp, _sz, _sz, _vp, _vp, _vp]),
             "ssdo_silu": (None, [_vp, _sz]),
             "ssdo_rmsnorm": (None, [_vp, _vp, _sz, ctypes.c_float]),
             "ssdo_fused_post_attn_norm": (None, [_vp, _vp, _vp, _sz, ctypes.c_float, _vp]),
@@ -219,3 +222,25 @@ def swiglu(dtype, w_gate, w_up, x, n_ff, n_embd):
     g = silu(g)
     u, _ = matvec(dtype, w_up, x, n_ff, n_embd)
     return (g * u).astype(np.float32)
+
+
+def kv_slot_bytes(block_size, kv_dim):
+    return lib().ssdo_kv_slot_bytes(block_size, kv_dim)
+
+
+def kv_swap_write(keys, values, block_size, kv_dim, num_filled):
+    keys = _c(keys, np.float32)
+    values = _c(values, np.float32)
+    slot = np.zeros(kv_slot_bytes(block_size, kv_dim), np.uint8)
+    lib().ssdo_kv_swap_write(keys.ctypes.data, values.ctypes.data, block_size, kv_dim, num_filled,
+                             slot.ctypes.data)
+    return slot
+
+
+def kv_swap_read(slot, block_size, kv_dim):
+    slot = _c(slot, np.uint8)
+    k = np.empty(block_size * kv_dim, np.float32)
+    v = np.empty(block_size * kv_dim, np.float32)
+    nf = np.zeros(1, np.uint32)
+    lib().ssdo_kv_swap_read(slot.ctypes.data, block_size, kv_dim, k.ctypes.data, v.ctypes.data, nf.ctypes.data)
+    return k, v, int(nf[0])

@@ -328,6 +328,48 @@ int ssdq_matvec_quantized(ssdq_ctx* c, const uint8_t* w_raw, size_t w_len, const
   return ok();
 }
 
+/* -------------------------------------------- INT8 KV swap slots */
+
+size_t ssdq_kv_slot_bytes(size_t block_size, size_t kv_dim) { return ssdq::kv_slot_bytes(block_size, kv_dim); }
+
+static int swap_args_ok(const char* fn, const void* kc, const void* ks, const void* vc, const void* vs,
+                        const void* ids, const void* slots, size_t n_blocks, size_t bs, size_t kv, size_t n_pool) {
+  if (!kc || !ks || !vc || !vs || !ids || !slots) return fail(SSDQ_ERR_INVALID_ARG, "%s: NULL pointer", fn);
+  if (bs == 0 || kv == 0 || kv % 4) return fail(SSDQ_ERR_INVALID_ARG, "%s: kv_dim must be a positive multiple of 4", fn);
+  if (((uintptr_t)kc | (uintptr_t)vc | (uintptr_t)ks | (uintptr_t)vs | (uintptr_t)slots) & 3)
+    return fail(SSDQ_ERR_INVALID_ARG, "%s: pools and slots must be 4-byte aligned", fn);
+  if (n_blocks > 65535 || !fits_int(bs * kv) || n_pool > (size_t)LONG_MAX / (bs * kv))
+    return fail(SSDQ_ERR_INVALID_ARG, "%s: too many blocks per call (at most 65535) or blocks too large", fn);
+  return SSDQ_OK;
+}
+
+int ssdq_kv_swap_out_dev(const int8_t* k_codes, const float* k_scales, const int8_t* v_codes,
+                         const float* v_scales, const int32_t* block_ids, const uint32_t* num_filled,
+                         size_t n_blocks, size_t block_size, size_t kv_dim, size_t n_pool_blocks, void* slots,
+                         ssdq_stream_t stream) {
+  if (n_blocks == 0) return ok();
+  int rc = swap_args_ok("ssdq_kv_swap_out_dev", k_codes, k_scales, v_codes, v_scales, block_ids, slots, n_blocks,
+                        block_size, kv_dim, n_pool_blocks);
+  if (rc) return rc;
+  hipError_t e = ssdq::launch_kv_swap_out(k_codes, k_scales, v_codes, v_scales, block_ids, num_filled, n_blocks,
+                                          block_size, kv_dim, n_pool_blocks, slots, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "ssdq_kv_swap_out_dev");
+  return ok();
+}
+
+int ssdq_kv_swap_in_dev(const void* slots, const int32_t* block_ids, size_t n_blocks, size_t block_size,
+                        size_t kv_dim, size_t n_pool_blocks, int8_t* k_codes, float* k_scales, int8_t* v_codes,
+                        float* v_scales, uint32_t* num_filled, ssdq_stream_t stream) {
+  if (n_blocks == 0) return ok();
+  int rc = swap_args_ok("ssdq_kv_swap_in_dev", k_codes, k_scales, v_codes, v_scales, block_ids, slots, n_blocks,
+                        block_size, kv_dim, n_pool_blocks);
+  if (rc) return rc;
+  hipError_t e = ssdq::launch_kv_swap_in(slots, block_ids, n_blocks, block_size, kv_dim, n_pool_blocks, k_codes,
+                                         k_scales, v_codes, v_scales, num_filled, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "ssdq_kv_swap_in_dev");
+  return ok();
+}
+
 /* ------------------------------------------------- decode-layer ops */
 
 namespace {

@@ -190,6 +190,64 @@ unsigned grid_waves(size_t rows) {
   return (unsigned)(g ? g : 1);
 }
 
+// INT8 swap-file slots (the reference's SwapQuantMode::Int8 format,
+// src/ssd/block_swap.rs:148-370): K codes [bs*kv] | V codes [bs*kv] |
+// K scales [bs] f32 | V scales [bs] f32 | num_filled u32.  The pool already
+// holds the bit-exact codes and scales, so swap-out is a gather of physical
+// blocks into consecutive slots and swap-in the scatter back.  Slots are
+// 2*bs*kv + 8*bs + 4 bytes apart (4-byte aligned), so the copies go a dword
+// per lane; slots may live in device memory or in mapped pinned host memory.
+// grid.y = slot, grid.x strides over its dwords.
+__global__ __launch_bounds__(256) void kv_swap_out_kernel(const int8_t* __restrict__ kc, const float* __restrict__ ks,
+                                                          const int8_t* __restrict__ vc, const float* __restrict__ vs,
+                                                          const int32_t* __restrict__ ids,
+                                                          const uint32_t* __restrict__ nfill, int bs, int kv,
+                                                          long n_pool, uint8_t* __restrict__ slots,
+                                                          size_t slot_bytes) {
+  const int blk = blockIdx.y;
+  const long b = ids[blk];
+  const bool valid = b >= 0 && b < n_pool;  // other ids give a zero slot
+  uint32_t* dst = reinterpret_cast<uint32_t*>(slots + (size_t)blk * slot_bytes);
+  const size_t nc = (size_t)bs * kv / 4, base = valid ? (size_t)b * bs : 0;
+  const uint32_t* kd = reinterpret_cast<const uint32_t*>(kc) + base * kv / 4;
+  const uint32_t* vd = reinterpret_cast<const uint32_t*>(vc) + base * kv / 4;
+  const size_t total = 2 * nc + 2 * (size_t)bs + 1;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+    uint32_t v = 0;
+    if (valid) {
+      if (i < nc) v = kd[i];
+      else if (i < 2 * nc) v = vd[i - nc];
+      else if (i < 2 * nc + bs) v = __float_as_uint(ks[base + (i - 2 * nc)]);
+      else if (i < 2 * nc + 2 * bs) v = __float_as_uint(vs[base + (i - 2 * nc - bs)]);
+      else v = nfill ? nfill[blk] : 0u;
+    }
+    dst[i] = v;
+  }
+}
+
+__global__ __launch_bounds__(256) void kv_swap_in_kernel(const uint8_t* __restrict__ slots, size_t slot_bytes,
+                                                         const int32_t* __restrict__ ids, int bs, int kv, long n_pool,
+                                                         int8_t* __restrict__ kc, float* __restrict__ ks,
+                                                         int8_t* __restrict__ vc, float* __restrict__ vs,
+                                                         uint32_t* __restrict__ nfill) {
+  const int blk = blockIdx.y;
+  const long b = ids[blk];
+  if (b < 0 || b >= n_pool) return;  // ignored
+  const uint32_t* src = reinterpret_cast<const uint32_t*>(slots + (size_t)blk * slot_bytes);
+  const size_t nc = (size_t)bs * kv / 4, base = (size_t)b * bs;
+  uint32_t* kd = reinterpret_cast<uint32_t*>(kc) + base * kv / 4;
+  uint32_t* vd = reinterpret_cast<uint32_t*>(vc) + base * kv / 4;
+  const size_t total = 2 * nc + 2 * (size_t)bs + 1;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+    const uint32_t v = src[i];
+    if (i < nc) kd[i] = v;
+    else if (i < 2 * nc) vd[i - nc] = v;
+    else if (i < 2 * nc + bs) ks[base + (i - 2 * nc)] = __uint_as_float(v);
+    else if (i < 2 * nc + 2 * bs) vs[base + (i - 2 * nc - bs)] = __uint_as_float(v);
+    else if (nfill) nfill[blk] = v;
+  }
+}
+
 }  // namespace
 
 hipError_t launch_kv_quantize(const float* in, int8_t* codes, float* scales, size_t n_rows,
@@ -239,6 +297,32 @@ hipError_t launch_kv_dequantize(const int8_t* codes, const float* scales, float*
   if (g > 65536) g = 65536;
   hipLaunchKernelGGL(kv_dequantize_kernel, dim3((unsigned)g), dim3(256), 0, s, codes, scales, out,
                      n_rows, (int)row_len);
+  return hipGetLastError();
+}
+
+size_t kv_slot_bytes(size_t bs, size_t kv) { return 2 * bs * kv + 8 * bs + 4; }
+
+static dim3 swap_grid(size_t n_blocks, size_t bs, size_t kv) {
+  const size_t dwords = (2 * bs * kv + 8 * bs + 4) / 4;
+  const size_t per = 256 * 8;  // about eight dwords per lane
+  return dim3((unsigned)std::min<size_t>((dwords + per - 1) / per, 1024), (unsigned)n_blocks);
+}
+
+hipError_t launch_kv_swap_out(const int8_t* kc, const float* ks, const int8_t* vc, const float* vs,
+                              const int32_t* ids, const uint32_t* nfill, size_t n_blocks, size_t bs, size_t kv,
+                              size_t n_pool, void* slots, hipStream_t s) {
+  if (n_blocks == 0) return hipSuccess;
+  hipLaunchKernelGGL(kv_swap_out_kernel, swap_grid(n_blocks, bs, kv), dim3(256), 0, s, kc, ks, vc, vs, ids, nfill,
+                     (int)bs, (int)kv, (long)n_pool, (uint8_t*)slots, kv_slot_bytes(bs, kv));
+  return hipGetLastError();
+}
+
+hipError_t launch_kv_swap_in(const void* slots, const int32_t* ids, size_t n_blocks, size_t bs, size_t kv,
+                             size_t n_pool, int8_t* kc, float* ks, int8_t* vc, float* vs, uint32_t* nfill,
+                             hipStream_t s) {
+  if (n_blocks == 0) return hipSuccess;
+  hipLaunchKernelGGL(kv_swap_in_kernel, swap_grid(n_blocks, bs, kv), dim3(256), 0, s, (const uint8_t*)slots,
+                     kv_slot_bytes(bs, kv), ids, (int)bs, (int)kv, (long)n_pool, kc, ks, vc, vs, nfill);
   return hipGetLastError();
 }
 

@@ -80,6 +80,18 @@ hipError_t launch_paged_kv_append(const float* k, const float* v, const int32_t*
                                   float* v_scales, size_t n_tokens, size_t kv_dim,
                                   hipStream_t stream);
 
+// INT8 swap-file slots of paged KV blocks (the reference's Int8 slot format):
+// slot bytes, gather of pool blocks ids[0..n) into consecutive slots (ids out
+// of [0, n_pool) give zero slots), and the scatter back (such ids ignored).
+size_t kv_slot_bytes(size_t block_size, size_t kv_dim);
+hipError_t launch_kv_swap_out(const int8_t* k_codes, const float* k_scales, const int8_t* v_codes,
+                              const float* v_scales, const int32_t* ids, const uint32_t* num_filled,
+                              size_t n_blocks, size_t block_size, size_t kv_dim, size_t n_pool, void* slots,
+                              hipStream_t stream);
+hipError_t launch_kv_swap_in(const void* slots, const int32_t* ids, size_t n_blocks, size_t block_size,
+                             size_t kv_dim, size_t n_pool, int8_t* k_codes, float* k_scales, int8_t* v_codes,
+                             float* v_scales, uint32_t* num_filled, hipStream_t stream);
+
 struct PagedAttnArgs {
   const float* q;
   const int8_t* k_codes;

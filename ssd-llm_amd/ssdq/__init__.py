@@ -53,6 +53,9 @@ SIGNATURES = {
     "ssdq_matvec_generic_dev": (_i, [_i, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     "ssdq_matvec_quantized": (_i, [_vp, _vp, _sz, _vp, _sz, _sz, _sz, _i, _vp]),
     "ssdq_gemm_q4k_bf16_dev": (_i, [_vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    "ssdq_kv_slot_bytes": (_sz, [_sz, _sz]),
+    "ssdq_kv_swap_out_dev": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp, _vp]),
+    "ssdq_kv_swap_in_dev": (_i, [_vp, _vp, _sz, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp]),
     "ssdq_qkv_rope_dev": (_i, [_i, _vp, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz,
                                _c.c_float, _vp]),
     "ssdq_swiglu_dev": (_i, [_i, _vp, _vp, _vp, _vp, _sz, _sz, _vp]),
@@ -135,6 +138,26 @@ def matvec(dtype, w, x, y, out_dim, in_dim, batch=1, stream=None, generic=False)
     f = lib().ssdq_matvec_generic_dev if generic else lib().ssdq_matvec_dev
     return check("ssdq_matvec_dev",
                  f(dtype, _ptr(w), _ptr(x), _ptr(y), out_dim, in_dim, batch, _stream(stream)))
+
+
+def kv_slot_bytes(block_size, kv_dim):
+    return lib().ssdq_kv_slot_bytes(block_size, kv_dim)
+
+
+def kv_swap_out(k_codes, k_scales, v_codes, v_scales, block_ids, num_filled, n_blocks, block_size, kv_dim,
+                n_pool_blocks, slots, stream=None):
+    return check("ssdq_kv_swap_out_dev",
+                 lib().ssdq_kv_swap_out_dev(_ptr(k_codes), _ptr(k_scales), _ptr(v_codes), _ptr(v_scales),
+                                            _ptr(block_ids), _ptr(num_filled), n_blocks, block_size, kv_dim,
+                                            n_pool_blocks, _ptr(slots), _stream(stream)))
+
+
+def kv_swap_in(slots, block_ids, n_blocks, block_size, kv_dim, n_pool_blocks, k_codes, k_scales, v_codes,
+               v_scales, num_filled, stream=None):
+    return check("ssdq_kv_swap_in_dev",
+                 lib().ssdq_kv_swap_in_dev(_ptr(slots), _ptr(block_ids), n_blocks, block_size, kv_dim,
+                                           n_pool_blocks, _ptr(k_codes), _ptr(k_scales), _ptr(v_codes),
+                                           _ptr(v_scales), _ptr(num_filled), _stream(stream)))
 
 
 def qkv_rope(dtypes, ws, x, q, k, v, q_dim, kv_dim, n_embd, head_dim, position, theta, stream=None):

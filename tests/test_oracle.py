@@ -418,3 +418,34 @@ def test_bf16_rounding_helper():
     x = np.array([1.0, 1.00390625, 1.01171875, -2.5], np.float32)
     r = synth.bf16_bits_to_f32(synth.f32_to_bf16_bits(x))
     assert list(r) == [1.0, 1.0, 1.015625, -2.5]
+
+
+# ------------------------------------------------- INT8 KV swap slots
+def test_kv_swap_slot_reference_known_answers():
+    # block_swap.rs:1177-1185: 16 x 128 -> 4228 bytes, f32 16388 (ratio ~3.88)
+    assert o.kv_slot_bytes(16, 128) == 4228
+    assert 3.0 < (16 * 128 * 2 * 4 + 4) / o.kv_slot_bytes(16, 128) < 4.5
+    # block_swap.rs:1028-1066: write / read within INT8 error, num_filled kept
+    bs, kv = 4, 8
+    keys = ((np.arange(bs * kv) - 16.0) * 0.1).astype(np.float32)
+    vals = ((np.arange(bs * kv) - 16.0) * 0.05).astype(np.float32)
+    k, v, nf = o.kv_swap_read(o.kv_swap_write(keys, vals, bs, kv, 3), bs, kv)
+    assert nf == 3 and np.all(np.abs(k - keys) < 0.02) and np.all(np.abs(v - vals) < 0.02)
+
+
+def test_kv_swap_slot_layout():
+    # codes K | codes V | scales K | scales V | num_filled (block_swap.rs:14-15, 228-252),
+    # checked against the quantizer's own outputs placed by numpy
+    g = np.random.default_rng(8)
+    bs, kv = 16, 1024
+    keys = g.standard_normal(bs * kv).astype(np.float32)
+    vals = g.standard_normal(bs * kv).astype(np.float32)
+    slot = o.kv_swap_write(keys, vals, bs, kv, 0xA1B2C3D4)
+    kc, ks = o.quantize_rows(keys, bs, kv)
+    vc, vs = o.quantize_rows(vals, bs, kv)
+    want = np.concatenate([kc.view(np.uint8).ravel(), vc.view(np.uint8).ravel(), ks.view(np.uint8),
+                           vs.view(np.uint8), np.array([0xD4, 0xC3, 0xB2, 0xA1], np.uint8)])
+    assert np.array_equal(slot, want)
+    k, v, nf = o.kv_swap_read(slot, bs, kv)
+    assert nf == 0xA1B2C3D4
+    assert np.array_equal(k, o.dequantize_rows(kc, ks, bs, kv).ravel())

@@ -58,7 +58,11 @@ extern "C" {
 #define SSDQ_TYPE_Q5_K 13
 #define SSDQ_TYPE_Q6_K 14
 #define SSDQ_TYPE_Q8_K 15
+#define SSDQ_TYPE_IQ2_XXS 16
+#define SSDQ_TYPE_IQ2_XS 17
+#define SSDQ_TYPE_IQ3_XXS 18
 #define SSDQ_TYPE_IQ4_NL 20
+#define SSDQ_TYPE_IQ3_S 21
 #define SSDQ_TYPE_IQ4_XS 23
 #define SSDQ_TYPE_BF16 30
 
@@ -115,8 +119,9 @@ int ssdq_dequantize_to_f32(ssdq_ctx* ctx, int dtype, const uint8_t* data, size_t
  * matvec_q4_0/q4_k/q6_k/q8_0 (gpu.rs:396-428) and matvec_quantized_cpu
  * (compute.rs:648-677); batch > 1 replaces the per-row loop of
  * batch_scheduler.rs:242-276. Types: Q4_0, Q8_0, Q4_K, Q6_K and the other
- * matvec_quantized types Q2_K, Q3_K, Q5_K, Q8_K, IQ4_NL, IQ4_XS, F16, BF16
- * (matvec_*_cpu, compute.rs:796-1077, 2249-2285). Other dtypes (F32 included,
+ * matvec_quantized types Q2_K, Q3_K, Q5_K, Q8_K, IQ2_XXS, IQ2_XS, IQ3_XXS,
+ * IQ3_S, IQ4_NL, IQ4_XS, F16, BF16 (matvec_*_cpu, compute.rs:796-2238,
+ * 2249-2285). Other dtypes (F32 included,
  * as in compute.rs:672-675) zero-fill y and return SSDQ_WARN_UNSUPPORTED_ZEROED. */
 int ssdq_matvec_dev(int dtype, const void* w, const float* x, float* y, size_t out_dim,
                     size_t in_dim, size_t batch, ssdq_stream_t stream);

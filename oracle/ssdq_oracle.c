@@ -11,6 +11,8 @@
  */
 #include "ssdq_oracle.h"
 
+#include "../ssd-llm_amd/csrc/iq_grids.h" /* IQ2 / IQ3 lattice code books */
+
 #include <math.h>
 #include <pthread.h>
 #include <stdlib.h>
@@ -22,7 +24,8 @@ size_t ssdo_block_size(int dtype) {
         case SSDO_F32: case SSDO_F16: case SSDO_BF16: return 1;
         case SSDO_Q4_0: case SSDO_Q8_0: case SSDO_IQ4_NL: return 32;
         case SSDO_Q2_K: case SSDO_Q3_K: case SSDO_Q4_K: case SSDO_Q5_K: case SSDO_Q6_K:
-        case SSDO_Q8_K: case SSDO_IQ4_XS: return 256;
+        case SSDO_Q8_K: case SSDO_IQ4_XS: case SSDO_IQ2_XXS: case SSDO_IQ2_XS: case SSDO_IQ3_XXS:
+        case SSDO_IQ3_S: return 256;
         default: return 0;
     }
 }
@@ -43,6 +46,10 @@ size_t ssdo_type_size(int dtype) {
         case SSDO_Q8_K: return 4 + 256 + 16 * 2;        /* 292 */
         case SSDO_IQ4_NL: return 2 + 16;                /* 18 */
         case SSDO_IQ4_XS: return 2 + 2 + 128 + 16;      /* 148 */
+        case SSDO_IQ2_XXS: return 2 + 256 / 8 * 2;      /* 66 */
+        case SSDO_IQ2_XS: return 2 + 256 / 8 * 2 + 256 / 32; /* 74 */
+        case SSDO_IQ3_XXS: return 2 + 3 * 256 / 8;      /* 98 */
+        case SSDO_IQ3_S: return 2 + 64 + 8 + 32 + 4;    /* 110 */
         default: return 0;
     }
 }
@@ -536,6 +543,114 @@ static void mv_bf16(const uint8_t* w, const float* x, size_t r0, size_t r1, size
     }
 }
 
+/* KSIGNS_IQ2XS (compute.rs:1964-1973): the 7-bit index with bit 7 set to its
+ * parity, so every mask has an even number of negative signs */
+static inline unsigned ksigns(unsigned i) { return i | ((unsigned)(__builtin_popcount(i) & 1) << 7); }
+static inline float sgn(unsigned mask, unsigned j) { return (mask >> j) & 1u ? -1.0f : 1.0f; }
+static inline unsigned le_u32(const uint8_t* p) {
+    return (unsigned)p[0] | ((unsigned)p[1] << 8) | ((unsigned)p[2] << 16) | ((unsigned)p[3] << 24);
+}
+static inline unsigned gbyte(uint64_t v, unsigned j) { return (unsigned)(v >> (8 * j)) & 0xFFu; }
+
+/* Element values of one 256-element block of the IQ2 / IQ3 types, as the
+ * matvecs below form them before the multiply by x (one product per element,
+ * in the reference's operand order db * grid * sign). */
+static void iq_block_elements(int dtype, const uint8_t* p, float* e) {
+    float d = le_f16(p);
+    for (unsigned ib32 = 0; ib32 < 8; ib32++) {
+        float* o = e + ib32 * 32;
+        if (dtype == SSDO_IQ2_XXS) { /* compute.rs:2137-2182 */
+            const uint8_t* g = p + 2 + ib32 * 8;
+            unsigned a0 = le_u32(g), a1 = le_u32(g + 4);
+            float db = d * (0.5f + (float)(a1 >> 28)) * 0.25f;
+            for (unsigned l = 0; l < 4; l++) {
+                uint64_t gr = ssdq_iq2xxs_grid[(a0 >> (8 * l)) & 0xFF];
+                unsigned sg = ksigns((a1 >> (7 * l)) & 127);
+                for (unsigned j = 0; j < 8; j++) o[l * 8 + j] = db * (float)gbyte(gr, j) * sgn(sg, j);
+            }
+        } else if (dtype == SSDO_IQ2_XS) { /* compute.rs:2192-2238 */
+            unsigned sbyte = p[2 + 64 + ib32 / 2];
+            unsigned nib = (ib32 % 2 == 0) ? (sbyte & 0x0F) : (sbyte >> 4);
+            float db = d * (0.5f + (float)nib) * 0.25f;
+            for (unsigned l = 0; l < 4; l++) {
+                const uint8_t* q = p + 2 + (ib32 * 4 + l) * 2;
+                unsigned qv = (unsigned)q[0] | ((unsigned)q[1] << 8);
+                uint64_t gr = ssdq_iq2xs_grid[qv & 511];
+                unsigned sg = ksigns(qv >> 9);
+                for (unsigned j = 0; j < 8; j++) o[l * 8 + j] = db * (float)gbyte(gr, j) * sgn(sg, j);
+            }
+        } else if (dtype == SSDO_IQ3_XXS) { /* compute.rs:1983-2034 */
+            unsigned aux = le_u32(p + 2 + 64 + ib32 * 4);
+            float db = d * (0.5f + (float)(aux >> 28)) * 0.5f;
+            for (unsigned l = 0; l < 4; l++) {
+                unsigned sg = ksigns((aux >> (7 * l)) & 127);
+                uint32_t g1 = ssdq_iq3xxs_grid[p[2 + ib32 * 8 + 2 * l]];
+                uint32_t g2 = ssdq_iq3xxs_grid[p[2 + ib32 * 8 + 2 * l + 1]];
+                for (unsigned j = 0; j < 4; j++) {
+                    o[l * 8 + j] = db * (float)gbyte(g1, j) * sgn(sg, j);
+                    o[l * 8 + j + 4] = db * (float)gbyte(g2, j) * sgn(sg, j + 4);
+                }
+            }
+        } else { /* SSDO_IQ3_S, compute.rs:2042-2128 */
+            unsigned sbyte = p[2 + 64 + 8 + 32 + ib32 / 2];
+            float db = d * (float)(1 + 2 * (int)((ib32 % 2 == 0) ? (sbyte & 0x0F) : (sbyte >> 4)));
+            unsigned qh = p[2 + 64 + ib32];
+            for (unsigned l = 0; l < 4; l++) {
+                unsigned i1 = p[2 + ib32 * 8 + 2 * l] | ((qh << (8 - 2 * l)) & 256);
+                unsigned i2 = p[2 + ib32 * 8 + 2 * l + 1] | ((qh << (7 - 2 * l)) & 256);
+                uint32_t g1 = ssdq_iq3s_grid[i1], g2 = ssdq_iq3s_grid[i2];
+                unsigned sg = p[2 + 64 + 8 + ib32 * 4 + l];
+                for (unsigned j = 0; j < 4; j++) {
+                    o[l * 8 + j] = db * (float)gbyte(g1, j) * sgn(sg, j);
+                    o[l * 8 + j + 4] = db * (float)gbyte(g2, j) * sgn(sg, j + 4);
+                }
+            }
+        }
+    }
+}
+
+/* The four IQ2 / IQ3 matvecs: the serial sum of element * x (sum += db * grid *
+ * sign * x, compute.rs:1983-2238), in the reference's order: element order for
+ * IQ2, and j, j+4 alternating within each group of 8 for IQ3 (its two grid
+ * words are consumed together). */
+/* GCC's -O3 tree vectorizer was seen to change the result of the alternating
+ * IQ3 sum below (a serial fp32 chain it may not reorder; correct at -O2 and
+ * with -fno-tree-vectorize), so this function is built without it. */
+__attribute__((optimize("no-tree-vectorize")))
+static void mv_iq_lattice(int dtype, const uint8_t* w, const float* x, size_t r0, size_t r1, size_t in_dim,
+                          float* y) {
+    const size_t bb = ssdo_type_size(dtype), bpr = in_dim / 256;
+    float e[256];
+    for (size_t row = r0; row < r1; row++) {
+        float sum = 0.0f;
+        for (size_t b = 0; b < bpr; b++) {
+            iq_block_elements(dtype, w + (row * bpr + b) * bb, e);
+            if (dtype == SSDO_IQ3_XXS || dtype == SSDO_IQ3_S) {
+                for (size_t g8 = 0; g8 < 256; g8 += 8)
+                    for (size_t j = 0; j < 4; j++) {
+                        sum += e[g8 + j] * x[b * 256 + g8 + j];
+                        sum += e[g8 + j + 4] * x[b * 256 + g8 + j + 4];
+                    }
+            } else {
+                for (size_t j = 0; j < 256; j++) sum += e[j] * x[b * 256 + j];
+            }
+        }
+        y[row] = sum;
+    }
+}
+static void mv_iq2_xxs(const uint8_t* w, const float* x, size_t r0, size_t r1, size_t k, float* y) {
+    mv_iq_lattice(SSDO_IQ2_XXS, w, x, r0, r1, k, y);
+}
+static void mv_iq2_xs(const uint8_t* w, const float* x, size_t r0, size_t r1, size_t k, float* y) {
+    mv_iq_lattice(SSDO_IQ2_XS, w, x, r0, r1, k, y);
+}
+static void mv_iq3_xxs(const uint8_t* w, const float* x, size_t r0, size_t r1, size_t k, float* y) {
+    mv_iq_lattice(SSDO_IQ3_XXS, w, x, r0, r1, k, y);
+}
+static void mv_iq3_s(const uint8_t* w, const float* x, size_t r0, size_t r1, size_t k, float* y) {
+    mv_iq_lattice(SSDO_IQ3_S, w, x, r0, r1, k, y);
+}
+
 typedef void (*mv_fn)(const uint8_t*, const float*, size_t, size_t, size_t, float*);
 
 static mv_fn pick_mv(int dtype) {
@@ -553,6 +668,10 @@ static mv_fn pick_mv(int dtype) {
         case SSDO_IQ4_XS: return mv_iq4_xs;
         case SSDO_BF16: return mv_bf16;
         case SSDO_F16: return mv_f16;
+        case SSDO_IQ2_XXS: return mv_iq2_xxs;
+        case SSDO_IQ2_XS: return mv_iq2_xs;
+        case SSDO_IQ3_XXS: return mv_iq3_xxs;
+        case SSDO_IQ3_S: return mv_iq3_s;
         default: return NULL;
     }
 }
@@ -695,6 +814,9 @@ static void row_elements(int dtype, const uint8_t* r, size_t row_bytes, size_t k
                     }
                 }
             }
+            return;
+        case SSDO_IQ2_XXS: case SSDO_IQ2_XS: case SSDO_IQ3_XXS: case SSDO_IQ3_S:
+            for (size_t b = 0; b < bpr; b++) iq_block_elements(dtype, r + b * ssdo_type_size(dtype), e + b * 256);
             return;
         default:
             ssdo_dequantize_to_f32(dtype, r, row_bytes, k, e);

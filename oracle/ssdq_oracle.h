@@ -26,7 +26,8 @@ extern "C" {
 enum {
     SSDO_F32 = 0, SSDO_F16 = 1, SSDO_Q4_0 = 2, SSDO_Q8_0 = 8,
     SSDO_Q2_K = 10, SSDO_Q3_K = 11, SSDO_Q4_K = 12, SSDO_Q5_K = 13, SSDO_Q6_K = 14,
-    SSDO_Q8_K = 15, SSDO_IQ4_NL = 20, SSDO_IQ4_XS = 23, SSDO_BF16 = 30
+    SSDO_Q8_K = 15, SSDO_IQ2_XXS = 16, SSDO_IQ2_XS = 17, SSDO_IQ3_XXS = 18, SSDO_IQ4_NL = 20,
+    SSDO_IQ3_S = 21, SSDO_IQ4_XS = 23, SSDO_BF16 = 30
 };
 
 /* block_size / type_size, src/model/gguf.rs:87-135 (0 for unknown ids) */

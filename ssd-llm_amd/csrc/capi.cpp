@@ -147,7 +147,8 @@ size_t ssdq_block_size(int dtype) {
     case SSDQ_TYPE_F32: case SSDQ_TYPE_F16: case SSDQ_TYPE_BF16: return 1;
     case SSDQ_TYPE_Q4_0: case SSDQ_TYPE_Q8_0: case SSDQ_TYPE_IQ4_NL: return 32;
     case SSDQ_TYPE_Q2_K: case SSDQ_TYPE_Q3_K: case SSDQ_TYPE_Q4_K: case SSDQ_TYPE_Q5_K:
-    case SSDQ_TYPE_Q6_K: case SSDQ_TYPE_Q8_K: case SSDQ_TYPE_IQ4_XS: return 256;
+    case SSDQ_TYPE_Q6_K: case SSDQ_TYPE_Q8_K: case SSDQ_TYPE_IQ4_XS: case SSDQ_TYPE_IQ2_XXS:
+    case SSDQ_TYPE_IQ2_XS: case SSDQ_TYPE_IQ3_XXS: case SSDQ_TYPE_IQ3_S: return 256;
     default: return 0;
   }
 }
@@ -166,6 +167,10 @@ size_t ssdq_type_size(int dtype) {
     case SSDQ_TYPE_Q8_K: return 292;
     case SSDQ_TYPE_IQ4_NL: return 18;
     case SSDQ_TYPE_IQ4_XS: return 148;
+    case SSDQ_TYPE_IQ2_XXS: return 66;
+    case SSDQ_TYPE_IQ2_XS: return 74;
+    case SSDQ_TYPE_IQ3_XXS: return 98;
+    case SSDQ_TYPE_IQ3_S: return 110;
     default: return 0;
   }
 }

@@ -25,11 +25,38 @@
 
 #include "common.hpp"
 #include "launch.hpp"
+#define SSDQ_IQ_GRIDS_DEVICE_ONLY
+#include "iq_grids.h"
 
 namespace ssdq {
 namespace {
 
-enum : int { kF16 = 1, kQ2_K = 10, kQ3_K = 11, kQ5_K = 13, kQ8_K = 15, kIQ4_NL = 20, kIQ4_XS = 23, kBF16 = 30 };
+enum : int {
+  kF16 = 1, kQ2_K = 10, kQ3_K = 11, kQ5_K = 13, kQ8_K = 15, kIQ2_XXS = 16, kIQ2_XS = 17, kIQ3_XXS = 18,
+  kIQ4_NL = 20, kIQ3_S = 21, kIQ4_XS = 23, kBF16 = 30
+};
+
+// IQ2 / IQ3 lattice code books (device copies; each workgroup stages its
+// type's table into LDS)
+__constant__ uint64_t k_iq2xxs_grid[256] = SSDQ_IQ2XXS_GRID_INIT;
+__constant__ uint64_t k_iq2xs_grid[512] = SSDQ_IQ2XS_GRID_INIT;
+__constant__ uint32_t k_iq3xxs_grid[256] = SSDQ_IQ3XXS_GRID_INIT;
+__constant__ uint32_t k_iq3s_grid[512] = SSDQ_IQ3S_GRID_INIT;
+
+template <int F> constexpr bool is_iq_lattice = F == kIQ2_XXS || F == kIQ2_XS || F == kIQ3_XXS || F == kIQ3_S;
+// bytes of the type's code book in LDS
+template <int F> constexpr int tab_bytes = F == kIQ2_XXS ? 2048 : F == kIQ2_XS ? 4096 : F == kIQ3_XXS ? 1024
+                                         : F == kIQ3_S ? 2048 : 0;
+template <int F>
+__device__ __forceinline__ const uint32_t* tab_src() {
+  if constexpr (F == kIQ2_XXS) return reinterpret_cast<const uint32_t*>(k_iq2xxs_grid);
+  else if constexpr (F == kIQ2_XS) return reinterpret_cast<const uint32_t*>(k_iq2xs_grid);
+  else if constexpr (F == kIQ3_XXS) return k_iq3xxs_grid;
+  else return k_iq3s_grid;
+}
+
+// KSIGNS_IQ2XS (compute.rs:1964-1973): the 7-bit index with its parity as bit 7
+__device__ __forceinline__ uint32_t ksigns(uint32_t i) { return i | ((__popc(i) & 1u) << 7); }
 
 // bs elements / bb bytes per block; NW raw dwords per 32-element group.
 template <int F> struct XG;
@@ -41,6 +68,10 @@ template <> struct XG<kIQ4_NL> { static constexpr int bs = 32, bb = 18, NW = 6; 
 template <> struct XG<kIQ4_XS> { static constexpr int bs = 256, bb = 148, NW = 6; };
 template <> struct XG<kF16> { static constexpr int bs = 1, bb = 2, NW = 16; };
 template <> struct XG<kBF16> { static constexpr int bs = 1, bb = 2, NW = 16; };
+template <> struct XG<kIQ2_XXS> { static constexpr int bs = 256, bb = 66, NW = 3; };
+template <> struct XG<kIQ2_XS> { static constexpr int bs = 256, bb = 74, NW = 4; };
+template <> struct XG<kIQ3_XXS> { static constexpr int bs = 256, bb = 98, NW = 4; };
+template <> struct XG<kIQ3_S> { static constexpr int bs = 256, bb = 110, NW = 6; };
 
 typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
 
@@ -115,6 +146,28 @@ __device__ __forceinline__ void load_group(const uint8_t* __restrict__ row, int 
     ld4(blk - mis, raw);                               // bytes -mis .. 15-mis
     raw[4] = ldh(blk + 14) | (ldh(blk + 16) << 16);    // bytes 14..17
     raw[5] = mis;
+  } else if constexpr (is_iq_lattice<F>) {  // 2-byte-aligned blocks: 16-bit loads
+    const uint8_t* blk = row + (size_t)(g >> 3) * XG<F>::bb;
+    const int ib = g & 7;
+    const uint8_t* q = blk + 2 + 8 * ib;  // grid indices (IQ2_XXS: + signs / scale word)
+    raw[0] = ldh(q) | (ldh(q + 2) << 16);
+    raw[1] = ldh(q + 4) | (ldh(q + 6) << 16);
+    if constexpr (F == kIQ2_XXS) {
+      raw[2] = ldh(blk);
+    } else if constexpr (F == kIQ2_XS) {
+      raw[2] = ldh(blk + 66 + ((ib >> 1) & ~1));  // scale bytes 2(ib/4), 2(ib/4)+1
+      raw[3] = ldh(blk);
+    } else if constexpr (F == kIQ3_XXS) {
+      const uint8_t* a = blk + 66 + 4 * ib;  // scales_and_signs word
+      raw[2] = ldh(a) | (ldh(a + 2) << 16);
+      raw[3] = ldh(blk);
+    } else {  // kIQ3_S
+      raw[2] = ldh(blk + 66 + (ib & ~1));            // qh bytes ib&~1, +1
+      const uint8_t* sg = blk + 74 + 4 * ib;          // sign bytes of the four 8-groups
+      raw[3] = ldh(sg) | (ldh(sg + 2) << 16);
+      raw[4] = ldh(blk + 106 + ((ib >> 1) & ~1));     // scale bytes
+      raw[5] = ldh(blk);
+    }
   } else {  // kIQ4_XS
     const uint8_t* blk = row + (size_t)(g >> 3) * 148;
     const int sb = g & 7;
@@ -126,8 +179,15 @@ __device__ __forceinline__ void load_group(const uint8_t* __restrict__ row, int 
 
 // Decodes group g: u[e] (integer or code-book values as floats) and per-half
 // scale S / offset O, element value = S*u - O.
+// Magnitude byte j of a code-book entry, with the sign of bit j of sg.
+__device__ __forceinline__ float signed_mag(uint32_t word, int j, uint32_t sg, int sj) {
+  const float m = (float)((word >> (8 * j)) & 0xFFu);
+  return ((sg >> sj) & 1u) ? -m : m;
+}
+
 template <int F>
-__device__ __forceinline__ void decode_group(const uint32_t* raw, int g, float* u, float* S, float* O) {
+__device__ __forceinline__ void decode_group(const uint32_t* raw, int g, float* u, float* S, float* O,
+                                             const uint32_t* tab = nullptr) {
   if constexpr (F == kF16) {
     // converted explicitly: left to itself the compiler folds the widening
     // into v_fma_mix_f32, which measured 2.5x slower here than cvt + fmac
@@ -218,6 +278,76 @@ __device__ __forceinline__ void decode_group(const uint32_t* raw, int g, float* 
     }
     S[0] = S[1] = d;
     O[0] = O[1] = 128.0f * d;
+  } else if constexpr (F == kIQ2_XXS || F == kIQ2_XS) {
+    // four 8-element groups: a 64-bit grid row (tab, two dwords) and a sign mask
+    const int ib = g & 7;
+    float db;
+    uint32_t gi[4], sg[4];
+    if constexpr (F == kIQ2_XXS) {  // compute.rs:2137-2182
+      const uint32_t a0 = raw[0], a1 = raw[1];
+      db = f16_to_f32(raw[2]) * (0.5f + (float)(a1 >> 28)) * 0.25f;
+#pragma unroll
+      for (int l = 0; l < 4; l++) {
+        gi[l] = (a0 >> (8 * l)) & 0xFFu;
+        sg[l] = ksigns((a1 >> (7 * l)) & 127u);
+      }
+    } else {  // compute.rs:2192-2238
+      const uint32_t sb = (raw[2] >> (8 * ((ib >> 1) & 1))) & 0xFFu;
+      db = f16_to_f32(raw[3]) * (0.5f + (float)((sb >> (4 * (ib & 1))) & 15u)) * 0.25f;
+#pragma unroll
+      for (int l = 0; l < 4; l++) {
+        const uint32_t qv = (raw[l >> 1] >> (16 * (l & 1))) & 0xFFFFu;
+        gi[l] = qv & 511u;
+        sg[l] = ksigns(qv >> 9);
+      }
+    }
+#pragma unroll
+    for (int l = 0; l < 4; l++) {
+      const uint32_t lo = tab[2 * gi[l]], hi = tab[2 * gi[l] + 1];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        u[8 * l + j] = signed_mag(lo, j, sg[l], j);
+        u[8 * l + j + 4] = signed_mag(hi, j, sg[l], j + 4);
+      }
+    }
+    S[0] = S[1] = db;
+    O[0] = O[1] = 0.f;
+  } else if constexpr (F == kIQ3_XXS || F == kIQ3_S) {
+    // four 8-element groups: two 32-bit grid entries and a sign mask each
+    const int ib = g & 7;
+    float db;
+    uint32_t i1[4], i2[4], sg[4];
+    if constexpr (F == kIQ3_XXS) {  // compute.rs:1983-2034
+      const uint32_t aux = raw[2];
+      db = f16_to_f32(raw[3]) * (0.5f + (float)(aux >> 28)) * 0.5f;
+#pragma unroll
+      for (int l = 0; l < 4; l++) {
+        i1[l] = (raw[l >> 1] >> (16 * (l & 1))) & 0xFFu;
+        i2[l] = (raw[l >> 1] >> (16 * (l & 1) + 8)) & 0xFFu;
+        sg[l] = ksigns((aux >> (7 * l)) & 127u);
+      }
+    } else {  // compute.rs:2042-2128
+      const uint32_t qh = (raw[2] >> (8 * (ib & 1))) & 0xFFu;
+      const uint32_t sb = (raw[4] >> (8 * ((ib >> 1) & 1))) & 0xFFu;
+      db = f16_to_f32(raw[5]) * (float)(1 + 2 * (int)((sb >> (4 * (ib & 1))) & 15u));
+#pragma unroll
+      for (int l = 0; l < 4; l++) {
+        i1[l] = ((raw[l >> 1] >> (16 * (l & 1))) & 0xFFu) | ((qh << (8 - 2 * l)) & 256u);
+        i2[l] = ((raw[l >> 1] >> (16 * (l & 1) + 8)) & 0xFFu) | ((qh << (7 - 2 * l)) & 256u);
+        sg[l] = (raw[3] >> (8 * l)) & 0xFFu;
+      }
+    }
+#pragma unroll
+    for (int l = 0; l < 4; l++) {
+      const uint32_t g1 = tab[i1[l]], g2 = tab[i2[l]];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        u[8 * l + j] = signed_mag(g1, j, sg[l], j);
+        u[8 * l + j + 4] = signed_mag(g2, j, sg[l], j + 4);
+      }
+    }
+    S[0] = S[1] = db;
+    O[0] = O[1] = 0.f;
   } else {  // IQ4_NL / IQ4_XS: 16 index bytes, element 2j / 2j+1 = low / high nibble of byte j
     uint32_t qs[4];
     float scale;
@@ -257,9 +387,9 @@ __device__ __forceinline__ void decode_group(const uint32_t* raw, int g, float* 
 
 constexpr int kGS = 36;  // LDS stride of a 32-float group
 
-template <int B>
+template <int F, int B>
 __host__ __device__ constexpr size_t ext_lds_bytes(int G) {
-  return (size_t)B * G * (kGS + 2) * sizeof(float);
+  return (size_t)B * G * (kGS + 2) * sizeof(float) + tab_bytes<F>;
 }
 
 template <int F, int B, int R>
@@ -269,6 +399,11 @@ __global__ __launch_bounds__(256) void mv_ext(const uint8_t* __restrict__ w, con
   extern __shared__ float smem[];
   float* xs = smem;                           // [B][G][kGS]
   float* xsum = smem + (size_t)B * G * kGS;   // [B][G][2]
+  uint32_t* tab = reinterpret_cast<uint32_t*>(xsum + (size_t)B * G * 2);  // code book (IQ2 / IQ3)
+  if constexpr (is_iq_lattice<F>) {
+    const uint32_t* src = tab_src<F>();
+    for (int i = threadIdx.x; i < tab_bytes<F> / 4; i += blockDim.x) tab[i] = src[i];
+  }
   // stage x: one thread per 8 floats; a group's four chunks sit on adjacent lanes
   const int n8 = B * G * 4;  // multiple of 4, so lanes i and i^1 are both live or both not
   for (int i = threadIdx.x; i < n8; i += blockDim.x) {
@@ -305,7 +440,7 @@ __global__ __launch_bounds__(256) void mv_ext(const uint8_t* __restrict__ w, con
 #pragma unroll
       for (int rr = 0; rr < R; rr++) {
         float u[32], S[2], O[2];
-        decode_group<F>(raw[rr], g, u, S, O);
+        decode_group<F>(raw[rr], g, u, S, O, tab);
 #pragma unroll
         for (int b = 0; b < B; b++) {
           const float* xg = xs + ((size_t)b * G + g) * kGS;
@@ -378,6 +513,42 @@ __device__ __forceinline__ float ext_value(const uint8_t* __restrict__ row, int 
     const int j = k & 31;
     const uint32_t bv = p[2 + j / 2];
     return f16_to_f32(ld_u16(p)) * (float)kIq4nl[(j & 1) ? (bv >> 4) : (bv & 15u)];
+  } else if constexpr (is_iq_lattice<F>) {
+    const uint8_t* p = row + (size_t)(k >> 8) * XG<F>::bb;
+    const int idx = k & 255, ib = idx >> 5, l = (idx >> 3) & 3, j = idx & 7;
+    const float d = f16_to_f32(ld_u16(p));
+    auto u32at = [](const uint8_t* q) {
+      return (uint32_t)q[0] | ((uint32_t)q[1] << 8) | ((uint32_t)q[2] << 16) | ((uint32_t)q[3] << 24);
+    };
+    if constexpr (F == kIQ2_XXS) {
+      const uint32_t a1 = u32at(p + 2 + 8 * ib + 4);
+      const float db = d * (0.5f + (float)(a1 >> 28)) * 0.25f;
+      const uint64_t gr = k_iq2xxs_grid[p[2 + 8 * ib + l]];
+      const uint32_t sg = ksigns((a1 >> (7 * l)) & 127u);
+      return db * (float)((gr >> (8 * j)) & 0xFFu) * (((sg >> j) & 1u) ? -1.0f : 1.0f);
+    } else if constexpr (F == kIQ2_XS) {
+      const uint32_t sb = p[66 + ib / 2];
+      const float db = d * (0.5f + (float)((ib % 2 == 0) ? (sb & 15u) : (sb >> 4))) * 0.25f;
+      const uint32_t qv = ld_u16(p + 2 + (ib * 4 + l) * 2);
+      const uint64_t gr = k_iq2xs_grid[qv & 511u];
+      const uint32_t sg = ksigns(qv >> 9);
+      return db * (float)((gr >> (8 * j)) & 0xFFu) * (((sg >> j) & 1u) ? -1.0f : 1.0f);
+    } else if constexpr (F == kIQ3_XXS) {
+      const uint32_t aux = u32at(p + 66 + 4 * ib);
+      const float db = d * (0.5f + (float)(aux >> 28)) * 0.5f;
+      const uint32_t gw = k_iq3xxs_grid[p[2 + 8 * ib + 2 * l + (j >> 2)]];
+      const uint32_t sg = ksigns((aux >> (7 * l)) & 127u);
+      return db * (float)((gw >> (8 * (j & 3))) & 0xFFu) * (((sg >> j) & 1u) ? -1.0f : 1.0f);
+    } else {  // kIQ3_S
+      const uint32_t sb = p[106 + ib / 2];
+      const float db = d * (float)(1 + 2 * (int)((ib % 2 == 0) ? (sb & 15u) : (sb >> 4)));
+      const uint32_t qh = p[66 + ib];
+      const int h = j >> 2;  // 0: first grid word of the pair, 1: second
+      const uint32_t gi = p[2 + 8 * ib + 2 * l + h] | ((qh << (8 - 2 * l - h)) & 256u);
+      const uint32_t gw = k_iq3s_grid[gi];
+      const uint32_t sg = p[74 + 4 * ib + l];
+      return db * (float)((gw >> (8 * (j & 3))) & 0xFFu) * (((sg >> j) & 1u) ? -1.0f : 1.0f);
+    }
   } else {  // kIQ4_XS
     const uint8_t* p = row + (size_t)(k >> 8) * 148;
     const int idx = k & 255, sb = idx >> 5, j = idx & 31;
@@ -450,20 +621,20 @@ hipError_t ext_fast(const uint8_t* w, const float* x, float* y, int out_dim, int
   if (((uintptr_t)w & 3) || ((uintptr_t)x & 15) || (in_dim & 3) || (keff & 31) || G == 0) return hipSuccess;
   if ((F == kF16 || F == kBF16) && (row_bytes & 3)) return hipSuccess;
   const size_t limit = (size_t)ext_lds_limit();
-  if (ext_lds_bytes<1>(G) > limit) return hipSuccess;
+  if (ext_lds_bytes<F, 1>(G) > limit) return hipSuccess;
   int b0 = 0;
   while (b0 < batch) {
     const int left = batch - b0;
     int take = left >= 8 ? 8 : left >= 4 ? 4 : left >= 2 ? 2 : 1;
-    while (take > 1 && (size_t)take * ext_lds_bytes<1>(G) > limit) take >>= 1;
+    while (take > 1 && (size_t)take * ext_lds_bytes<F, 1>(G) > limit) take >>= 1;  // (table counted per take)
     const float* xb = x + (size_t)b0 * in_dim;
     float* yb = y + (size_t)b0 * out_dim;
     hipError_t e;
     switch (take) {
-      case 8: e = run_ext<F, 8, 1>(w, xb, yb, out_dim, in_dim, G, row_bytes, ext_lds_bytes<8>(G), s); break;
-      case 4: e = run_ext<F, 4, 1>(w, xb, yb, out_dim, in_dim, G, row_bytes, ext_lds_bytes<4>(G), s); break;
-      case 2: e = run_ext<F, 2, 2>(w, xb, yb, out_dim, in_dim, G, row_bytes, ext_lds_bytes<2>(G), s); break;
-      default: e = run_ext<F, 1, 4>(w, xb, yb, out_dim, in_dim, G, row_bytes, ext_lds_bytes<1>(G), s); break;
+      case 8: e = run_ext<F, 8, 1>(w, xb, yb, out_dim, in_dim, G, row_bytes, ext_lds_bytes<F, 8>(G), s); break;
+      case 4: e = run_ext<F, 4, 1>(w, xb, yb, out_dim, in_dim, G, row_bytes, ext_lds_bytes<F, 4>(G), s); break;
+      case 2: e = run_ext<F, 2, 2>(w, xb, yb, out_dim, in_dim, G, row_bytes, ext_lds_bytes<F, 2>(G), s); break;
+      default: e = run_ext<F, 1, 4>(w, xb, yb, out_dim, in_dim, G, row_bytes, ext_lds_bytes<F, 1>(G), s); break;
     }
     if (e != hipSuccess) return e;
     b0 += take;
@@ -518,6 +689,7 @@ hipError_t ext_dispatch(const uint8_t* w, const float* x, float* y, size_t out_d
 bool matvec_ext_type(int dtype) {
   switch (dtype) {
     case kQ2_K: case kQ3_K: case kQ5_K: case kQ8_K: case kIQ4_NL: case kIQ4_XS: case kF16: case kBF16:
+    case kIQ2_XXS: case kIQ2_XS: case kIQ3_XXS: case kIQ3_S:
       return true;
     default:
       return false;
@@ -536,6 +708,10 @@ hipError_t launch_matvec_ext(int dtype, const uint8_t* w, const float* x, float*
     case kIQ4_XS: return ext_dispatch<kIQ4_XS>(w, x, y, out_dim, in_dim, batch, s, generic);
     case kF16: return ext_dispatch<kF16>(w, x, y, out_dim, in_dim, batch, s, generic);
     case kBF16: return ext_dispatch<kBF16>(w, x, y, out_dim, in_dim, batch, s, generic);
+    case kIQ2_XXS: return ext_dispatch<kIQ2_XXS>(w, x, y, out_dim, in_dim, batch, s, generic);
+    case kIQ2_XS: return ext_dispatch<kIQ2_XS>(w, x, y, out_dim, in_dim, batch, s, generic);
+    case kIQ3_XXS: return ext_dispatch<kIQ3_XXS>(w, x, y, out_dim, in_dim, batch, s, generic);
+    case kIQ3_S: return ext_dispatch<kIQ3_S>(w, x, y, out_dim, in_dim, batch, s, generic);
     default: return hipErrorInvalidValue;
   }
 }

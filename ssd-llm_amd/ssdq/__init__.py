@@ -17,13 +17,14 @@ LIB_PATH = os.path.join(PKG_ROOT, "libssdq.so")
 # GgmlType ids, src/model/gguf.rs:17-48
 F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, BF16 = 0, 1, 2, 8, 12, 14, 30
 Q2_K, Q3_K, Q5_K, Q8_K, IQ4_NL, IQ4_XS = 10, 11, 13, 15, 20, 23
+IQ2_XXS, IQ2_XS, IQ3_XXS, IQ3_S = 16, 17, 18, 21
 # dequant (streamer.rs:93-125) and the prefill path cover these four
 QUANT_TYPES = (Q4_0, Q8_0, Q4_K, Q6_K)
 # the other matvec_quantized types (compute.rs:655-671)
-MATVEC_EXTRA_TYPES = (Q2_K, Q3_K, Q5_K, Q8_K, IQ4_NL, IQ4_XS, F16, BF16)
+MATVEC_EXTRA_TYPES = (Q2_K, Q3_K, Q5_K, Q8_K, IQ4_NL, IQ4_XS, F16, BF16, IQ2_XXS, IQ2_XS, IQ3_XXS, IQ3_S)
 TYPE_NAMES = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K", Q2_K: "Q2_K", Q3_K: "Q3_K",
               Q5_K: "Q5_K", Q8_K: "Q8_K", IQ4_NL: "IQ4_NL", IQ4_XS: "IQ4_XS", F16: "F16",
-              BF16: "BF16"}
+              BF16: "BF16", IQ2_XXS: "IQ2_XXS", IQ2_XS: "IQ2_XS", IQ3_XXS: "IQ3_XXS", IQ3_S: "IQ3_S"}
 
 OK = 0
 WARN_UNSUPPORTED_ZEROED = 1

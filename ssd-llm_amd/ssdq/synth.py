@@ -12,6 +12,8 @@ Distributions follow the benchmark configurations of the reference path:
   Q2_K / Q3_K / Q5_K / IQ4_NL / IQ4_XS  f16 scales ~ U[0.001, 0.01]
         (IQ4_NL U[0.002, 0.02], IQ4_XS U[0.0001, 0.001]), every other byte
         uniform random (scale fields included)
+  IQ2_XXS / IQ2_XS / IQ3_XXS / IQ3_S  f16 d ~ U[0.001, 0.01], every other byte
+        uniform random
   Q8_K  f32 d ~ U[0.001, 0.01], int8 codes uniform in [-127, 127], bsums the
         16-element code sums
   F16 / BF16  N(0, 0.05) rounded to the type
@@ -24,11 +26,13 @@ from __future__ import annotations
 
 import numpy as np
 
-from . import BF16, F16, IQ4_NL, IQ4_XS, Q2_K, Q3_K, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, Q8_K
+from . import (BF16, F16, IQ2_XS, IQ2_XXS, IQ3_S, IQ3_XXS, IQ4_NL, IQ4_XS, Q2_K, Q3_K, Q4_0, Q4_K, Q5_K,
+               Q6_K, Q8_0, Q8_K)
 
 BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210), Q2_K: (256, 84),
          Q3_K: (256, 110), Q5_K: (256, 176), Q8_K: (256, 292), IQ4_NL: (32, 18),
-         IQ4_XS: (256, 148), F16: (1, 2), BF16: (1, 2)}
+         IQ4_XS: (256, 148), F16: (1, 2), BF16: (1, 2), IQ2_XXS: (256, 66), IQ2_XS: (256, 74),
+         IQ3_XXS: (256, 98), IQ3_S: (256, 110)}
 
 
 def rng(seed: int) -> np.random.Generator:
@@ -74,6 +78,9 @@ def quant_weights(dtype: int, out_dim: int, in_dim: int, seed: int) -> np.ndarra
     elif dtype in (IQ4_NL, IQ4_XS):
         lo, hi = (0.002, 0.02) if dtype == IQ4_NL else (0.0001, 0.001)
         blk[:, 0:2] = _f16_bytes(g.uniform(lo, hi, nb).astype(np.float32))
+        blk[:, 2:] = g.integers(0, 256, (nb, bb - 2), dtype=np.uint8)
+    elif dtype in (IQ2_XXS, IQ2_XS, IQ3_XXS, IQ3_S):  # d first, every other byte random
+        blk[:, 0:2] = _f16_bytes(g.uniform(0.001, 0.01, nb).astype(np.float32))
         blk[:, 2:] = g.integers(0, 256, (nb, bb - 2), dtype=np.uint8)
     elif dtype in (F16, BF16):
         v = (g.standard_normal(nb, dtype=np.float32) * np.float32(0.05)).astype(np.float32)

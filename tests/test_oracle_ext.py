@@ -32,7 +32,8 @@ def test_type_table_matches_gguf():
     # bytes, but matvec_q3_k_cpu (compute.rs:798) and the GGUF format read 110-byte
     # blocks (32 hmask + 64 qs + 12 scales + 2 d); the matvec's layout is the one kept
     want = {Q2_K: (256, 84), Q3_K: (256, 110), Q5_K: (256, 176), Q8_K: (256, 292),
-            IQ4_NL: (32, 18), IQ4_XS: (256, 148), F16: (1, 2), BF16: (1, 2)}
+            IQ4_NL: (32, 18), IQ4_XS: (256, 148), F16: (1, 2), BF16: (1, 2), 16: (256, 66),
+            17: (256, 74), 18: (256, 98), 21: (256, 110)}
     for t, v in want.items():
         assert (o.block_size(t), o.type_size(t)) == v, t
 
@@ -261,7 +262,7 @@ def test_float_types_serial_sum():
     assert np.array_equal(_bits(y), _bits(_serial_sum((wbf * x).astype(np.float32))))
 
 
-@pytest.mark.parametrize("dtype", EXT + [F16, BF16])
+@pytest.mark.parametrize("dtype", EXT + [F16, BF16, 16, 17, 18, 21])
 def test_matvec_within_fp32_bound_of_exact(dtype):
     from ssdq import synth
     out_dim, in_dim = 32, 4096

@@ -18,17 +18,18 @@
 // fp32 chain by rounding only (measured: closer to the exact sum than the
 // reference itself).
 //
-// A prep kernel writes X as fp16 in the order the main kernel consumes it,
-// plus XS: in a super-block, MFMA step t (32 k values) gives lane group c
-// (lanes 16c .. 16c+15) the 8 values of sub-block 4*(t/4) + c at offset
-// 8*(t%4), so one 16-byte load hands a lane the codes of a whole sub-block.
-// Tiling: a workgroup of 4 waves computes a (16*MT) x 128 tile, two
-// workgroups per CU.  X tiles are staged through LDS (double-buffered, fed
-// from a register ring one super-block deep); weights are prefetched a
-// super-block ahead; each wave owns 32 columns and builds its B fragments from
-// the codes in registers.  Every global load is consumed outside branches, so
-// the compiler's waits stay partial (a load consumed under a branch costs a
-// full vmcnt(0) drain).
+// A prep kernel writes X as fp16 in MFMA fragment order, plus XS: in a
+// super-block, MFMA step t (32 k values) gives lane group c (lanes
+// 16c .. 16c+15) the 8 values of sub-block 4*(t/4) + c at offset 8*(t%4), so
+// one 16-byte load hands a lane the codes of a whole sub-block, and a 1 KB
+// chunk of the prepared X is one A fragment.
+// Tiling: a workgroup of 8 waves computes a 128 x 256 tile, one workgroup per
+// CU; each wave owns 32 columns and all 128 rows, and builds its B fragments
+// from the codes in registers.  K runs in stages of four MFMA steps; each
+// stage's X fragments go straight from global memory into LDS (one 16-byte
+// load per lane, issued a stage ahead into the other of two buffers), the
+// weights of a stage are loaded into registers a stage ahead, and one wait
+// plus one barrier per stage publishes both.
 #include <algorithm>
 #include <type_traits>
 
@@ -47,10 +48,7 @@ typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
 // calls that keep register arrays of it in memory)
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int BN = 128, BK = 32;
-constexpr int XS = BK + 8;  // LDS row stride in halves (80 B keeps 16-byte reads conflict free)
-constexpr int NT = 2;       // N sub-tiles (of 16 columns) per wave
-constexpr int PF = 8;       // X staging: K steps in flight (one super-block)
+constexpr int NT = 2;    // N sub-tiles (of 16 columns) per wave
 
 __global__ __launch_bounds__(256) void widen_bf16_kernel(const uint16_t* __restrict__ x,
                                                          float* __restrict__ out, size_t n) {
@@ -59,19 +57,23 @@ __global__ __launch_bounds__(256) void widen_bf16_kernel(const uint16_t* __restr
     out[i] = __uint_as_float((uint32_t)x[i] << 16);
 }
 
-// One thread per 8 consecutive X values: writes them as fp16 at their place in
-// the step order, and (lanes q = 0 / 1 of each sub-block's four) the sub-block
-// sum's fp16 hi / lo parts: xsp[t][blk][0..7] = hi, [8..15] = lo.
-__global__ __launch_bounds__(256) void gemm_prep_x(const uint16_t* __restrict__ x,
-                                                   _Float16* __restrict__ xp,
+// X prepared for the main kernel: fp16 in MFMA fragment order.  Chunk
+// (m16, s) is 1 KB: lane 16 c + r holds the 8 values of row 16 m16 + r that
+// K step s gives lane group c (sub-block 4 (t / 4) + c of super-block s / 8,
+// at offset 8 (t % 4), t = s % 8).  Rows are padded to a multiple of 16 with
+// copies of row M - 1.  Sub-block sums: chunk (m16, super-block) is 512 B:
+// lane r holds the fp16 hi parts of row 16 m16 + r's 8 sums, lane 16 + r their
+// lo parts.  One workgroup per (16 rows, super-block): each thread reads 8
+// consecutive values of a row (coalesced), the tile is reordered in LDS, and
+// the 8 chunks of the super-block, contiguous in xp, are written as one 8 KB
+// run.
+__global__ __launch_bounds__(512) void gemm_prep_x(const uint16_t* __restrict__ x, _Float16* __restrict__ xp,
                                                    _Float16* __restrict__ xsp, int M, int K) {
-  const long groups = K / 8, total = (long)M * groups;
-  const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  const bool live = gid < total;
-  const long g = live ? gid : total - 1;  // every lane takes part in the shuffles
-  const int m = (int)(g / groups), e8 = (int)(g % groups);
-  const int q = e8 & 3, sbg = e8 >> 2, blk = sbg >> 3, gl = sbg & 7;
-  const uint4 v = *reinterpret_cast<const uint4*>(x + (size_t)m * K + (size_t)e8 * 8);
+  __shared__ h8 tile[512];
+  const int blk = blockIdx.x, m16 = blockIdx.y, nblk = K / 256;
+  const int r = threadIdx.x >> 5, p = threadIdx.x & 31;  // row in the tile, 8-value piece of the super-block
+  const int sb = p >> 2, q = p & 3;
+  const uint4 v = *reinterpret_cast<const uint4*>(x + (size_t)min(16 * m16 + r, M - 1) * K + (size_t)blk * 256 + 8 * p);
   const uint32_t d[4] = {v.x, v.y, v.z, v.w};
   h8 h;
   float sum = 0.f;
@@ -83,17 +85,19 @@ __global__ __launch_bounds__(256) void gemm_prep_x(const uint16_t* __restrict__ 
     sum += a;
     sum += b;
   }
-  const int t = 4 * (gl >> 2) + q, c = gl & 3;
-  if (live) *reinterpret_cast<h8*>(xp + (size_t)m * K + (size_t)blk * 256 + t * 32 + c * 8) = h;
-  // lanes 4i .. 4i+3 hold one sub-block (groups is a multiple of 4); a + b is
-  // commutative, so all four lanes end with the same sum
+  const int t = 4 * (sb >> 2) + q, c = sb & 3;
+  tile[t * 64 + 16 * c + r] = h;
+  // lanes 4i .. 4i+3 hold one sub-block; a + b is commutative, so all four
+  // lanes end with the same sum
   sum += __shfl_xor(sum, 1);
   sum += __shfl_xor(sum, 2);
   const _Float16 hi = (_Float16)sum;
   const _Float16 lo = (_Float16)(sum - (float)hi);
-  _Float16* o = xsp + ((size_t)m * (K / 256) + blk) * 16;
-  if (live && q == 0) o[gl] = hi;
-  if (live && q == 1) o[8 + gl] = lo;
+  _Float16* o = xsp + ((size_t)m16 * nblk + blk) * 256;
+  if (q == 0) o[r * 8 + sb] = hi;
+  if (q == 1) o[(16 + r) * 8 + sb] = lo;
+  __syncthreads();
+  reinterpret_cast<h8*>(xp)[((size_t)m16 * (K / 32) + (size_t)blk * 8) * 64 + threadIdx.x] = tile[threadIdx.x];
 }
 
 // Two 4-bit codes per byte -> 8 fp16 values s*q in element order (byte i:
@@ -125,27 +129,68 @@ __device__ __forceinline__ void bytes_to_f16(uint32_t b, uint32_t* r) {
   }
 }
 
-// blockIdx.z selects split z of the K range (split = gridDim.z); split z
-// writes its partial product to y + z * M * N (a workspace when split > 1).
-template <int MT>
-__global__ __launch_bounds__(256, 2) void gemm_q4k_mfma(const uint8_t* __restrict__ w,
+// One 16-byte load per lane straight into LDS: lane l writes bytes
+// [16 l, 16 l + 16) above the wave-uniform LDS offset lds.  Written as inline
+// assembly so that the compiler, which cannot tell which LDS buffer such a load
+// fills, does not wait for it before every LDS read; the kernel waits for its
+// own loads (vmcnt(0)) before the barrier that publishes a stage.  M0 is
+// restored.
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+  uint32_t keep;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %2, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(keep)
+               : "s"(lds), "v"(g)
+               : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// All of this wave's LDS loads have landed; then every wave's have.  The
+// scheduling barriers keep the next stage's work (which consumes registers
+// loaded during this stage) from being hoisted above the wait: the compiler
+// does not count the inline-assembly loads, so an early wait it placed for a
+// register load would also drain the next stage's LDS loads.
+__device__ __forceinline__ void publish_stage() {
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0)
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Workgroup tile (16 MT) x (32 WAVES): each wave owns 32 columns and all
+// 16 MT rows.  K runs in stages of 4 MFMA steps (half a super-block); the X
+// chunks of a stage (MT per step) and the sub-block sums of a super-block are
+// loaded straight into LDS one stage ahead, double-buffered, and the weights
+// of a stage are loaded into registers one stage ahead, so one wait and one
+// barrier per stage cover every load.  blockIdx.z selects split z of the K
+// range (split = gridDim.z); split z writes its partial product to
+// y + z * M * N (a workspace when split > 1).
+template <int MT, int WAVES>
+__global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void gemm_q4k_mfma(const uint8_t* __restrict__ w,
                                                         const _Float16* __restrict__ xp,
                                                         const _Float16* __restrict__ xsp,
                                                         float* __restrict__ y, int M, int N, int K) {
-  constexpr int BM = 16 * MT;
-  constexpr int XCH = BM * 4 / 256;  // 16-byte X chunks per thread per step
-  constexpr int SS = 32;                   // LDS row stride (halves) of the sub-block sums
-  constexpr int SCH = BM * 4 / 256;        // 8-byte pieces of sub-block sums per thread
-  __shared__ __align__(16) _Float16 xs[2][BM * XS];
-  __shared__ __align__(16) _Float16 xsum[BM * SS];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  static_assert(MT == 8 && (WAVES == 4 || WAVES == 8), "the waves move the 8 X chunks of a step evenly");
+  constexpr int BM = 16 * MT, BN = 32 * WAVES;
+  constexpr int XPW = MT / WAVES;  // X chunks each wave moves per step
+  constexpr int CH = MT * 64;  // h8 slots of one step's X in LDS
+  __shared__ __align__(16) h8 xa[4 * CH];  // stages 2b (first half of a super-block)
+  __shared__ __align__(16) h8 xb[4 * CH];  // stages 2b + 1
+  __shared__ __align__(16) h8 xsl[2][MT / 2 * 64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int c = lane >> 4;  // lane group: k = 8c .. 8c+7 of each step
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-  const int nblk = K / 256, z = blockIdx.z, nz = gridDim.z;
+  const int nblk = K / 256, S = K / 32, z = blockIdx.z, nz = gridDim.z;
   const int b_begin = (int)((long)nblk * z / nz), b_end = (int)((long)nblk * (z + 1) / nz);
-  const int s0 = b_begin * 8, steps = (b_end - b_begin) * 8;  // K steps of this split
+  const int nb = b_end - b_begin, last_step = 8 * nb - 1;
   y += (size_t)z * M * N;
   const size_t row_bytes = (size_t)nblk * 144;
-  const int c = lane >> 4;  // lane group: k = 8c .. 8c+7 of each step
+  const int m16 = m0 >> 4, M16 = (M + 15) >> 4;
 
   // weight rows of this lane's B fragments (clamped; columns past N are not stored)
   const uint8_t* wrow[NT];
@@ -154,65 +199,45 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_mfma(const uint8_t* __restric
     const int n = min(n0 + 32 * wave + 16 * j + (lane & 15), N - 1);
     wrow[j] = w + (size_t)n * row_bytes;
   }
-  // X staging: chunk i of thread t is row (t + 256 i) / 4, 16-byte piece t % 4
-  const _Float16* xsrc[XCH];
-  int xdst[XCH];
+  // this wave moves X chunks XPW wave .. XPW wave + XPW - 1 of every step
+  // (row tiles past the padded M are clamped: their rows are never stored);
+  // waves 0-3 move the sum chunks of a super-block, wave w chunks 2 w (lanes
+  // 0-31) and 2 w + 1 (lanes 32-63)
+  const _Float16* xsrc[XPW];
 #pragma unroll
-  for (int i = 0; i < XCH; i++) {
-    const int ch = threadIdx.x + 256 * i, r = ch >> 2, pc = ch & 3;
-    xsrc[i] = xp + (size_t)min(m0 + r, M - 1) * K + 8 * pc;
-    xdst[i] = r * XS + 8 * pc;
-  }
-  u32x4 xq[PF][XCH];
-  auto fetch_x = [&](int s, auto slot_c) {
-    constexpr int slot = decltype(slot_c)::value;
-    const size_t off = (size_t)(s0 + min(s, steps - 1)) * BK;
+  for (int i = 0; i < XPW; i++) xsrc[i] = xp + (size_t)min(m16 + XPW * wave + i, M16 - 1) * S * 512 + lane * 8;
+  const _Float16* ssrc = xsp + (size_t)min(m16 + 2 * (wave & 3) + (lane >> 5), M16 - 1) * nblk * 256 + (lane & 31) * 8;
+  const uint32_t lds_a = lds_offset(xa) + wave * XPW * 1024, lds_b = lds_offset(xb) + wave * XPW * 1024;
+  auto stage_x = [&](int g, uint32_t base) {
 #pragma unroll
-    for (int i = 0; i < XCH; i++) xq[slot][i] = *reinterpret_cast<const u32x4*>(xsrc[i] + off);
-  };
-  auto store_x = [&](auto slot_c, auto buf_c) {
-    constexpr int slot = decltype(slot_c)::value, buf = decltype(buf_c)::value;
+    for (int t = 0; t < 4; t++) {
+      const size_t s = (size_t)(8 * b_begin + min(4 * g + t, last_step)) * 512;
 #pragma unroll
-    for (int i = 0; i < XCH; i++) *reinterpret_cast<u32x4*>(&xs[buf][xdst[i]]) = xq[slot][i];
-  };
-
-  // Sub-block sums of the current super-block: loaded at step 0, written to
-  // LDS at step 6, read after step 7 (piece i of thread t: row (t + 256 i) / 4,
-  // halves 4 * (t % 4) .. +4 of hi[8] | lo[8])
-  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-  u32x2 sq[SCH];
-  auto fetch_sums = [&](int b) {
-#pragma unroll
-    for (int i = 0; i < SCH; i++) {
-      const int ch = threadIdx.x + 256 * i, r = ch >> 2;
-      sq[i] = *reinterpret_cast<const u32x2*>(xsp + ((size_t)min(m0 + r, M - 1) * nblk + b_begin + b) * 16 + 4 * (ch & 3));
+      for (int i = 0; i < XPW; i++) dma16(xsrc[i] + s, base + t * 8192 + i * 1024);
     }
   };
-  auto store_sums = [&]() {
-#pragma unroll
-    for (int i = 0; i < SCH; i++) {
-      const int ch = threadIdx.x + 256 * i;
-      *reinterpret_cast<u32x2*>(&xsum[(ch >> 2) * SS + 4 * (ch & 3)]) = sq[i];
-    }
+  auto stage_sums = [&](int b) {
+    if (wave < 4)
+      dma16(ssrc + (size_t)(b_begin + min(b, nb - 1)) * 256, lds_offset(&xsl[b & 1][0]) + wave * 1024);
   };
 
-  // Weights, loaded a whole super-block (8 steps) ahead into queue registers:
-  // the header (d|dmin, scale bytes 0-3, 4-7, 8-11) with the 16 code bytes of
-  // sub-block c (used in steps 0-3) at step 0 of the previous super-block, the
-  // 16 code bytes of sub-block 4+c (steps 4-7) at its step 4.
-  u32x4a4 hdrq[NT], code0q[NT], code1q[NT], code0[NT], code1[NT];
-  auto wptr = [&](int j, int b) { return wrow[j] + (size_t)(b_begin + min(b, b_end - b_begin - 1)) * 144; };
-  auto fetch_head = [&](int b) {
+  // Weights of super-block b: the header (d|dmin, scale bytes 0-3, 4-7, 8-11)
+  // and the 16 code bytes of sub-block c (steps 0-3) are loaded during the
+  // second stage of super-block b - 1; the code bytes of sub-block 4 + c
+  // (steps 4-7) during the first stage of b.
+  u32x4a4 hdr_n[NT], cd0_n[NT], cd0[NT], cd1[NT];
+  auto wptr = [&](int j, int b) { return wrow[j] + (size_t)(b_begin + min(b, nb - 1)) * 144; };
+  auto fetch_first = [&](int b) {
 #pragma unroll
     for (int j = 0; j < NT; j++) {
       const uint8_t* p = wptr(j, b);
-      hdrq[j] = *reinterpret_cast<const u32x4a4*>(p);
-      code0q[j] = *reinterpret_cast<const u32x4a4*>(p + 16 + 16 * c);
+      hdr_n[j] = *reinterpret_cast<const u32x4a4*>(p);
+      cd0_n[j] = *reinterpret_cast<const u32x4a4*>(p + 16 + 16 * c);
     }
   };
-  auto fetch_tail = [&](int b) {
+  auto fetch_second = [&](int b) {
 #pragma unroll
-    for (int j = 0; j < NT; j++) code1q[j] = *reinterpret_cast<const u32x4a4*>(wptr(j, b) + 16 + 16 * (4 + c));
+    for (int j = 0; j < NT; j++) cd1[j] = *reinterpret_cast<const u32x4a4*>(wptr(j, b) + 16 + 16 * (4 + c));
   };
 
   f4 acc[MT][NT], tot[MT][NT];
@@ -221,55 +246,20 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_mfma(const uint8_t* __restric
 #pragma unroll
     for (int j = 0; j < NT; j++) tot[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
-  // halves 16..31 of every sub-block-sum row stay zero: lanes 32-63 read them
-  // as their part of the min-term A operand
-  for (int r = threadIdx.x; r < BM; r += 256)
-    *reinterpret_cast<u32x4*>(&xsum[r * SS + 16]) = *reinterpret_cast<u32x4*>(&xsum[r * SS + 24]) = u32x4{0u, 0u, 0u, 0u};
-  fetch_head(0);
-  fetch_tail(0);
-  fetch_x(0, std::integral_constant<int, 0>{});
-  fetch_x(1, std::integral_constant<int, 1>{});
-  fetch_x(2, std::integral_constant<int, 2>{});
-  fetch_x(3, std::integral_constant<int, 3>{});
-  fetch_x(4, std::integral_constant<int, 4>{});
-  fetch_x(5, std::integral_constant<int, 5>{});
-  fetch_x(6, std::integral_constant<int, 6>{});
-  fetch_x(7, std::integral_constant<int, 7>{});
-  store_x(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
-  __syncthreads();
-
-  // One MFMA step t of super-block b (K step s = 8b + t); X of step s is in LDS
-  // buffer t % 2; queue slot t holds X of step s until step s-1 stored it.
-  auto step = [&](auto t_c, int s, int b, const uint32_t (&s2)[NT][2]) {
-    constexpr int t = decltype(t_c)::value, slot = t & 1;
-    if (t == 4) {  // sub-block 4+c codes arrive for steps 4-7; queue the next ones
-#pragma unroll
-      for (int j = 0; j < NT; j++) code1[j] = code1q[j];
-      fetch_tail(b + 1);
-    }
+  // One MFMA step t (0-7) of a super-block, X from LDS stage buffer xs
+  auto step = [&](auto t_c, const h8* xs, const uint32_t (&s2)[NT][2], const u32x4a4 (&cd)[NT]) {
+    constexpr int t = decltype(t_c)::value;
     h8 bf[NT];
 #pragma unroll
     for (int j = 0; j < NT; j++) {
-      const u32x4a4 cw = t < 4 ? code0[j] : code1[j];
-      const uint32_t qd = (t & 3) == 0 ? cw.x : (t & 3) == 1 ? cw.y : (t & 3) == 2 ? cw.z : cw.w;
+      const uint32_t qd = (t & 3) == 0 ? cd[j].x : (t & 3) == 1 ? cd[j].y : (t & 3) == 2 ? cd[j].z : cd[j].w;
       bf[j] = codes_times_s(qd, s2[j][t >> 2]);
     }
-    if (t == 0) fetch_sums(b);
-    if (t == 6) store_sums();
-    // X of step s+1 goes to the other LDS buffer (its readers finished at the
-    // barrier that ended step s-1; after the last step it is never read, and
-    // the clamped fetch kept it in bounds); queue slot t is refilled with step
-    // s+8.  No branch here: a load consumed under a branch costs a full
-    // vmcnt(0) wait.
-    store_x(std::integral_constant<int, (t + 1) & 7>{}, std::integral_constant<int, slot ^ 1>{});
-    fetch_x(s + PF, std::integral_constant<int, t>{});
-    // A fragments in groups of four (fewer registers live at once)
 #pragma unroll
     for (int m4 = 0; m4 < MT; m4 += 4) {
       h8 a[4];
 #pragma unroll
-      for (int u = 0; u < 4; u++)
-        a[u] = *reinterpret_cast<const h8*>(&xs[slot][((m4 + u) * 16 + (lane & 15)) * XS + 8 * c]);
+      for (int u = 0; u < 4; u++) a[u] = xs[((t & 3) * MT + m4 + u) * 64 + lane];
 #pragma unroll
       for (int u = 0; u < 4; u++)
 #pragma unroll
@@ -277,29 +267,25 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_mfma(const uint8_t* __restric
           acc[m4 + u][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
               a[u], bf[j], t == 0 ? f4{0.f, 0.f, 0.f, 0.f} : acc[m4 + u][j], 0, 0, 0);
     }
-    // LDS-only barrier: the prefetched global loads stay in flight
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
   };
 
-  const int nb = b_end - b_begin;
+  fetch_first(0);
+  stage_x(0, lds_a);
+  stage_sums(0);
   for (int b = 0; b < nb; b++) {
-    const int s = 8 * b;
+    // ---- first stage of super-block b (steps 0-3, buffer xa)
+    publish_stage();
+    fetch_second(b);
+    stage_x(2 * b + 1, lds_b);
     // this super-block's scales (reference unpacking, compute.rs:724-735):
     // s[0..3] = sc[0..3] & 63, s[4..7] = sc[0..3] >> 6 | (sc[8..11] & 15) << 2,
     // m[0..3] = sc[4..7] & 63, m[4..7] = sc[4..7] >> 6 | (sc[8..11] >> 4) << 2
     uint32_t s2[NT][2], mlo[NT], mhi[NT], dbits[NT];
-    u32x4a4 hdr[NT];
 #pragma unroll
     for (int j = 0; j < NT; j++) {
-      hdr[j] = hdrq[j];
-      code0[j] = code0q[j];
-    }
-    fetch_head(b + 1);
-#pragma unroll
-    for (int j = 0; j < NT; j++) {
-      const uint32_t h1 = hdr[j].y, h2v = hdr[j].z, h3 = hdr[j].w;
+      const u32x4a4 hdr = hdr_n[j];
+      cd0[j] = cd0_n[j];
+      const uint32_t h1 = hdr.y, h2v = hdr.z, h3 = hdr.w;
       const uint32_t slo = h1 & 0x3F3F3F3Fu;
       const uint32_t shi = ((h1 >> 6) & 0x03030303u) | ((h3 & 0x0F0F0F0Fu) << 2);
       mlo[j] = h2v & 0x3F3F3F3Fu;
@@ -307,16 +293,21 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_mfma(const uint8_t* __restric
       const uint32_t sa = (slo >> (8 * c)) & 0xFFu, sb = (shi >> (8 * c)) & 0xFFu;
       s2[j][0] = sa | (sa << 16);
       s2[j][1] = sb | (sb << 16);
-      dbits[j] = hdr[j].x;
+      dbits[j] = hdr.x;
     }
-    step(std::integral_constant<int, 0>{}, s, b, s2);
-    step(std::integral_constant<int, 1>{}, s + 1, b, s2);
-    step(std::integral_constant<int, 2>{}, s + 2, b, s2);
-    step(std::integral_constant<int, 3>{}, s + 3, b, s2);
-    step(std::integral_constant<int, 4>{}, s + 4, b, s2);
-    step(std::integral_constant<int, 5>{}, s + 5, b, s2);
-    step(std::integral_constant<int, 6>{}, s + 6, b, s2);
-    step(std::integral_constant<int, 7>{}, s + 7, b, s2);
+    step(std::integral_constant<int, 0>{}, xa, s2, cd0);
+    step(std::integral_constant<int, 1>{}, xa, s2, cd0);
+    step(std::integral_constant<int, 2>{}, xa, s2, cd0);
+    step(std::integral_constant<int, 3>{}, xa, s2, cd0);
+    // ---- second stage (steps 4-7, buffer xb)
+    publish_stage();
+    fetch_first(b + 1);
+    stage_x(2 * b + 2, lds_a);
+    stage_sums(b + 1);
+    step(std::integral_constant<int, 4>{}, xb, s2, cd1);
+    step(std::integral_constant<int, 5>{}, xb, s2, cd1);
+    step(std::integral_constant<int, 6>{}, xb, s2, cd1);
+    step(std::integral_constant<int, 7>{}, xb, s2, cd1);
     // min term: A = XS hi (lanes 0-15) / lo (16-31) / zeros (32-63), B = the
     // 8 mins m in every lane group (finite, so the zero A lanes add 0)
     h8 bmin[NT];
@@ -327,12 +318,15 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_mfma(const uint8_t* __restric
       bytes_to_f16(mlo[j], mv);
       bytes_to_f16(mhi[j], mv + 2);
       bmin[j] = __builtin_bit_cast(h8, u32x4{mv[0], mv[1], mv[2], mv[3]});
-      dd[j] = f16_to_f32(dbits[j] & 0xFFFFu);
-      dm[j] = f16_to_f32(dbits[j] >> 16);
+      // opaque: kept as f32 values, not folded into v_fma_mix_f32 (slower here)
+      dd[j] = __uint_as_float(opaque(__float_as_uint(f16_to_f32(dbits[j] & 0xFFFFu))));
+      dm[j] = __uint_as_float(opaque(__float_as_uint(f16_to_f32(dbits[j] >> 16))));
     }
+    const h8* sums = &xsl[b & 1][0];
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
-      const h8 amin = *reinterpret_cast<const h8*>(&xsum[(mt * 16 + (lane & 15)) * SS + 8 * c]);
+      const h8 raw = sums[(mt >> 1) * 64 + (mt & 1) * 32 + (lane & 31)];
+      const h8 amin = lane < 32 ? raw : h8{};
 #pragma unroll
       for (int j = 0; j < NT; j++) {
         const f4 qm = __builtin_amdgcn_mfma_f32_16x16x32_f16(amin, bmin[j], f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
@@ -344,6 +338,8 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_mfma(const uint8_t* __restric
       }
     }
   }
+  // the last stage's loads (clamped repeats) land before the workgroup's LDS is released
+  __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
 
   // C fragment layout: element i of acc[mt][j] is row 4*(lane/16)+i, column lane%16
 #pragma unroll
@@ -379,26 +375,30 @@ bool gemm_q4k_mfma_ok(const void* w, const void* x) {
 
 namespace {
 
-// Workgroup tiles are 64 (M) x 128 (N): 16 x 4 = 64 rows per wave.  128-row
-// tiles would halve the B-fragment work per MFMA but need more than the 256
-// registers two waves per SIMD allow (measured: 31 spilled).
-constexpr int kMT = 4;
+// Workgroup tiles are 128 (M) x 256 (N): eight waves, each 128 rows x 32
+// columns, one workgroup per CU.  Sharing each X tile among 256 columns halves
+// the X traffic from L2 of 128-column tiles, which bounds this kernel.
+constexpr int kMT = 8, kWaves = 8, kBN = 32 * kWaves;
 
-// K splits for a GEMM: enough workgroups for two per CU, at most 8 splits and
-// never more than one split per 256-element block.
+// K splits for a GEMM: none while the tiles fill at least half of the
+// workgroup slots (8 / kWaves per CU) (a split costs a partial product per split written
+// and summed again); below that, as many as still fit one round of slots (at
+// most 8, at most one per 256-element block).
 int gemm_split(size_t M, size_t N, size_t K) {
   const size_t bm = 16 * (size_t)kMT;
-  const size_t tiles = ((N + BN - 1) / BN) * ((M + bm - 1) / bm);
-  const size_t want = 2 * (size_t)device_cu_count();
-  size_t split = tiles >= want ? 1 : (want + tiles - 1) / tiles;
-  split = std::min<size_t>(split, 8);
-  split = std::min<size_t>(split, K / 256);
+  const size_t tiles = ((N + kBN - 1) / kBN) * ((M + bm - 1) / bm);
+  const size_t slots = (size_t)(8 / kWaves) * (size_t)device_cu_count();
+  if (2 * tiles >= slots) return 1;
+  const size_t split = std::min<size_t>(std::min<size_t>(slots / tiles, 8), K / 256);
   return (int)std::max<size_t>(split, 1);
 }
 
-// workspace layout: X in step order (M*K fp16) | sub-block sums (M*K/256*16
-// fp16) | split partials (split*M*N f32)
-size_t prep_bytes(size_t M, size_t K) { return M * K * 2 + M * (K / 256) * 32; }
+// workspace layout: X in fragment order (M16*K fp16, M16 = M rounded up to
+// 16) | sub-block sums (M16*K/256*16 fp16) | split partials (split*M*N f32)
+size_t prep_bytes(size_t M, size_t K) {
+  const size_t M16 = (M + 15) / 16 * 16;
+  return M16 * K * 2 + M16 * (K / 256) * 32;
+}
 
 }  // namespace
 
@@ -417,18 +417,19 @@ hipError_t launch_gemm_q4k(const uint8_t* w, const uint16_t* x, float* y, size_t
     const size_t need = prep_bytes(M, K) + (split > 1 ? (size_t)split * M * N * sizeof(float) : 0);
     if (workspace_bytes < need) return hipErrorInvalidValue;
     _Float16* xp = static_cast<_Float16*>(workspace);
-    _Float16* xsp = xp + M * K;
+    _Float16* xsp = xp + (M + 15) / 16 * 16 * K;
     float* part = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + prep_bytes(M, K));
-    const size_t groups = M * K / 8;
-    hipLaunchKernelGGL(gemm_prep_x, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, s, x, xp, xsp,
-                       (int)M, (int)K);
+    const dim3 pgrid((unsigned)(K / 256), (unsigned)((M + 15) / 16));
+    if (pgrid.y > 65535) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(gemm_prep_x, pgrid, dim3(512), 0, s, x, xp, xsp, (int)M, (int)K);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int bm = 16 * kMT;
-    const dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + bm - 1) / bm), (unsigned)split);
+    const dim3 grid((unsigned)((N + kBN - 1) / kBN), (unsigned)((M + bm - 1) / bm), (unsigned)split);
     if (grid.y > 65535) return hipErrorInvalidValue;
     float* dst = split > 1 ? part : y;
-    hipLaunchKernelGGL(gemm_q4k_mfma<kMT>, grid, dim3(256), 0, s, w, xp, xsp, dst, (int)M, (int)N, (int)K);
+    hipLaunchKernelGGL((gemm_q4k_mfma<kMT, kWaves>), grid, dim3(64 * kWaves), 0, s, w, xp, xsp, dst, (int)M, (int)N,
+                       (int)K);
     e = hipGetLastError();
     if (e != hipSuccess || split == 1) return e;
     const size_t mn = M * N;

@@ -311,29 +311,41 @@ def extras(torch, ssdq, synth, timer, np):
         "GB/s": round(hb / el / 1e9, 2), "us": round(el * 1e6, 1),
         "note": "ssdq_matvec_quantized: host W and x copied in, y copied out, per call"}
 
-    # config 4: one Llama-3-8B layer of Q4_K prefill GEMMs at M = 512
+    # config 4: one Llama-3-8B layer of Q4_K prefill GEMMs at M = 512.  q/k/v
+    # and gate/up read the same X and run as one GEMM each (multi entry point);
+    # the seven separate GEMMs are timed as well.
     layer = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
              ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]
     M = 512
-    mats = []
+    W, Y = {}, {}
     flops = 0
     for i, (nm, N, K) in enumerate(layer):
-        w = torch.from_numpy(synth.quant_weights(ssdq.Q4_K, N, K, synth.seed(4, i))).cuda()
-        x = torch.randn(M, K, device="cuda").to(torch.bfloat16).view(torch.int16)
-        y = torch.empty(M * N, device="cuda")
-        mats.append((w, x, y, N, K))
+        W[nm] = torch.from_numpy(synth.quant_weights(ssdq.Q4_K, N, K, synth.seed(4, i))).cuda()
+        Y[nm] = torch.empty(M * N, device="cuda")
         flops += 2.0 * M * N * K
+    X = {4096: torch.randn(M, 4096, device="cuda").to(torch.bfloat16).view(torch.int16),
+         14336: torch.randn(M, 14336, device="cuda").to(torch.bfloat16).view(torch.int16)}
+    dims = {nm: (N, K) for nm, N, K in layer}
+    groups = [("q", "k", "v"), ("o",), ("gate", "up"), ("down",)]
 
-    def layer_step(i):
-        for w, x, y, N, K in mats:
-            ssdq.gemm_q4k_bf16(w, x, y, M, N, K)
+    def layer_fused(i):
+        for g in groups:
+            K = dims[g[0]][1]
+            ssdq.gemm_q4k_bf16_multi([W[n] for n in g], X[K], [Y[n] for n in g], M, [dims[n][0] for n in g], K)
 
-    t, _, _ = timer.run(layer_step, 5, 1, graph=False)
+    def layer_separate(i):
+        for nm, N, K in layer:
+            ssdq.gemm_q4k_bf16(W[nm], X[K], Y[nm], M, N, K)
+
+    t, _, _ = timer.run(layer_fused, 5, 1, graph=False)
+    t_sep, _, _ = timer.run(layer_separate, 5, 1, graph=False)
     tfl = flops / (t / 5) / 1e12
     out["prefill_gemm_q4k_layer_m512"] = {"TFLOP/s": round(tfl, 2),
                                           "pct_bf16_peak": round(100 * tfl / BF16_PEAK_TFLOPS, 2),
-                                          "ms_per_layer": round(t / 5 * 1e3, 3)}
-    del mats
+                                          "ms_per_layer": round(t / 5 * 1e3, 3),
+                                          "ms_per_layer_seven_separate_gemms": round(t_sep / 5 * 1e3, 3),
+                                          "note": "q/k/v and gate/up each one GEMM over shared X"}
+    del W, Y, X
     torch.cuda.empty_cache()
 
     # config 5a: INT8 quantize of 8 x 32768 tokens x {K, V} x 1024

@@ -199,6 +199,15 @@ int ssdq_rmsnorm_dev(const float* x, const float* residual, const float* weight,
  * compute.rs:707-750); this computes the same Y in one pass. K % 256 == 0. */
 int ssdq_gemm_q4k_bf16_dev(const void* w, const uint16_t* x_bf16, float* y, size_t M,
                            size_t N, size_t K, ssdq_stream_t stream);
+/* The same for count = 1..3 Q4_K matrices that read the same X: Y_i[M, n[i]] =
+ * X W_i^T, computed as one GEMM over the concatenated columns with X prepared
+ * once.  Replaces the per-token q/k/v (or gate/up) matvecs of one layer's
+ * prefill, which the reference runs on one shared input per token
+ * (transformer.rs:166-196 -> multi_head_attention_fused_rope; the FFN's gate
+ * and up, feed_forward.rs:28-40).  Every n[i] >= 1; K % 256 == 0. */
+int ssdq_gemm_q4k_bf16_multi_dev(const void* const* w, const size_t* n, size_t count,
+                                 const uint16_t* x_bf16, float* const* y, size_t M, size_t K,
+                                 ssdq_stream_t stream);
 
 /* ------------------------------------------------------ INT8 KV cache */
 /* Per-row absmax INT8 quantization, bit-exact codes and scales:

@@ -505,22 +505,42 @@ int ssdq_rmsnorm_matvec_dev(int dtype, const void* w, const float* x, const floa
   return ssdq_matvec_dev(dtype, w, (const float*)tmp, y, out_dim, n_embd, 1, stream);
 }
 
+namespace {
+int gemm_multi(const char* fn, const void* const* w, const size_t* n, size_t count, const uint16_t* x,
+               float* const* y, size_t M, size_t K, ssdq_stream_t stream) {
+  if (count < 1 || count > 3) return fail(SSDQ_ERR_INVALID_ARG, "%s: count must be 1, 2 or 3", fn);
+  if (!w || !n || !y || !x) return fail(SSDQ_ERR_INVALID_ARG, "%s: NULL pointer", fn);
+  size_t N = 0;
+  for (size_t i = 0; i < count; i++) {
+    if (!w[i] || !y[i]) return fail(SSDQ_ERR_INVALID_ARG, "%s: NULL pointer", fn);
+    if (n[i] == 0) return fail(SSDQ_ERR_INVALID_ARG, "%s: every matrix needs at least one row", fn);
+    N += n[i];
+  }
+  if (M == 0) return ok();
+  if (K == 0 || K % 256) return fail(SSDQ_ERR_INVALID_ARG, "%s: K must be a positive multiple of 256", fn);
+  if (!fits_int(M) || !fits_int(N) || !fits_int(K) || !fits_int(M * K) || !fits_int(M * N))
+    return fail(SSDQ_ERR_INVALID_ARG, "%s: dimensions exceed 2^31", fn);
+  hipStream_t s = (hipStream_t)stream;
+  const uint8_t* const* wb = reinterpret_cast<const uint8_t* const*>(w);
+  const size_t wsb = ssdq::gemm_q4k_workspace_bytes(w, n, (int)count, x, M, K);
+  void* ws = nullptr;
+  hipError_t e = hipSuccess;
+  if (wsb && (e = workspace_get(wsb, s, &ws)) != hipSuccess) return hip_fail(e, "ssdq_gemm_q4k_bf16 workspace");
+  e = ssdq::launch_gemm_q4k(wb, n, (int)count, x, y, M, K, ws, wsb, s);
+  if (e != hipSuccess) return hip_fail(e, fn);
+  return ok();
+}
+}  // namespace
+
 int ssdq_gemm_q4k_bf16_dev(const void* w, const uint16_t* x, float* y, size_t M, size_t N,
                            size_t K, ssdq_stream_t stream) {
   if (M == 0 || N == 0) return ok();
-  if (!w || !x || !y) return fail(SSDQ_ERR_INVALID_ARG, "ssdq_gemm_q4k_bf16_dev: NULL pointer");
-  if (K == 0 || K % 256) return fail(SSDQ_ERR_INVALID_ARG, "ssdq_gemm_q4k_bf16_dev: K must be a positive multiple of 256");
-  if (!fits_int(M) || !fits_int(N) || !fits_int(K) || !fits_int(M * K) || !fits_int(M * N))
-    return fail(SSDQ_ERR_INVALID_ARG, "ssdq_gemm_q4k_bf16_dev: dimensions exceed 2^31");
-  hipStream_t s = (hipStream_t)stream;
-  const size_t wsb = ssdq::gemm_q4k_workspace_bytes(w, x, M, N, K);
-  void* ws = nullptr;
-  hipError_t e = hipSuccess;
-  if (wsb && (e = workspace_get(wsb, s, &ws)) != hipSuccess)
-    return hip_fail(e, "ssdq_gemm_q4k_bf16_dev: workspace");
-  e = ssdq::launch_gemm_q4k((const uint8_t*)w, x, y, M, N, K, ws, wsb, s);
-  if (e != hipSuccess) return hip_fail(e, "ssdq_gemm_q4k_bf16_dev");
-  return ok();
+  return gemm_multi("ssdq_gemm_q4k_bf16_dev", &w, &N, 1, x, &y, M, K, stream);
+}
+
+int ssdq_gemm_q4k_bf16_multi_dev(const void* const* w, const size_t* n, size_t count, const uint16_t* x_bf16,
+                                 float* const* y, size_t M, size_t K, ssdq_stream_t stream) {
+  return gemm_multi("ssdq_gemm_q4k_bf16_multi_dev", w, n, count, x_bf16, y, M, K, stream);
 }
 
 int ssdq_kv_quantize_rows_dev(const float* in, int8_t* codes, float* scales, size_t n_rows,

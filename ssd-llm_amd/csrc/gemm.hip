@@ -161,19 +161,46 @@ __device__ __forceinline__ void publish_stage() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
+// Up to three Q4_K matrices with the same K that share X, as one GEMM over
+// their concatenated columns: matrix i has columns start_i .. start_{i+1} - 1
+// (start_0 = 0, start_3 = N; absent matrices have start = N).  The kernels take
+// the fields as separate scalar arguments: inside one aggregate, the selects
+// below fold into a run-time index, which puts the arguments in private
+// memory.
+struct GemmMats {
+  const uint8_t* w0;
+  const uint8_t* w1;
+  const uint8_t* w2;
+  float* y0;
+  float* y1;
+  float* y2;
+  int start1, start2;
+};
+#define GEMM_MATS_PARAMS                                                                            \
+  const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, const uint8_t *__restrict__ w2, \
+      float *__restrict__ y0, float *__restrict__ y1, float *__restrict__ y2, int start1, int start2
+#define GEMM_MATS_ARGS(m) m.w0, m.w1, m.w2, m.y0, m.y1, m.y2, m.start1, m.start2
+// column c (< N) -> matrix, its first column, its weights and output
+#define GEMM_SEGMENT(c) (MULTI ? ((c) >= start1) + ((c) >= start2) : 0)
+#define GEMM_FIRST(sg) ((sg) == 0 ? 0 : (sg) == 1 ? start1 : (sg) == 2 ? start2 : N)
+#define GEMM_WEIGHTS(sg) ((sg) == 0 ? w0 : (sg) == 1 ? w1 : w2)
+#define GEMM_OUT(sg) ((sg) == 0 ? y0 : (sg) == 1 ? y1 : y2)
+
 // Workgroup tile (16 MT) x (32 WAVES): each wave owns 32 columns and all
 // 16 MT rows.  K runs in stages of 4 MFMA steps (half a super-block); the X
 // chunks of a stage (MT per step) and the sub-block sums of a super-block are
 // loaded straight into LDS one stage ahead, double-buffered, and the weights
 // of a stage are loaded into registers one stage ahead, so one wait and one
-// barrier per stage cover every load.  blockIdx.z selects split z of the K
-// range (split = gridDim.z); split z writes its partial product to
-// y + z * M * N (a workspace when split > 1).
-template <int MT, int WAVES>
-__global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void gemm_q4k_mfma(const uint8_t* __restrict__ w,
+// barrier per stage cover every load.  The N columns are those of up to three
+// matrices that share X, concatenated (GemmMats).  blockIdx.z selects split z
+// of the K range (split = gridDim.z); with one split the results go to the
+// matrices' own outputs, otherwise split z writes its partial product of the
+// concatenated columns to part + z * M * N.
+template <int MT, int WAVES, bool MULTI>
+__global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void gemm_q4k_mfma(GEMM_MATS_PARAMS,
                                                         const _Float16* __restrict__ xp,
                                                         const _Float16* __restrict__ xsp,
-                                                        float* __restrict__ y, int M, int N, int K) {
+                                                        float* __restrict__ part, int M, int N, int K) {
   static_assert(MT == 8 && (WAVES == 4 || WAVES == 8), "the waves move the 8 X chunks of a step evenly");
   constexpr int BM = 16 * MT, BN = 32 * WAVES;
   constexpr int XPW = MT / WAVES;  // X chunks each wave moves per step
@@ -188,7 +215,7 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void gemm_q4k_mfma(const uin
   const int nblk = K / 256, S = K / 32, z = blockIdx.z, nz = gridDim.z;
   const int b_begin = (int)((long)nblk * z / nz), b_end = (int)((long)nblk * (z + 1) / nz);
   const int nb = b_end - b_begin, last_step = 8 * nb - 1;
-  y += (size_t)z * M * N;
+  part += (size_t)z * M * N;
   const size_t row_bytes = (size_t)nblk * 144;
   const int m16 = m0 >> 4, M16 = (M + 15) >> 4;
 
@@ -197,7 +224,8 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void gemm_q4k_mfma(const uin
 #pragma unroll
   for (int j = 0; j < NT; j++) {
     const int n = min(n0 + 32 * wave + 16 * j + (lane & 15), N - 1);
-    wrow[j] = w + (size_t)n * row_bytes;
+    const int sg = GEMM_SEGMENT(n);
+    wrow[j] = GEMM_WEIGHTS(sg) + (size_t)(n - GEMM_FIRST(sg)) * row_bytes;
   }
   // this wave moves X chunks XPW wave .. XPW wave + XPW - 1 of every step
   // (row tiles past the padded M are clamped: their rows are never stored);
@@ -348,22 +376,35 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void gemm_q4k_mfma(const uin
     for (int j = 0; j < NT; j++) {
       const int n = n0 + 32 * wave + 16 * j + (lane & 15);
       if (n >= N) continue;
+      const int sg = GEMM_SEGMENT(n);
+      const int ncols = GEMM_FIRST(sg + 1) - GEMM_FIRST(sg);
+      float* dst = nz > 1 ? part + n : GEMM_OUT(sg) + (n - GEMM_FIRST(sg));
+      const int ld = nz > 1 ? N : ncols;
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int m = m0 + mt * 16 + 4 * c + i;
-        if (m < M) y[(size_t)m * N + n] = tot[mt][j][i];
+        if (m < M) dst[(size_t)m * ld] = tot[mt][j][i];
       }
     }
 }
 
-// Sums split-K partials in a fixed order (deterministic results).
-__global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ part, float* __restrict__ y,
-                                                     size_t mn, int split) {
-  const size_t stride = (size_t)gridDim.x * blockDim.x;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < mn; i += stride) {
+// Sums split-K partials (M x N, concatenated columns) in a fixed order
+// (deterministic results) into the matrices' outputs.
+template <bool MULTI>
+__global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ part, GEMM_MATS_PARAMS, int M,
+                                                     int N, int split) {
+  const int mn = M * N;
+  const int stride = gridDim.x * blockDim.x;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < mn; i += stride) {
     float s = part[i];
     for (int z = 1; z < split; z++) s += part[(size_t)z * mn + i];
-    y[i] = s;
+    if (!MULTI) {
+      y0[i] = s;
+      continue;
+    }
+    const int m = i / N, n = i - m * N;
+    const int sg = GEMM_SEGMENT(n);
+    GEMM_OUT(sg)[(size_t)m * (GEMM_FIRST(sg + 1) - GEMM_FIRST(sg)) + (n - GEMM_FIRST(sg))] = s;
   }
 }
 
@@ -377,13 +418,14 @@ namespace {
 
 // Workgroup tiles are 128 (M) x 256 (N): eight waves, each 128 rows x 32
 // columns, one workgroup per CU.  Sharing each X tile among 256 columns halves
-// the X traffic from L2 of 128-column tiles, which bounds this kernel.
+// the X traffic from L2 of 128-column tiles (measured slightly faster than
+// those at two workgroups per CU).
 constexpr int kMT = 8, kWaves = 8, kBN = 32 * kWaves;
 
 // K splits for a GEMM: none while the tiles fill at least half of the
-// workgroup slots (8 / kWaves per CU) (a split costs a partial product per split written
-// and summed again); below that, as many as still fit one round of slots (at
-// most 8, at most one per 256-element block).
+// workgroup slots (8 / kWaves per CU), since a split costs a partial product
+// per split written and summed again; below that, as many as still fit one
+// round of slots (at most 8, at most one per 256-element block).
 int gemm_split(size_t M, size_t N, size_t K) {
   const size_t bm = 16 * (size_t)kMT;
   const size_t tiles = ((N + kBN - 1) / kBN) * ((M + bm - 1) / bm);
@@ -402,17 +444,43 @@ size_t prep_bytes(size_t M, size_t K) {
 
 }  // namespace
 
-size_t gemm_q4k_workspace_bytes(const void* w, const void* x, size_t M, size_t N, size_t K) {
-  if (!gemm_q4k_mfma_ok(w, x)) return M * K * sizeof(float);
+size_t gemm_q4k_workspace_bytes(const void* const* w, const size_t* n, int count, const void* x, size_t M,
+                                size_t K) {
+  size_t N = 0;
+  bool aligned = ((uintptr_t)x & 15) == 0;
+  for (int i = 0; i < count; i++) {
+    N += n[i];
+    aligned = aligned && gemm_q4k_mfma_ok(w[i], x);
+  }
+  if (!aligned) return M * K * sizeof(float);
   const int split = gemm_split(M, N, K);
   return prep_bytes(M, K) + (split > 1 ? (size_t)split * M * N * sizeof(float) : 0);
 }
 
-hipError_t launch_gemm_q4k(const uint8_t* w, const uint16_t* x, float* y, size_t M, size_t N,
-                           size_t K, void* workspace, size_t workspace_bytes, hipStream_t s) {
-  if (M == 0 || N == 0) return hipSuccess;
+hipError_t launch_gemm_q4k(const uint8_t* const* w, const size_t* n, int count, const uint16_t* x,
+                           float* const* y, size_t M, size_t K, void* workspace, size_t workspace_bytes,
+                           hipStream_t s) {
+  if (count < 1 || count > 3) return hipErrorInvalidValue;
   if (K % 256 != 0) return hipErrorInvalidValue;
-  if (gemm_q4k_mfma_ok(w, x)) {
+  size_t N = 0;
+  bool aligned = ((uintptr_t)x & 15) == 0;
+  const uint8_t* wv[3];
+  float* yv[3];
+  int st[3];
+  for (int i = 0; i < 3; i++) {
+    const int j = i < count ? i : count - 1;
+    wv[i] = w[j];
+    yv[i] = y[j];
+    st[i] = (int)N;
+    if (i < count) {
+      N += n[i];
+      aligned = aligned && gemm_q4k_mfma_ok(w[i], x);
+    }
+  }
+  for (int i = count; i < 3; i++) st[i] = (int)N;
+  const GemmMats mats{wv[0], wv[1], wv[2], yv[0], yv[1], yv[2], st[1], st[2]};
+  if (M == 0 || N == 0) return hipSuccess;
+  if (aligned) {
     const int split = gemm_split(M, N, K);
     const size_t need = prep_bytes(M, K) + (split > 1 ? (size_t)split * M * N * sizeof(float) : 0);
     if (workspace_bytes < need) return hipErrorInvalidValue;
@@ -427,26 +495,34 @@ hipError_t launch_gemm_q4k(const uint8_t* w, const uint16_t* x, float* y, size_t
     const int bm = 16 * kMT;
     const dim3 grid((unsigned)((N + kBN - 1) / kBN), (unsigned)((M + bm - 1) / bm), (unsigned)split);
     if (grid.y > 65535) return hipErrorInvalidValue;
-    float* dst = split > 1 ? part : y;
-    hipLaunchKernelGGL((gemm_q4k_mfma<kMT, kWaves>), grid, dim3(64 * kWaves), 0, s, w, xp, xsp, dst, (int)M, (int)N,
-                       (int)K);
+    if (count > 1)
+      hipLaunchKernelGGL((gemm_q4k_mfma<kMT, kWaves, true>), grid, dim3(64 * kWaves), 0, s, GEMM_MATS_ARGS(mats), xp,
+                         xsp, part, (int)M, (int)N, (int)K);
+    else
+      hipLaunchKernelGGL((gemm_q4k_mfma<kMT, kWaves, false>), grid, dim3(64 * kWaves), 0, s, GEMM_MATS_ARGS(mats), xp,
+                         xsp, part, (int)M, (int)N, (int)K);
     e = hipGetLastError();
     if (e != hipSuccess || split == 1) return e;
-    const size_t mn = M * N;
-    const unsigned g = (unsigned)std::min<size_t>((mn + 255) / 256, 8192);
-    hipLaunchKernelGGL(splitk_reduce, dim3(g), dim3(256), 0, s, part, y, mn, split);
+    const unsigned g = (unsigned)std::min<size_t>((M * N + 255) / 256, 8192);
+    if (count > 1)
+      hipLaunchKernelGGL(splitk_reduce<true>, dim3(g), dim3(256), 0, s, part, GEMM_MATS_ARGS(mats), (int)M, (int)N,
+                         split);
+    else
+      hipLaunchKernelGGL(splitk_reduce<false>, dim3(g), dim3(256), 0, s, part, GEMM_MATS_ARGS(mats), (int)M, (int)N,
+                         split);
     return hipGetLastError();
   }
   // Misaligned operands: widen X to f32 (exact) and run the batched matvec,
   // which reads W once per group of up to 8 tokens.
   if (workspace_bytes < M * K * sizeof(float)) return hipErrorInvalidValue;
   float* xf = static_cast<float*>(workspace);
-  size_t n = M * K, g = (n + 255) / 256;
+  size_t nx = M * K, g = (nx + 255) / 256;
   if (g > 65536) g = 65536;
-  hipLaunchKernelGGL(widen_bf16_kernel, dim3((unsigned)g), dim3(256), 0, s, x, xf, n);
+  hipLaunchKernelGGL(widen_bf16_kernel, dim3((unsigned)g), dim3(256), 0, s, x, xf, nx);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  return launch_matvec(kQ4_K, w, xf, y, N, K, M, s);
+  for (int i = 0; i < count && e == hipSuccess; i++)
+    if (n[i]) e = launch_matvec(kQ4_K, w[i], xf, y[i], n[i], K, M, s);
+  return e;
 }
 
 }  // namespace ssdq

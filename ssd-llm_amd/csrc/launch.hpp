@@ -115,10 +115,13 @@ hipError_t launch_flash_attn_f32(const float* q, const float* k, const float* v,
                                  int window_start, int window_end, void* workspace,
                                  hipStream_t stream);
 
-// Prefill GEMM: Y[M,N] f32 = X[M,K] bf16 x W[N,K] Q4_K (reference layout).
-hipError_t launch_gemm_q4k(const uint8_t* w, const uint16_t* x, float* y, size_t M, size_t N,
-                           size_t K, void* workspace, size_t workspace_bytes, hipStream_t stream);
-size_t gemm_q4k_workspace_bytes(const void* w, const void* x, size_t M, size_t N, size_t K);
+// Prefill GEMM: Y_i[M,n_i] f32 = X[M,K] bf16 x W_i[n_i,K] Q4_K (reference
+// layout) for count = 1..3 matrices sharing X, computed as one GEMM.
+hipError_t launch_gemm_q4k(const uint8_t* const* w, const size_t* n, int count, const uint16_t* x,
+                           float* const* y, size_t M, size_t K, void* workspace, size_t workspace_bytes,
+                           hipStream_t stream);
+size_t gemm_q4k_workspace_bytes(const void* const* w, const size_t* n, int count, const void* x, size_t M,
+                                size_t K);
 
 int device_cu_count();
 

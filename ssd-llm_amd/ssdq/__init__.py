@@ -54,6 +54,7 @@ SIGNATURES = {
     "ssdq_matvec_generic_dev": (_i, [_i, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     "ssdq_matvec_quantized": (_i, [_vp, _vp, _sz, _vp, _sz, _sz, _sz, _i, _vp]),
     "ssdq_gemm_q4k_bf16_dev": (_i, [_vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    "ssdq_gemm_q4k_bf16_multi_dev": (_i, [_vp, _vp, _sz, _vp, _vp, _sz, _sz, _vp]),
     "ssdq_kv_slot_bytes": (_sz, [_sz, _sz]),
     "ssdq_kv_swap_out_dev": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp, _vp]),
     "ssdq_kv_swap_in_dev": (_i, [_vp, _vp, _sz, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp]),
@@ -191,6 +192,19 @@ def gemm_q4k_bf16(w, x_bf16, y, M, N, K, stream=None):
     return check("ssdq_gemm_q4k_bf16_dev",
                  lib().ssdq_gemm_q4k_bf16_dev(_ptr(w), _ptr(x_bf16), _ptr(y), M, N, K,
                                               _stream(stream)))
+
+
+def gemm_q4k_bf16_multi(ws, x_bf16, ys, M, ns, K, stream=None):
+    """Y_i = X W_i^T for up to three Q4_K matrices sharing X, as one GEMM."""
+    count = len(ws)
+    if not (len(ys) == len(ns) == count):
+        raise ValueError("ws, ys and ns must have the same length")
+    warr = (_c.c_void_p * max(count, 1))(*[w.data_ptr() for w in ws])
+    yarr = (_c.c_void_p * max(count, 1))(*[y.data_ptr() for y in ys])
+    narr = (_c.c_size_t * max(count, 1))(*ns)
+    return check("ssdq_gemm_q4k_bf16_multi_dev",
+                 lib().ssdq_gemm_q4k_bf16_multi_dev(warr, narr, count, _ptr(x_bf16), yarr, M, K,
+                                                    _stream(stream)))
 
 
 def kv_quantize_rows(x, codes, scales, n_rows, row_len, stream=None):

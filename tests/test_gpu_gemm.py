@@ -72,3 +72,72 @@ def test_gemm_misaligned_x_takes_fallback():
     ref = o.gemm_q4k_bf16(w, xb, M, N, K, threads=8)
     exact = o.gemm_q4k_bf16(w, xb, M, N, K, threads=8, exact=True)
     assert_close_attributed(from_dev(y), ref, exact, "gemm misaligned")
+
+
+def multi(ws, xb, M, ns, K, x_dev=None):
+    ys = [empty_dev(M * n, torch.float32) for n in ns]
+    rc = ssdq.gemm_q4k_bf16_multi([to_dev(w) for w in ws], x_dev if x_dev is not None else to_dev(xb), ys, M,
+                                  list(ns), K)
+    return [from_dev(y) for y in ys], rc
+
+
+@pytest.mark.parametrize("names", [("q", "k", "v"), ("gate", "up")])
+def test_gemm_multi_config4(names):
+    # q/k/v (and gate/up) share X: one GEMM over the concatenated columns
+    M = 512
+    mats = [m for m in LAYER if m[0] in names]
+    K = mats[0][2]
+    ws = [synth.quant_weights(ssdq.Q4_K, N, K, synth.seed(4, LAYER.index(m))) for m in mats for N in [m[1]]]
+    xb = synth.f32_to_bf16_bits(synth.normal_f32((M, K), synth.seed(4, 8)))
+    announce("gemm multi", names, M, K)
+    ys, rc = multi(ws, xb, M, [m[1] for m in mats], K)
+    assert rc == 0
+    sel = np.r_[0:16, 250:266, 496:512]
+    xs = xb.reshape(M, K)[sel]
+    for (name, N, _), w, y in zip(mats, ws, ys):
+        ref = o.gemm_q4k_bf16(w, xs, sel.size, N, K, threads=16)
+        exact = o.gemm_q4k_bf16(w, xs, sel.size, N, K, threads=16, exact=True)
+        assert_close_attributed(y.reshape(M, N)[sel], ref, exact, f"gemm multi {name}")
+
+
+@pytest.mark.parametrize("M,ns,K", [(77, (100, 37, 300), 512), (130, (256, 64), 768), (5, (300,), 256),
+                                    (300, (1, 2, 3), 256)])
+def test_gemm_multi_ragged(M, ns, K):
+    ws = [synth.quant_weights(ssdq.Q4_K, n, K, 900 + i) for i, n in enumerate(ns)]
+    xb = synth.f32_to_bf16_bits(synth.normal_f32((M, K), 901))
+    announce("gemm multi ragged", M, ns, K)
+    ys, rc = multi(ws, xb, M, ns, K)
+    assert rc == 0
+    for n, w, y in zip(ns, ws, ys):
+        ref = o.gemm_q4k_bf16(w, xb, M, n, K, threads=8)
+        exact = o.gemm_q4k_bf16(w, xb, M, n, K, threads=8, exact=True)
+        assert_close_attributed(y, ref, exact, f"gemm multi ragged n={n}")
+        # the single-matrix entry point computes the same columns
+        y1, rc1 = gemm(w, xb, M, n, K)
+        assert rc1 == 0
+        assert_close_attributed(y, y1.astype(np.float32), exact, "multi vs single")
+
+
+def test_gemm_multi_misaligned_x_takes_fallback():
+    M, K, ns = 9, 512, (48, 20)
+    ws = [synth.quant_weights(ssdq.Q4_K, n, K, 70 + n) for n in ns]
+    xb = synth.f32_to_bf16_bits(synth.normal_f32((M, K), 79))
+    buf = torch.empty(M * K + 1, dtype=torch.int16, device="cuda")
+    buf[1:].copy_(torch.from_numpy(xb.view(np.int16).ravel()).cuda())
+    announce("gemm multi misaligned", M, ns, K)
+    ys, rc = multi(ws, xb, M, ns, K, x_dev=buf[1:])
+    assert rc == 0
+    for n, w, y in zip(ns, ws, ys):
+        ref = o.gemm_q4k_bf16(w, xb, M, n, K, threads=8)
+        exact = o.gemm_q4k_bf16(w, xb, M, n, K, threads=8, exact=True)
+        assert_close_attributed(y, ref, exact, "gemm multi misaligned")
+
+
+def test_gemm_multi_rejects_bad_arguments():
+    t = empty_dev(4096, torch.float32)
+    with pytest.raises(ssdq.SsdqError):  # four matrices
+        ssdq.gemm_q4k_bf16_multi([t] * 4, t, [t] * 4, 4, [4] * 4, 256)
+    with pytest.raises(ssdq.SsdqError):  # an empty matrix
+        ssdq.gemm_q4k_bf16_multi([t, t], t, [t, t], 4, [4, 0], 256)
+    with pytest.raises(ssdq.SsdqError):  # K not a multiple of 256
+        ssdq.gemm_q4k_bf16_multi([t], t, [t], 4, [4], 300)

@@ -222,6 +222,8 @@ def extras(torch, ssdq, synth, timer, np):
         ("q8_0_matvec_11008x4096_b4", ssdq.Q8_0, 11008, 4096, 4, 2),
         ("q8_0_matvec_11008x4096_b8", ssdq.Q8_0, 11008, 4096, 8, 2),
         ("q6_k_matvec_4096x14336_b1", ssdq.Q6_K, 4096, 14336, 1, 3),
+        ("q4_k_matvec_4096x14336_b1", ssdq.Q4_K, 4096, 14336, 1, 3),  # FFN down: K-sliced rows
+        ("q5_k_matvec_4096x14336_b1", ssdq.Q5_K, 4096, 14336, 1, 3),
     ]
     # the reference's other matvec_quantized types at the north-star shape
     for k, dt in enumerate(ssdq.MATVEC_EXTRA_TYPES):

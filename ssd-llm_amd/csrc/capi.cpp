@@ -268,7 +268,15 @@ static int matvec_common(int dtype, const void* w, const float* x, float* y, siz
     return fail(SSDQ_ERR_INVALID_ARG, "%s: x and y must be 4-byte aligned", fn);
   hipError_t e = hipSuccess;
   if (ssdq::matvec_ext_type(dtype)) {
-    e = ssdq::launch_matvec_ext(dtype, (const uint8_t*)w, x, y, out_dim, in_dim, batch, s, generic);
+    bool used = false;
+    if (!generic && batch == 1) {  // the batch-1 digit-plane kernel, where the type has one
+      const size_t wsb = ssdq::matvec_b1_ext_workspace_bytes(dtype, w, x, out_dim, in_dim);
+      void* ws = nullptr;
+      if (wsb && (e = workspace_get(wsb, s, &ws)) != hipSuccess) return hip_fail(e, "ssdq_matvec_dev: workspace");
+      e = ssdq::launch_matvec_b1_ext(dtype, (const uint8_t*)w, x, y, out_dim, in_dim, s, ws, wsb, &used);
+      if (e != hipSuccess) return hip_fail(e, fn);
+    }
+    if (!used) e = ssdq::launch_matvec_ext(dtype, (const uint8_t*)w, x, y, out_dim, in_dim, batch, s, generic);
   } else if (generic) {
     e = ssdq::launch_matvec_generic(dtype, (const uint8_t*)w, x, y, out_dim, in_dim, batch, s);
   } else {

@@ -43,6 +43,7 @@ namespace {
 //   Q4_K: two sub-blocks of one super-block (64 elements, one 16-byte header)
 //   Q4_0 / Q8_0: two consecutive 18- / 34-byte blocks (64 elements, dword aligned)
 //   Q6_K: a 32-element quarter of a 210-byte block
+//   Q5_K (batch-1 kernel only): two sub-blocks (header, 8 high-bit bytes, 32 code bytes)
 // E elements, NSUM x-sum groups of SUMG elements, NW dwords of raw data.
 template <int F> struct FastUnit;
 template <> struct FastUnit<kQ4_K> {
@@ -56,6 +57,10 @@ template <> struct FastUnit<kQ4_0> {
 template <> struct FastUnit<kQ8_0> {
   static constexpr int E = 64, NSUM = 2, SUMG = 32, NW = 17;
   static constexpr bool prescale = false;
+};
+template <> struct FastUnit<kQ5_K> {
+  static constexpr int E = 64, NSUM = 2, SUMG = 32, NW = 14;
+  static constexpr bool prescale = true;
 };
 template <> struct FastUnit<kQ6_K> {
   static constexpr int E = 32, NSUM = 2, SUMG = 16, NW = 10;
@@ -89,6 +94,15 @@ __device__ __forceinline__ void load_unit(const uint8_t* __restrict__ row, int u
     ld4(blk, raw);                          // d, dmin, scales[12]
     ld4(blk + 16 + 32 * (u & 3), raw + 4);  // qs of sub-block 2*(u&3)
     ld4(blk + 32 + 32 * (u & 3), raw + 8);  // qs of sub-block 2*(u&3)+1
+  } else if constexpr (F == kQ5_K) {
+    // block (compute.rs:855-860): d, dmin, scales[12] | qh[32] | ql[128]
+    const uint8_t* blk = row + (size_t)(u >> 2) * 176;
+    ld4(blk, raw);                          // d, dmin, scales[12]
+    ld4(blk + 48 + 32 * (u & 3), raw + 4);  // low nibbles of sub-block 2*(u&3)
+    ld4(blk + 64 + 32 * (u & 3), raw + 8);  // low nibbles of sub-block 2*(u&3)+1
+    const uint2 h = *reinterpret_cast<const uint2*>(blk + 16 + 8 * (u & 3));  // high bits of the 64 elements
+    raw[12] = h.x;
+    raw[13] = h.y;
   } else if constexpr (F == kQ4_0) {
     const uint8_t* p = row + (size_t)u * 36;  // two 18-byte blocks, dword aligned
     ld4(p, raw);
@@ -271,6 +285,7 @@ __device__ __forceinline__ void stage_x(const float* __restrict__ x, int in_dim,
 template <int F> struct Dig;
 template <> struct Dig<kQ4_K> { static constexpr int NG = 2, GW = 26, US = 52; static constexpr bool contig = false; };
 template <> struct Dig<kQ4_0> { static constexpr int NG = 2, GW = 26, US = 52; static constexpr bool contig = false; };
+template <> struct Dig<kQ5_K> { static constexpr int NG = 2, GW = 26, US = 52; static constexpr bool contig = false; };
 template <> struct Dig<kQ8_0> { static constexpr int NG = 2, GW = 26, US = 52; static constexpr bool contig = true; };
 template <> struct Dig<kQ6_K> { static constexpr int NG = 1, GW = 28, US = 28; static constexpr bool contig = false; };
 
@@ -389,12 +404,24 @@ __device__ __forceinline__ float digits_value(int i0, int i1, int i2) {
 
 // Applies one unit (raw weight dwords) to x given as digit planes pl[] (the
 // unit's US dwords).
+// The fifth bits of a Q5_K weight dword's 8 elements (bits 0-7 of one qh byte,
+// element 2i at bit 2i) as bit 4 of four bytes, for the even (elements 0, 2,
+// 4, 6) and the odd elements.  A 24-bit multiply spreads the four bits: the
+// copies of the byte land 6 bits apart, so each target bit 8j+4 receives only
+// bit 2j (2j+1) and the carries where copies overlap stay below it.
+__device__ __forceinline__ uint32_t q5_high_even(uint32_t hb) {
+  return __umul24(hb & 0x55u, 0x00410410u) & 0x10101010u;
+}
+__device__ __forceinline__ uint32_t q5_high_odd(uint32_t hb) {
+  return __umul24(hb & 0xAAu, 0x00208208u) & 0x10101010u;
+}
+
 template <int F, class PL>
 __device__ __forceinline__ void accumulate_dig(const uint32_t* raw, int u, PL pl, float& acc) {
   using D = Dig<F>;
-  if constexpr (F == kQ4_K || F == kQ4_0) {
+  if constexpr (F == kQ4_K || F == kQ4_0 || F == kQ5_K) {
     float sc[2], off[2];
-    if constexpr (F == kQ4_K) {
+    if constexpr (F == kQ4_K || F == kQ5_K) {
       const float d = f16_to_f32(raw[0] & 0xFFFFu), dmin = f16_to_f32(raw[0] >> 16);
       const int sb = 2 * (u & 3);
 #pragma unroll
@@ -416,9 +443,14 @@ __device__ __forceinline__ void accumulate_dig(const uint32_t* raw, int u, PL pl
 #pragma unroll
       for (int k = 0; k < 4; k++) {
         uint32_t wd;
-        if constexpr (F == kQ4_K) wd = raw[4 + 4 * h + k];
+        if constexpr (F == kQ4_K || F == kQ5_K) wd = raw[4 + 4 * h + k];
         else wd = h == 0 ? __builtin_amdgcn_alignbit(raw[k + 1], raw[k], 16) : raw[5 + k];
-        const uint32_t lo = wd & 0x0F0F0F0Fu, hi = (wd >> 4) & 0x0F0F0F0Fu;
+        uint32_t lo = wd & 0x0F0F0F0Fu, hi = (wd >> 4) & 0x0F0F0F0Fu;
+        if constexpr (F == kQ5_K) {  // codes 0..31 (compute.rs:882-892)
+          const uint32_t hb = raw[12 + h] >> (8 * k);
+          lo |= q5_high_even(hb);
+          hi |= q5_high_odd(hb);
+        }
         const int b = h * D::GW + 6 * k;
         i0 = dot4(lo, pl(b + 0), i0);
         i1 = dot4(lo, pl(b + 1), i1);
@@ -493,7 +525,7 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 // Vector memory instructions one load_unit issues.
-template <int F> constexpr int loads_per_unit() { return (F == kQ4_K || F == kQ4_0) ? 3 : 5; }
+template <int F> constexpr int loads_per_unit() { return (F == kQ4_K || F == kQ4_0) ? 3 : F == kQ5_K ? 4 : 5; }
 
 // rows whose weight loads are in flight at once in a wave (measured at
 // 14336 x 4096 Q4_K: depth 1 9.8 us, 2 8.5 us, 3 9.2 us, 5 11.2 us)
@@ -1123,7 +1155,7 @@ template <int F>
 bool fast_aligned(const uint8_t* w, const float* x, int in_dim, int bpr) {
   const uintptr_t a = (uintptr_t)w;
   if ((((uintptr_t)x) & 15) || (in_dim & 3)) return false;  // float4 staging of x
-  if constexpr (F == kQ4_K) return (a & 15u) == 0;
+  if constexpr (F == kQ4_K || F == kQ5_K) return (a & 15u) == 0;
   else return (a & 3u) == 0 && (bpr % 2) == 0;  // Q4_0 / Q8_0 pairs, Q6_K dword rows
 }
 
@@ -1175,7 +1207,21 @@ hipError_t b1_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, 
   float* dst = p.slices > 1 ? ws : y;
   *used = true;
   hipError_t e;
-  if (p.upl == 1)
+  // K-sliced rows: 5 or 8 rows per wave, whichever needs fewer rounds of
+  // workgroups (one per CU, 12 row streams each, as run_b1_sit sizes the grid)
+  // times rows.  4096 x 14336 Q4_K: 4 slices x 43 workgroups in one round,
+  // 13.9 us, against 4 x 69 in two rounds with 5 rows, 18.2 us; Q6_K's 7 slices
+  // need two rounds either way and keep 5 rows (15.8 us against 19.9).
+  auto sliced_cost = [&](int rmax) {
+    const long cu = device_cu_count(), streams = (out_dim + rmax - 1) / rmax;
+    long n_wg = std::max<long>((cu + p.slices - 1) / p.slices, (streams + 11) / 12);
+    n_wg = std::max<long>(1, std::min<long>(n_wg, (out_dim + 11) / 12));
+    return (n_wg * p.slices + cu - 1) / cu * rmax;
+  };
+  if (p.upl == 1 && p.slices > 1 && sliced_cost(8) < sliced_cost(5))
+    e = p.full ? run_b1<F, 1, 8, true>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s)
+               : run_b1<F, 1, 8, false>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s);
+  else if (p.upl == 1)
     e = p.full ? run_b1<F, 1, 5, true>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s)
                : run_b1<F, 1, 5, false>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s);
   else
@@ -1444,6 +1490,24 @@ hipError_t fast_dispatch(const uint8_t* w, const float* x, float* y, int out_dim
 }
 
 }  // namespace
+
+size_t matvec_b1_ext_workspace_bytes(int dtype, const void* w, const float* x, size_t out_dim, size_t in_dim) {
+  if (dtype != kQ5_K || out_dim == 0) return 0;
+  const int id = (int)in_dim;
+  if (!fast_aligned<kQ5_K>((const uint8_t*)w, x, id, id / 256)) return 0;
+  return b1_workspace_floats<kQ5_K>((int)out_dim, id / 256) * sizeof(float);
+}
+
+hipError_t launch_matvec_b1_ext(int dtype, const uint8_t* w, const float* x, float* y, size_t out_dim,
+                                size_t in_dim, hipStream_t s, void* workspace, size_t workspace_bytes,
+                                bool* used) {
+  *used = false;
+  if (dtype != kQ5_K || out_dim == 0) return hipSuccess;
+  const int id = (int)in_dim, bpr = id / 256;
+  if (bpr == 0 || !fast_aligned<kQ5_K>(w, x, id, bpr)) return hipSuccess;
+  return b1_dispatch<kQ5_K>(w, x, y, (int)out_dim, bpr, s, static_cast<float*>(workspace),
+                            workspace_bytes / sizeof(float), used);
+}
 
 hipError_t launch_matvec_fused(int dtype, const MatvecFuse& f, int total_rows, const float* x,
                                size_t in_dim, hipStream_t s, bool* used) {

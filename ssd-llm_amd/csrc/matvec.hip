@@ -1081,8 +1081,9 @@ hipError_t run_b1_sit(const uint8_t* w, const float* x, float* y, int out_dim, i
   // 4096: 11.0 us vs 11.5 us); the other formats with contiguous runs.
   const bool interleave = F == kQ8_0;
   const long streams_needed = (out_dim + RMAX - 1) / RMAX;
-  // about one workgroup per CU over all slices
-  long n_wg = std::max<long>((device_cu_count() + slices - 1) / slices, (streams_needed + rs - 1) / rs);
+  // about one workgroup per CU over all slices (rounded down, so that the
+  // slices together do not spill a few workgroups into a second round)
+  long n_wg = std::max<long>(device_cu_count() / slices, (streams_needed + rs - 1) / rs);
   n_wg = std::max<long>(1, std::min<long>(n_wg, (out_dim + rs - 1) / rs));
   hipLaunchKernelGGL(kern, dim3((unsigned)n_wg, (unsigned)slices), dim3(threads), lds, s, w, x, y,
                      out_dim, row_bpr, slice_bpr, ks, interleave, NoFuse{});
@@ -1209,12 +1210,12 @@ hipError_t b1_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, 
   hipError_t e;
   // K-sliced rows: 5 or 8 rows per wave, whichever needs fewer rounds of
   // workgroups (one per CU, 12 row streams each, as run_b1_sit sizes the grid)
-  // times rows.  4096 x 14336 Q4_K: 4 slices x 43 workgroups in one round,
-  // 13.9 us, against 4 x 69 in two rounds with 5 rows, 18.2 us; Q6_K's 7 slices
-  // need two rounds either way and keep 5 rows (15.8 us against 19.9).
+  // times rows.  4096 x 14336 Q4_K: 4 slices x 64 workgroups in one round,
+  // 14.0 us, against 4 x 69 in two rounds with 5 rows, 18.2 us; Q6_K's 7 slices
+  // need two rounds either way and keep 5 rows (16.0 us against 19.9).
   auto sliced_cost = [&](int rmax) {
     const long cu = device_cu_count(), streams = (out_dim + rmax - 1) / rmax;
-    long n_wg = std::max<long>((cu + p.slices - 1) / p.slices, (streams + 11) / 12);
+    long n_wg = std::max<long>(cu / p.slices, (streams + 11) / 12);
     n_wg = std::max<long>(1, std::min<long>(n_wg, (out_dim + 11) / 12));
     return (n_wg * p.slices + cu - 1) / cu * rmax;
   };
@@ -1387,7 +1388,7 @@ hipError_t run_bn(const uint8_t* w, const float* x, float* dst, int out_dim, int
   const int nchunk = NB * (slice_bpr * Geom<F>::bs / 8);
   const int sit = (nchunk + threads - 1) / threads;
   const long streams_needed = (out_dim + RMAX - 1) / RMAX;
-  long n_wg = std::max<long>((device_cu_count() + slices - 1) / slices, (streams_needed + rs - 1) / rs);
+  long n_wg = std::max<long>(device_cu_count() / slices, (streams_needed + rs - 1) / rs);  // as in run_b1_sit
   n_wg = std::max<long>(1, std::min<long>(n_wg, (out_dim + rs - 1) / rs));
   const bool interleave = F == kQ8_0;
   auto launch = [&](auto kern) {

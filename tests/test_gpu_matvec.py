@@ -201,3 +201,24 @@ def test_extreme_and_nonfinite_activations(dtype, batch):
     # row 3: relative agreement (the absolute 1e-4 term says nothing at 1e-30)
     scale = np.abs(exact[3]).max()
     assert np.all(np.abs(y[3] - exact[3]) <= 1e-3 * scale)
+
+
+LONG_ROWS = [  # batch-1 rows of 129-256 units (K slices summed in slice order)
+    (Q4_K, 77, 256 * 36), (Q4_K, 1000, 256 * 64), (Q4_K, 4096, 14336),
+    (Q4_0, 300, 64 * 144), (Q4_0, 64, 64 * 256), (Q8_0, 129, 64 * 192), (Q8_0, 4096, 14336),
+]
+
+
+@pytest.mark.parametrize("dtype,out_dim,in_dim", LONG_ROWS)
+def test_batch1_long_rows(dtype, out_dim, in_dim):
+    w = synth.quant_weights(dtype, out_dim, in_dim, 80 + out_dim)
+    x = synth.normal_f32(in_dim, 81 + in_dim)
+    announce("matvec long rows", ssdq.TYPE_NAMES[dtype], out_dim, in_dim)
+    y, rc = run(dtype, w, x, out_dim, in_dim)
+    assert rc == 0
+    sel = np.arange(out_dim) if out_dim <= 1000 else np.r_[0:500, out_dim - 500:out_dim]
+    rb = w.size // out_dim
+    ref, exact = reference(dtype, w.reshape(out_dim, rb)[sel].ravel(), x, sel.size, in_dim)
+    assert_close_attributed(y[sel], ref, exact, "long rows")
+    y2, _ = run(dtype, w, x, out_dim, in_dim)
+    assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))  # fixed summation order

@@ -44,6 +44,7 @@ namespace {
 //   Q4_0 / Q8_0: two consecutive 18- / 34-byte blocks (64 elements, dword aligned)
 //   Q6_K: a 32-element quarter of a 210-byte block
 //   Q5_K (batch-1 kernel only): two sub-blocks (header, 8 high-bit bytes, 32 code bytes)
+//   Q2_K (batch-1 kernel only): four 16-element sub-blocks (d|dmin, 4 scale bytes, 16 code bytes)
 // E elements, NSUM x-sum groups of SUMG elements, NW dwords of raw data.
 template <int F> struct FastUnit;
 template <> struct FastUnit<kQ4_K> {
@@ -61,6 +62,10 @@ template <> struct FastUnit<kQ8_0> {
 template <> struct FastUnit<kQ5_K> {
   static constexpr int E = 64, NSUM = 2, SUMG = 32, NW = 14;
   static constexpr bool prescale = true;
+};
+template <> struct FastUnit<kQ2_K> {
+  static constexpr int E = 64, NSUM = 4, SUMG = 16, NW = 6;
+  static constexpr bool prescale = false;
 };
 template <> struct FastUnit<kQ6_K> {
   static constexpr int E = 32, NSUM = 2, SUMG = 16, NW = 10;
@@ -103,6 +108,12 @@ __device__ __forceinline__ void load_unit(const uint8_t* __restrict__ row, int u
     const uint2 h = *reinterpret_cast<const uint2*>(blk + 16 + 8 * (u & 3));  // high bits of the 64 elements
     raw[12] = h.x;
     raw[13] = h.y;
+  } else if constexpr (F == kQ2_K) {
+    // block (compute.rs:940-944): d, dmin | scales[16] | qs[64]; dword aligned
+    const uint8_t* blk = row + (size_t)(u >> 2) * 84;
+    raw[0] = ld1(blk);                       // d | dmin
+    raw[1] = ld1(blk + 4 + 4 * (u & 3));     // scale|min bytes of sub-blocks 4*(u&3) .. +3
+    ld4(blk + 20 + 16 * (u & 3), raw + 2);  // one code dword per 16-element sub-block
   } else if constexpr (F == kQ4_0) {
     const uint8_t* p = row + (size_t)u * 36;  // two 18-byte blocks, dword aligned
     ld4(p, raw);
@@ -288,6 +299,10 @@ template <> struct Dig<kQ4_0> { static constexpr int NG = 2, GW = 26, US = 52; s
 template <> struct Dig<kQ5_K> { static constexpr int NG = 2, GW = 26, US = 52; static constexpr bool contig = false; };
 template <> struct Dig<kQ8_0> { static constexpr int NG = 2, GW = 26, US = 52; static constexpr bool contig = true; };
 template <> struct Dig<kQ6_K> { static constexpr int NG = 1, GW = 28, US = 28; static constexpr bool contig = false; };
+// Q2_K: a group record holds two 16-element sub-blocks, each as 4 phase planes
+// (elements p, p+4, p+8, p+12: the bytes a code dword yields for shift 2p) x 3
+// digits, then the scale and the two sub-block sums as for Q6_K.
+template <> struct Dig<kQ2_K> { static constexpr int NG = 2, GW = 28, US = 56; static constexpr bool contig = false; };
 
 __device__ __forceinline__ uint32_t plane_bytes(uint32_t a, uint32_t b, uint32_t c, uint32_t e, int d) {
   // byte d of a, b, c, e -> bytes 0, 1, 2, 3
@@ -373,6 +388,17 @@ __device__ __forceinline__ void stage_store(const XChunks<SIT>& st, int keff, ui
       const int g = c >> 2;
       uint32_t* rec = lds + (size_t)r * lds_stride + (size_t)(g / D::NG) * D::US + (g % D::NG) * D::GW;
       uint32_t* pl = rec + 6 * k;
+      if constexpr (F == kQ2_K) {
+        // chunk k is half k & 1 of sub-block k >> 1: bytes 2 (k & 1), +1 of its
+        // phase planes (elements p and p + 4 of this chunk)
+        uint16_t* pb = reinterpret_cast<uint16_t*>(rec + 12 * (k >> 1)) + (k & 1);
+#pragma unroll
+        for (int ph = 0; ph < 4; ph++)
+#pragma unroll
+          for (int d = 0; d < 3; d++)
+            pb[2 * (3 * ph + d)] =
+                (uint16_t)__builtin_amdgcn_perm(u[4 + ph], u[ph], (uint32_t)d | ((uint32_t)(4 + d) << 8) | 0x0C0C0000u);
+      } else
 #pragma unroll
       for (int d = 0; d < 3; d++) {
         if (D::contig) {
@@ -480,6 +506,31 @@ __device__ __forceinline__ void accumulate_dig(const uint32_t* raw, int u, PL pl
       const float xscale = __uint_as_float(pl(h * D::GW + 24));
       acc = fmaf(d * xscale, digits_value(i0, i1, i2), acc);
     }
+  } else if constexpr (F == kQ2_K) {
+    // 16 sub-blocks of 16 elements; scale / min = low / high nibble of the
+    // sub-block's byte (compute.rs:948-960): value d*s*q - dmin*m
+    const float d = f16_to_f32(raw[0] & 0xFFFFu), dmin = f16_to_f32(raw[0] >> 16);
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const float xscale = __uint_as_float(pl(h * D::GW + 24));
+#pragma unroll
+      for (int sb = 0; sb < 2; sb++) {
+        const uint32_t wd = raw[2 + 2 * h + sb];
+        const uint32_t scb = (raw[1] >> (8 * (2 * h + sb))) & 0xFFu;
+        int i0 = 0, i1 = 0, i2 = 0;
+#pragma unroll
+        for (int ph = 0; ph < 4; ph++) {
+          const uint32_t q = (wd >> (2 * ph)) & 0x03030303u;
+          const int b = h * D::GW + 12 * sb + 3 * ph;
+          i0 = dot4(q, pl(b + 0), i0);
+          i1 = dot4(q, pl(b + 1), i1);
+          i2 = dot4(q, pl(b + 2), i2);
+        }
+        const float S = d * (float)(scb & 15u), Mn = dmin * (float)(scb >> 4);
+        const float xsum = __uint_as_float(pl(h * D::GW + 25 + sb));
+        acc = fmaf(S * xscale, digits_value(i0, i1, i2), fmaf(-Mn, xsum, acc));
+      }
+    }
   } else {  // kQ6_K quarter: 6-bit codes + 32 as bytes, two 16-element scale groups
     const uint32_t sh = raw[9];
     uint32_t ql[4], qh[2];
@@ -525,7 +576,9 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 // Vector memory instructions one load_unit issues.
-template <int F> constexpr int loads_per_unit() { return (F == kQ4_K || F == kQ4_0) ? 3 : F == kQ5_K ? 4 : 5; }
+template <int F> constexpr int loads_per_unit() {
+  return (F == kQ4_K || F == kQ4_0 || F == kQ2_K) ? 3 : F == kQ5_K ? 4 : 5;
+}
 
 // rows whose weight loads are in flight at once in a wave (measured at
 // 14336 x 4096 Q4_K: depth 1 9.8 us, 2 8.5 us, 3 9.2 us, 5 11.2 us)
@@ -1158,6 +1211,7 @@ bool fast_aligned(const uint8_t* w, const float* x, int in_dim, int bpr) {
   const uintptr_t a = (uintptr_t)w;
   if ((((uintptr_t)x) & 15) || (in_dim & 3)) return false;  // float4 staging of x
   if constexpr (F == kQ4_K || F == kQ5_K) return (a & 15u) == 0;
+  else if constexpr (F == kQ2_K) return (a & 3u) == 0;
   else return (a & 3u) == 0 && (bpr % 2) == 0;  // Q4_0 / Q8_0 pairs, Q6_K dword rows
 }
 
@@ -1497,21 +1551,35 @@ hipError_t fast_dispatch(const uint8_t* w, const float* x, float* y, int out_dim
 }  // namespace
 
 size_t matvec_b1_ext_workspace_bytes(int dtype, const void* w, const float* x, size_t out_dim, size_t in_dim) {
-  if (dtype != kQ5_K || out_dim == 0) return 0;
+  if (out_dim == 0) return 0;
   const int id = (int)in_dim;
-  if (!fast_aligned<kQ5_K>((const uint8_t*)w, x, id, id / 256)) return 0;
-  return b1_workspace_floats<kQ5_K>((int)out_dim, id / 256) * sizeof(float);
+  const uint8_t* wb = (const uint8_t*)w;
+  switch (dtype) {
+    case kQ5_K:
+      return fast_aligned<kQ5_K>(wb, x, id, id / 256) ? b1_workspace_floats<kQ5_K>((int)out_dim, id / 256) * 4 : 0;
+    case kQ2_K:
+      return fast_aligned<kQ2_K>(wb, x, id, id / 256) ? b1_workspace_floats<kQ2_K>((int)out_dim, id / 256) * 4 : 0;
+    default: return 0;
+  }
 }
 
 hipError_t launch_matvec_b1_ext(int dtype, const uint8_t* w, const float* x, float* y, size_t out_dim,
                                 size_t in_dim, hipStream_t s, void* workspace, size_t workspace_bytes,
                                 bool* used) {
   *used = false;
-  if (dtype != kQ5_K || out_dim == 0) return hipSuccess;
+  if (out_dim == 0) return hipSuccess;
   const int id = (int)in_dim, bpr = id / 256;
-  if (bpr == 0 || !fast_aligned<kQ5_K>(w, x, id, bpr)) return hipSuccess;
-  return b1_dispatch<kQ5_K>(w, x, y, (int)out_dim, bpr, s, static_cast<float*>(workspace),
-                            workspace_bytes / sizeof(float), used);
+  float* ws = static_cast<float*>(workspace);
+  const size_t wf = workspace_bytes / sizeof(float);
+  switch (dtype) {
+    case kQ5_K:
+      if (bpr == 0 || !fast_aligned<kQ5_K>(w, x, id, bpr)) return hipSuccess;
+      return b1_dispatch<kQ5_K>(w, x, y, (int)out_dim, bpr, s, ws, wf, used);
+    case kQ2_K:
+      if (bpr == 0 || !fast_aligned<kQ2_K>(w, x, id, bpr)) return hipSuccess;
+      return b1_dispatch<kQ2_K>(w, x, y, (int)out_dim, bpr, s, ws, wf, used);
+    default: return hipSuccess;
+  }
 }
 
 hipError_t launch_matvec_fused(int dtype, const MatvecFuse& f, int total_rows, const float* x,

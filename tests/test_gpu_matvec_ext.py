@@ -157,20 +157,23 @@ def test_host_twin_new_types():
         assert np.all(y == 0)
 
 
+@pytest.mark.parametrize("dtype", [ssdq.Q5_K, ssdq.Q2_K], ids=["Q5_K", "Q2_K"])
 @pytest.mark.parametrize("out_dim,in_dim", [(14336, 4096), (4096, 14336), (77, 768), (130, 256 * 5)])
-def test_q5k_batch1_digit_kernel(out_dim, in_dim):
-    # batch 1 with 16-byte aligned weights runs the digit-plane kernel (K-sliced
-    # past 128 units per row); the byte-addressed float kernel is the cross-check
-    w = synth.quant_weights(ssdq.Q5_K, out_dim, in_dim, 7000 + in_dim)
+def test_batch1_digit_kernel(dtype, out_dim, in_dim):
+    # batch 1 with aligned weights (Q5_K: 16 bytes, Q2_K: 4) runs the digit-plane
+    # kernel (K-sliced past 128 units per row); the byte-addressed float kernel
+    # is the cross-check
+    w = synth.quant_weights(dtype, out_dim, in_dim, 7000 + in_dim + dtype)
     x = synth.normal_f32(in_dim, 7001)
-    announce("matvec Q5_K digit", out_dim, in_dim)
-    y, rc = run(ssdq.Q5_K, to_dev(w), x, out_dim, in_dim)
+    name = ssdq.TYPE_NAMES[dtype]
+    announce("matvec digit", name, out_dim, in_dim)
+    y, rc = run(dtype, to_dev(w), x, out_dim, in_dim)
     assert rc == 0
     sel = np.arange(out_dim) if out_dim <= 4096 else np.r_[0:2048, out_dim - 2048:out_dim]
-    rows = synth.BLOCK[ssdq.Q5_K][1] * (in_dim // 256)
+    rows = synth.BLOCK[dtype][1] * (in_dim // 256)
     wsel = w.reshape(out_dim, rows)[sel].ravel()
-    ref, exact = reference(ssdq.Q5_K, wsel, x, sel.size, in_dim)
-    assert_close_attributed(y[sel], ref, exact, f"Q5_K digit {out_dim}x{in_dim}", max_ill_frac=ILL)
-    yg, rcg = run(ssdq.Q5_K, to_dev(w), x, out_dim, in_dim, generic=True)
+    ref, exact = reference(dtype, wsel, x, sel.size, in_dim)
+    assert_close_attributed(y[sel], ref, exact, f"{name} digit {out_dim}x{in_dim}", max_ill_frac=ILL)
+    yg, rcg = run(dtype, to_dev(w), x, out_dim, in_dim, generic=True)
     assert rcg == 0
     assert_close_attributed(y[sel], yg[sel], exact, "digit vs float kernel", max_ill_frac=ILL)

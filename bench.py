@@ -30,7 +30,8 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=400)
-    ap.add_argument("--warmup", type=int, default=40)
+    # ~9 ms of untimed replays: the first millisecond after a pause runs up to 5% slow
+    ap.add_argument("--warmup", type=int, default=1000)
     ap.add_argument("--no-extras", action="store_true", help="only the headline workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--profile-pass", action="store_true",
@@ -230,7 +231,7 @@ def extras(torch, ssdq, synth, timer, np):
         cases.append((f"{ssdq.TYPE_NAMES[dt].lower()}_matvec_14336x4096_b1", dt, 14336, 4096, 1, 6 + k))
     for name, dt, od, idim, b, cfg in cases:
         step, nbytes, _ = matvec_case(torch, ssdq, synth, dt, od, idim, b, cfg)
-        t, _, n = timer.run(step, 200, 20)
+        t, _, n = timer.run(step, 200, 500)
         gbs = nbytes / (t / n) / 1e9
         out[name] = {"GB/s": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
                      "us": round(t / n * 1e6, 3)}
@@ -248,9 +249,9 @@ def extras(torch, ssdq, synth, timer, np):
         n = copies_for(nbytes)  # weights rotated over copies larger than 2x the last-level cache
         sets = [base] + [[(dt, w.clone(), r, y) for dt, w, r, y in base] for _ in range(n - 1)]
         x = torch.randn(n_embd, device="cuda")
-        tf, _, nf = timer.run(lambda i: fused(sets[i % n], x), 200, 20)
+        tf, _, nf = timer.run(lambda i: fused(sets[i % n], x), 200, 500)
         ts, _, ns = timer.run(lambda i: [ssdq.matvec(dt, w, x, y, r, n_embd) for dt, w, r, y in sets[i % n]],
-                              200, 20)
+                              200, 500)
         del sets, base
         out[name] = {"us": round(tf / nf * 1e6, 3), "GB/s": round(nbytes / (tf / nf) / 1e9, 1),
                      "pct_hbm_peak": round(100 * nbytes / (tf / nf) / 1e9 / HBM_PEAK_GBS, 2),

@@ -1370,9 +1370,18 @@ hipError_t fused_dispatch(const MatvecFuse& f, int vrows, const float* x, int in
   for (const uint8_t* w : {f.w0, f.w1, f.w2})
     if (w && !fast_aligned<F>(w, x, in_dim, bpr)) return hipSuccess;
   if (U == 64) {
-    hipError_t e = run_fused<F, 1, 6, 2>(f, x, vrows, bpr, s, used);
+    // the fewest rows per wave that still fit one round of workgroups: rows
+    // past a wave's share are still loaded (clamped), so spare capacity costs
+    // bandwidth (SwiGLU 2 x 14336: 10 rows 9.3 in use; QKV 6144: 2 rows)
+    hipError_t e = run_fused<F, 1, 2, 2>(f, x, vrows, bpr, s, used);
     if (e != hipSuccess || *used) return e;
-    return run_fused<F, 1, 12, 2>(f, x, vrows, bpr, s, used);  // up to 12 rows per wave
+    e = run_fused<F, 1, 4, 2>(f, x, vrows, bpr, s, used);
+    if (e != hipSuccess || *used) return e;
+    e = run_fused<F, 1, 6, 2>(f, x, vrows, bpr, s, used);
+    if (e != hipSuccess || *used) return e;
+    e = run_fused<F, 1, 10, 2>(f, x, vrows, bpr, s, used);
+    if (e != hipSuccess || *used) return e;
+    return run_fused<F, 1, 12, 2>(f, x, vrows, bpr, s, used);
   }
   // two units per lane: Q4_K / Q8_0 (12 / 17 raw dwords per unit) would spill
   // in the fused form, so those rows take the separate launches

@@ -1280,6 +1280,11 @@ hipError_t b1_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, 
   if (p.upl == 1 && p.slices > 1 && sliced_cost(8) < sliced_cost(5))
     e = p.full ? run_b1<F, 1, 8, true>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s)
                : run_b1<F, 1, 8, false>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s);
+  else if (p.upl == 1 && p.slices == 1 && out_dim <= 2 * 12 * device_cu_count())
+    // at most 2 rows per row stream: rows past a wave's share would still be
+    // loaded (clamped), so small matrices take 2 rows per wave
+    e = p.full ? run_b1<F, 1, 2, true>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s)
+               : run_b1<F, 1, 2, false>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s);
   else if (p.upl == 1)
     e = p.full ? run_b1<F, 1, 5, true>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s)
                : run_b1<F, 1, 5, false>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s);

@@ -45,6 +45,7 @@ namespace {
 //   Q6_K: a 32-element quarter of a 210-byte block
 //   Q5_K (batch-1 kernel only): two sub-blocks (header, 8 high-bit bytes, 32 code bytes)
 //   Q2_K (batch-1 kernel only): four 16-element sub-blocks (d|dmin, 4 scale bytes, 16 code bytes)
+//   Q3_K (batch-1 kernel only): four 16-element sub-blocks (8 high-bit bytes, 16 code bytes, scales, d)
 // E elements, NSUM x-sum groups of SUMG elements, NW dwords of raw data.
 template <int F> struct FastUnit;
 template <> struct FastUnit<kQ4_K> {
@@ -65,6 +66,10 @@ template <> struct FastUnit<kQ5_K> {
 };
 template <> struct FastUnit<kQ2_K> {
   static constexpr int E = 64, NSUM = 4, SUMG = 16, NW = 6;
+  static constexpr bool prescale = false;
+};
+template <> struct FastUnit<kQ3_K> {
+  static constexpr int E = 64, NSUM = 4, SUMG = 16, NW = 12;
   static constexpr bool prescale = false;
 };
 template <> struct FastUnit<kQ6_K> {
@@ -114,6 +119,19 @@ __device__ __forceinline__ void load_unit(const uint8_t* __restrict__ row, int u
     raw[0] = ld1(blk);                       // d | dmin
     raw[1] = ld1(blk + 4 + 4 * (u & 3));     // scale|min bytes of sub-blocks 4*(u&3) .. +3
     ld4(blk + 20 + 16 * (u & 3), raw + 2);  // one code dword per 16-element sub-block
+  } else if constexpr (F == kQ3_K) {
+    // block (compute.rs:807-810): hmask[32] | qs[64] | scales[12] | d; 110 bytes,
+    // 2-byte aligned: dwords are read from 0 or 2 bytes below and realigned
+    const uint8_t* blk = row + (size_t)(u >> 2) * 110;
+    const int j = u & 3;
+    const uint32_t mis = (uint32_t)(uintptr_t)blk & 2u;  // 0 or 2
+    ld3(blk + 8 * j - mis, raw);           // hmask[8j .. 8j+8) (+ slack)
+    ld4(blk + 32 + 16 * j - mis, raw + 3);  // qs[16j .. 16j+16) (+ slack)
+    raw[7] = ld1(blk + 48 + 16 * j - mis);
+    raw[8] = ldh(blk + 96 + 2 * j) | (ldh(blk + 104 + (j & 2)) << 16);  // low-nibble scale bytes | high-bit bytes
+    raw[9] = ldh(blk + 108);                                              // d
+    raw[10] = mis * 8u;                                                   // realignment shift
+    raw[11] = 0;
   } else if constexpr (F == kQ4_0) {
     const uint8_t* p = row + (size_t)u * 36;  // two 18-byte blocks, dword aligned
     ld4(p, raw);
@@ -303,6 +321,7 @@ template <> struct Dig<kQ6_K> { static constexpr int NG = 1, GW = 28, US = 28; s
 // (elements p, p+4, p+8, p+12: the bytes a code dword yields for shift 2p) x 3
 // digits, then the scale and the two sub-block sums as for Q6_K.
 template <> struct Dig<kQ2_K> { static constexpr int NG = 2, GW = 28, US = 56; static constexpr bool contig = false; };
+template <> struct Dig<kQ3_K> { static constexpr int NG = 2, GW = 28, US = 56; static constexpr bool contig = false; };
 
 __device__ __forceinline__ uint32_t plane_bytes(uint32_t a, uint32_t b, uint32_t c, uint32_t e, int d) {
   // byte d of a, b, c, e -> bytes 0, 1, 2, 3
@@ -388,7 +407,7 @@ __device__ __forceinline__ void stage_store(const XChunks<SIT>& st, int keff, ui
       const int g = c >> 2;
       uint32_t* rec = lds + (size_t)r * lds_stride + (size_t)(g / D::NG) * D::US + (g % D::NG) * D::GW;
       uint32_t* pl = rec + 6 * k;
-      if constexpr (F == kQ2_K) {
+      if constexpr (F == kQ2_K || F == kQ3_K) {
         // chunk k is half k & 1 of sub-block k >> 1: bytes 2 (k & 1), +1 of its
         // phase planes (elements p and p + 4 of this chunk)
         uint16_t* pb = reinterpret_cast<uint16_t*>(rec + 12 * (k >> 1)) + (k & 1);
@@ -531,6 +550,47 @@ __device__ __forceinline__ void accumulate_dig(const uint32_t* raw, int u, PL pl
         acc = fmaf(S * xscale, digits_value(i0, i1, i2), fmaf(-Mn, xsum, acc));
       }
     }
+  } else if constexpr (F == kQ3_K) {
+    // 3-bit codes q = low2 | hbit << 2, value d * scale * (q - 4) with a
+    // signed 6-bit scale (compute.rs:813-833): sum = S (sum q x - 4 sum x)
+    const uint32_t sh = raw[10];
+    const uint32_t hm0 = __builtin_amdgcn_alignbit(raw[1], raw[0], sh);
+    const uint32_t hm1 = __builtin_amdgcn_alignbit(raw[2], raw[1], sh);
+    uint32_t qd[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) qd[k] = __builtin_amdgcn_alignbit(raw[4 + k], raw[3 + k], sh);
+    const float d = f16_to_f32(raw[9] & 0xFFFFu);
+    const int j = u & 3;
+    const uint32_t hi2byte = (raw[8] >> (16 + 8 * (j & 1))) & 0xFFu;  // scales[8 + j]
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const float xscale = __uint_as_float(pl(h * D::GW + 24));
+#pragma unroll
+      for (int sb = 0; sb < 2; sb++) {
+        const int s4 = 2 * h + sb;  // sub-block 4j + s4
+        // high bits of its 16 elements: bytes 2 s4, 2 s4 + 1 of hmask[8j ..]
+        const uint32_t hw = ((s4 < 2 ? hm0 : hm1) >> (16 * (s4 & 1))) & 0xFFFFu;
+        // bytes: A, A >> 4, B, B >> 4 (A, B the two hmask bytes): bit p of
+        // byte i is the high bit of element 4 i + p
+        const uint32_t nib = (hw >> 4) & 0x0F0Fu;
+        const uint32_t hr = __builtin_amdgcn_perm(nib, hw, 0x05010400u);
+        int i0 = 0, i1 = 0, i2 = 0;
+#pragma unroll
+        for (int ph = 0; ph < 4; ph++) {
+          const uint32_t q = ((qd[s4] >> (2 * ph)) & 0x03030303u) | (((hr >> ph) & 0x01010101u) << 2);
+          const int b = h * D::GW + 12 * sb + 3 * ph;
+          i0 = dot4(q, pl(b + 0), i0);
+          i1 = dot4(q, pl(b + 1), i1);
+          i2 = dot4(q, pl(b + 2), i2);
+        }
+        const uint32_t lo4 = (raw[8] >> (8 * h + 4 * sb)) & 15u;  // scales[2j + h] nibble sb
+        const uint32_t hi2 = (hi2byte >> (2 * s4)) & 3u;
+        const int sv = (int)((lo4 | (hi2 << 4)) ^ 32u) - 32;  // sign-extended 6 bits
+        const float S = d * (float)sv;
+        const float xsum = __uint_as_float(pl(h * D::GW + 25 + sb));
+        acc = fmaf(S * xscale, digits_value(i0, i1, i2), fmaf(-4.0f * S, xsum, acc));
+      }
+    }
   } else {  // kQ6_K quarter: 6-bit codes + 32 as bytes, two 16-element scale groups
     const uint32_t sh = raw[9];
     uint32_t ql[4], qh[2];
@@ -577,7 +637,7 @@ __device__ __forceinline__ void lds_barrier() {
 
 // Vector memory instructions one load_unit issues.
 template <int F> constexpr int loads_per_unit() {
-  return (F == kQ4_K || F == kQ4_0 || F == kQ2_K) ? 3 : F == kQ5_K ? 4 : 5;
+  return (F == kQ4_K || F == kQ4_0 || F == kQ2_K) ? 3 : F == kQ5_K ? 4 : F == kQ3_K ? 6 : 5;
 }
 
 // rows whose weight loads are in flight at once in a wave (measured at
@@ -1211,7 +1271,7 @@ bool fast_aligned(const uint8_t* w, const float* x, int in_dim, int bpr) {
   const uintptr_t a = (uintptr_t)w;
   if ((((uintptr_t)x) & 15) || (in_dim & 3)) return false;  // float4 staging of x
   if constexpr (F == kQ4_K || F == kQ5_K) return (a & 15u) == 0;
-  else if constexpr (F == kQ2_K) return (a & 3u) == 0;
+  else if constexpr (F == kQ2_K || F == kQ3_K) return (a & 3u) == 0;
   else return (a & 3u) == 0 && (bpr % 2) == 0;  // Q4_0 / Q8_0 pairs, Q6_K dword rows
 }
 
@@ -1573,6 +1633,8 @@ size_t matvec_b1_ext_workspace_bytes(int dtype, const void* w, const float* x, s
       return fast_aligned<kQ5_K>(wb, x, id, id / 256) ? b1_workspace_floats<kQ5_K>((int)out_dim, id / 256) * 4 : 0;
     case kQ2_K:
       return fast_aligned<kQ2_K>(wb, x, id, id / 256) ? b1_workspace_floats<kQ2_K>((int)out_dim, id / 256) * 4 : 0;
+    case kQ3_K:
+      return fast_aligned<kQ3_K>(wb, x, id, id / 256) ? b1_workspace_floats<kQ3_K>((int)out_dim, id / 256) * 4 : 0;
     default: return 0;
   }
 }
@@ -1592,6 +1654,9 @@ hipError_t launch_matvec_b1_ext(int dtype, const uint8_t* w, const float* x, flo
     case kQ2_K:
       if (bpr == 0 || !fast_aligned<kQ2_K>(w, x, id, bpr)) return hipSuccess;
       return b1_dispatch<kQ2_K>(w, x, y, (int)out_dim, bpr, s, ws, wf, used);
+    case kQ3_K:
+      if (bpr == 0 || !fast_aligned<kQ3_K>(w, x, id, bpr)) return hipSuccess;
+      return b1_dispatch<kQ3_K>(w, x, y, (int)out_dim, bpr, s, ws, wf, used);
     default: return hipSuccess;
   }
 }

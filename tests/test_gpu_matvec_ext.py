@@ -157,12 +157,13 @@ def test_host_twin_new_types():
         assert np.all(y == 0)
 
 
-@pytest.mark.parametrize("dtype", [ssdq.Q5_K, ssdq.Q2_K], ids=["Q5_K", "Q2_K"])
+@pytest.mark.parametrize("dtype", [ssdq.Q5_K, ssdq.Q2_K, ssdq.Q3_K], ids=["Q5_K", "Q2_K", "Q3_K"])
 @pytest.mark.parametrize("out_dim,in_dim", [(14336, 4096), (4096, 14336), (77, 768), (130, 256 * 5)])
 def test_batch1_digit_kernel(dtype, out_dim, in_dim):
-    # batch 1 with aligned weights (Q5_K: 16 bytes, Q2_K: 4) runs the digit-plane
-    # kernel (K-sliced past 128 units per row); the byte-addressed float kernel
-    # is the cross-check
+    # batch 1 with aligned weights (Q5_K: 16 bytes, Q2_K / Q3_K: 4) runs the
+    # digit-plane kernel (K-sliced past 128 units per row; Q3_K rows of an odd
+    # block count start 2 bytes off a dword); the byte-addressed float kernel is
+    # the cross-check
     w = synth.quant_weights(dtype, out_dim, in_dim, 7000 + in_dim + dtype)
     x = synth.normal_f32(in_dim, 7001)
     name = ssdq.TYPE_NAMES[dtype]

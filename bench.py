@@ -225,6 +225,7 @@ def extras(torch, ssdq, synth, timer, np):
         ("q6_k_matvec_4096x14336_b1", ssdq.Q6_K, 4096, 14336, 1, 3),
         ("q4_k_matvec_4096x14336_b1", ssdq.Q4_K, 4096, 14336, 1, 3),  # FFN down: K-sliced rows
         ("q5_k_matvec_4096x14336_b1", ssdq.Q5_K, 4096, 14336, 1, 3),
+        ("q4_k_matvec_28672x8192_b1", ssdq.Q4_K, 28672, 8192, 1, 3),  # a 70B-sized FFN up projection
     ]
     # the reference's other matvec_quantized types at the north-star shape
     for k, dt in enumerate(ssdq.MATVEC_EXTRA_TYPES):

@@ -1284,10 +1284,13 @@ struct B1Plan {
 };
 
 template <int F>
-B1Plan<F> b1_plan(int bpr) {
+B1Plan<F> b1_plan(int bpr, int out_dim) {
   const int U = bpr * Geom<F>::bs / FastUnit<F>::E;
   B1Plan<F> p;
-  if (U <= 128) {
+  // Rows of 65-128 units run whole with two units per lane (3 rows per wave)
+  // while that fits one round of workgroups; beyond it two K slices of one
+  // unit per lane fit more rows per wave (14336 x 4096 Q6_K: 18.4 -> 15.2 us)
+  if (U <= 64 || (U <= 128 && out_dim <= 3 * 12 * device_cu_count())) {
     p.upl = U <= 64 ? 1 : 2;
     p.slice_bpr = bpr;
     p.full = (U == p.upl * 64);
@@ -1309,7 +1312,7 @@ B1Plan<F> b1_plan(int bpr) {
 
 template <int F>
 size_t b1_workspace_floats(int out_dim, int bpr) {
-  const B1Plan<F> p = b1_plan<F>(bpr);
+  const B1Plan<F> p = b1_plan<F>(bpr, out_dim);
   return p.slices > 1 ? (size_t)p.slices * out_dim : 0;
 }
 
@@ -1318,7 +1321,7 @@ hipError_t b1_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, 
                        hipStream_t s, float* ws, size_t ws_floats, bool* used) {
   const int U = bpr * Geom<F>::bs / FastUnit<F>::E;
   if (U == 0) return hipSuccess;
-  const B1Plan<F> p = b1_plan<F>(bpr);
+  const B1Plan<F> p = b1_plan<F>(bpr, out_dim);
   if (p.slices > 1 && (!ws || ws_floats < (size_t)p.slices * out_dim)) return hipSuccess;
   float* dst = p.slices > 1 ? ws : y;
   *used = true;
@@ -1326,18 +1329,28 @@ hipError_t b1_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, 
   // (Four waves sharing each row of 129-256 units, summed in LDS, avoid the
   // slices' partials and second launch, but every workgroup then stages the
   // whole x: 4096 x 14336 Q4_K took 15.6 us against 14.0 us sliced.)
-  // K-sliced rows: 5 or 8 rows per wave, whichever needs fewer rounds of
-  // workgroups (one per CU, 12 row streams each, as run_b1_sit sizes the grid)
-  // times rows.  4096 x 14336 Q4_K: 4 slices x 64 workgroups in one round,
-  // 14.0 us, against 4 x 69 in two rounds with 5 rows, 18.2 us; Q6_K's 7 slices
-  // need two rounds either way and keep 5 rows (16.0 us against 19.9).
-  auto sliced_cost = [&](int rmax) {
+  // K-sliced rows: 5, 8 or 10 rows per wave, whichever needs the fewest rounds
+  // of workgroups (one per CU, 12 row streams each, as run_b1_sit sizes the
+  // grid) times rows, ties to fewer rounds.  4096 x 14336 Q4_K: 4 slices x 64
+  // workgroups in one round with 8 rows, 14.0 us, against 4 x 69 in two rounds
+  // with 5 rows, 18.2 us.
+  auto sliced_rounds = [&](int rmax) {
     const long cu = device_cu_count(), streams = (out_dim + rmax - 1) / rmax;
     long n_wg = std::max<long>(cu / p.slices, (streams + 11) / 12);
     n_wg = std::max<long>(1, std::min<long>(n_wg, (out_dim + 11) / 12));
-    return (n_wg * p.slices + cu - 1) / cu * rmax;
+    return (n_wg * p.slices + cu - 1) / cu;
   };
-  if (p.upl == 1 && p.slices > 1 && sliced_cost(8) < sliced_cost(5))
+  int rsl = 5;
+  if (p.upl == 1 && p.slices > 1) {
+    for (int cand : {8, 10}) {
+      const long c = sliced_rounds(cand) * cand, b = sliced_rounds(rsl) * rsl;
+      if (c < b || (c == b && sliced_rounds(cand) < sliced_rounds(rsl))) rsl = cand;
+    }
+  }
+  if (p.upl == 1 && p.slices > 1 && rsl == 10)
+    e = p.full ? run_b1<F, 1, 10, true>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s)
+               : run_b1<F, 1, 10, false>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s);
+  else if (p.upl == 1 && p.slices > 1 && rsl == 8)
     e = p.full ? run_b1<F, 1, 8, true>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s)
                : run_b1<F, 1, 8, false>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s);
   else if (p.upl == 1 && p.slices == 1 && out_dim <= 2 * 12 * device_cu_count())

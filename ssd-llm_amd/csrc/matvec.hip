@@ -1329,33 +1329,33 @@ hipError_t b1_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, 
   // (Four waves sharing each row of 129-256 units, summed in LDS, avoid the
   // slices' partials and second launch, but every workgroup then stages the
   // whole x: 4096 x 14336 Q4_K took 15.6 us against 14.0 us sliced.)
-  // K-sliced rows: 5, 8 or 10 rows per wave, whichever needs the fewest rounds
-  // of workgroups (one per CU, 12 row streams each, as run_b1_sit sizes the
-  // grid) times rows, ties to fewer rounds.  4096 x 14336 Q4_K: 4 slices x 64
-  // workgroups in one round with 8 rows, 14.0 us, against 4 x 69 in two rounds
-  // with 5 rows, 18.2 us.
-  auto sliced_rounds = [&](int rmax) {
+  // Rows per wave (one unit per lane): the fewest of 2, 5, 8, 10 whose
+  // workgroups (one per CU, 12 row streams each, as run_b1_sit sizes the grid)
+  // fit one round, else the fewest rounds x rows.  Rows past a wave's share are
+  // still loaded (clamped), so spare capacity costs bandwidth; a second round
+  // costs a whole round.  4096 x 4096 Q4_0: 2 rows, 5.55 -> 4.92 us; 4096 x
+  // 14336 Q4_K (4 slices): 8 rows, 18.2 -> 14.0 us; 14336 x 4096: 5 rows.
+  auto rounds = [&](int rmax) {
     const long cu = device_cu_count(), streams = (out_dim + rmax - 1) / rmax;
     long n_wg = std::max<long>(cu / p.slices, (streams + 11) / 12);
     n_wg = std::max<long>(1, std::min<long>(n_wg, (out_dim + 11) / 12));
     return (n_wg * p.slices + cu - 1) / cu;
   };
-  int rsl = 5;
-  if (p.upl == 1 && p.slices > 1) {
-    for (int cand : {8, 10}) {
-      const long c = sliced_rounds(cand) * cand, b = sliced_rounds(rsl) * rsl;
-      if (c < b || (c == b && sliced_rounds(cand) < sliced_rounds(rsl))) rsl = cand;
-    }
+  int rsl = 0;
+  for (int cand : {2, 5, 8, 10})
+    if (!rsl && rounds(cand) == 1) rsl = cand;
+  if (!rsl) {
+    rsl = 5;
+    for (int cand : {8, 10})
+      if (rounds(cand) * cand < rounds(rsl) * rsl) rsl = cand;
   }
-  if (p.upl == 1 && p.slices > 1 && rsl == 10)
+  if (p.upl == 1 && rsl == 10)
     e = p.full ? run_b1<F, 1, 10, true>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s)
                : run_b1<F, 1, 10, false>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s);
-  else if (p.upl == 1 && p.slices > 1 && rsl == 8)
+  else if (p.upl == 1 && rsl == 8)
     e = p.full ? run_b1<F, 1, 8, true>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s)
                : run_b1<F, 1, 8, false>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s);
-  else if (p.upl == 1 && p.slices == 1 && out_dim <= 2 * 12 * device_cu_count())
-    // at most 2 rows per row stream: rows past a wave's share would still be
-    // loaded (clamped), so small matrices take 2 rows per wave
+  else if (p.upl == 1 && rsl == 2)
     e = p.full ? run_b1<F, 1, 2, true>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s)
                : run_b1<F, 1, 2, false>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s);
   else if (p.upl == 1)

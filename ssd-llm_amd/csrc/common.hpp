@@ -9,7 +9,7 @@ namespace ssdq {
 constexpr int kWave = 64;  // CDNA wavefront width
 
 // GgmlType ids (src/model/gguf.rs:17-48) and block geometry (gguf.rs:87-135).
-enum : int { kQ4_0 = 2, kQ8_0 = 8, kQ2_K = 10, kQ3_K = 11, kQ4_K = 12, kQ5_K = 13, kQ6_K = 14 };
+enum : int { kQ4_0 = 2, kQ8_0 = 8, kQ2_K = 10, kQ3_K = 11, kQ4_K = 12, kQ5_K = 13, kQ6_K = 14, kQ8_K = 15 };
 
 template <int F> struct Geom;
 template <> struct Geom<kQ4_0> { static constexpr int bs = 32, bb = 18; };
@@ -19,6 +19,7 @@ template <> struct Geom<kQ3_K> { static constexpr int bs = 256, bb = 110; };
 template <> struct Geom<kQ4_K> { static constexpr int bs = 256, bb = 144; };
 template <> struct Geom<kQ5_K> { static constexpr int bs = 256, bb = 176; };
 template <> struct Geom<kQ6_K> { static constexpr int bs = 256, bb = 210; };
+template <> struct Geom<kQ8_K> { static constexpr int bs = 256, bb = 292; };
 
 // IEEE binary16 -> binary32 (exact widening, v_cvt_f32_f16).
 __device__ __forceinline__ float f16_to_f32(uint32_t bits16) {

@@ -59,7 +59,7 @@ struct MatvecFuse {
 };
 // One fused launch when the shapes allow it (Q4_0 / Q8_0 / Q4_K / Q6_K, whole
 // rows of at most 128 units, aligned operands); *used = false otherwise.
-// Batch-1 digit-plane kernel for a matvec_ext type that has one (Q5_K, Q2_K, Q3_K); sets
+// Batch-1 digit-plane kernel for a matvec_ext type that has one (Q5_K, Q2_K, Q3_K, Q8_K); sets
 // *used = false (nothing launched) when the type, alignment or workspace does
 // not fit, and the caller takes launch_matvec_ext.
 size_t matvec_b1_ext_workspace_bytes(int dtype, const void* w, const float* x, size_t out_dim, size_t in_dim);

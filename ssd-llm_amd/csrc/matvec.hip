@@ -46,6 +46,7 @@ namespace {
 //   Q5_K (batch-1 kernel only): two sub-blocks (header, 8 high-bit bytes, 32 code bytes)
 //   Q2_K (batch-1 kernel only): four 16-element sub-blocks (d|dmin, 4 scale bytes, 16 code bytes)
 //   Q3_K (batch-1 kernel only): four 16-element sub-blocks (8 high-bit bytes, 16 code bytes, scales, d)
+//   Q8_K (batch-1 kernel only): 64 int8 codes and the block's f32 scale
 // E elements, NSUM x-sum groups of SUMG elements, NW dwords of raw data.
 template <int F> struct FastUnit;
 template <> struct FastUnit<kQ4_K> {
@@ -70,6 +71,10 @@ template <> struct FastUnit<kQ2_K> {
 };
 template <> struct FastUnit<kQ3_K> {
   static constexpr int E = 64, NSUM = 4, SUMG = 16, NW = 12;
+  static constexpr bool prescale = false;
+};
+template <> struct FastUnit<kQ8_K> {
+  static constexpr int E = 64, NSUM = 2, SUMG = 32, NW = 17;
   static constexpr bool prescale = false;
 };
 template <> struct FastUnit<kQ6_K> {
@@ -132,6 +137,15 @@ __device__ __forceinline__ void load_unit(const uint8_t* __restrict__ row, int u
     raw[9] = ldh(blk + 108);                                              // d
     raw[10] = mis * 8u;                                                   // realignment shift
     raw[11] = 0;
+  } else if constexpr (F == kQ8_K) {
+    // block (compute.rs:981-987): f32 d | int8 qs[256] | bsums (unused); dword aligned
+    const uint8_t* blk = row + (size_t)(u >> 2) * 292;
+    raw[0] = ld1(blk);
+    const uint8_t* q = blk + 4 + 64 * (u & 3);
+    ld4(q, raw + 1);
+    ld4(q + 16, raw + 5);
+    ld4(q + 32, raw + 9);
+    ld4(q + 48, raw + 13);
   } else if constexpr (F == kQ4_0) {
     const uint8_t* p = row + (size_t)u * 36;  // two 18-byte blocks, dword aligned
     ld4(p, raw);
@@ -316,6 +330,7 @@ template <> struct Dig<kQ4_K> { static constexpr int NG = 2, GW = 26, US = 52; s
 template <> struct Dig<kQ4_0> { static constexpr int NG = 2, GW = 26, US = 52; static constexpr bool contig = false; };
 template <> struct Dig<kQ5_K> { static constexpr int NG = 2, GW = 26, US = 52; static constexpr bool contig = false; };
 template <> struct Dig<kQ8_0> { static constexpr int NG = 2, GW = 26, US = 52; static constexpr bool contig = true; };
+template <> struct Dig<kQ8_K> { static constexpr int NG = 2, GW = 26, US = 52; static constexpr bool contig = true; };
 template <> struct Dig<kQ6_K> { static constexpr int NG = 1, GW = 28, US = 28; static constexpr bool contig = false; };
 // Q2_K: a group record holds two 16-element sub-blocks, each as 4 phase planes
 // (elements p, p+4, p+8, p+12: the bytes a code dword yields for shift 2p) x 3
@@ -525,6 +540,22 @@ __device__ __forceinline__ void accumulate_dig(const uint32_t* raw, int u, PL pl
       const float xscale = __uint_as_float(pl(h * D::GW + 24));
       acc = fmaf(d * xscale, digits_value(i0, i1, i2), acc);
     }
+  } else if constexpr (F == kQ8_K) {
+    const float d = __uint_as_float(raw[0]);
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      int i0 = 0, i1 = 0, i2 = 0;
+#pragma unroll
+      for (int c = 0; c < 8; c++) {
+        const uint32_t wd = raw[1 + 8 * h + c];
+        const int b = h * D::GW + 6 * (c >> 1) + 3 * (c & 1);
+        i0 = dot4(wd, pl(b + 0), i0);
+        i1 = dot4(wd, pl(b + 1), i1);
+        i2 = dot4(wd, pl(b + 2), i2);
+      }
+      const float xscale = __uint_as_float(pl(h * D::GW + 24));
+      acc = fmaf(d * xscale, digits_value(i0, i1, i2), acc);
+    }
   } else if constexpr (F == kQ2_K) {
     // 16 sub-blocks of 16 elements; scale / min = low / high nibble of the
     // sub-block's byte (compute.rs:948-960): value d*s*q - dmin*m
@@ -637,7 +668,7 @@ __device__ __forceinline__ void lds_barrier() {
 
 // Vector memory instructions one load_unit issues.
 template <int F> constexpr int loads_per_unit() {
-  return (F == kQ4_K || F == kQ4_0 || F == kQ2_K) ? 3 : F == kQ5_K ? 4 : F == kQ3_K ? 6 : 5;
+  return (F == kQ4_K || F == kQ4_0 || F == kQ2_K) ? 3 : F == kQ5_K ? 4 : F == kQ3_K ? 6 : 5;  // Q8_0 / Q8_K / Q6_K: 5
 }
 
 // rows whose weight loads are in flight at once in a wave (measured at
@@ -1271,7 +1302,7 @@ bool fast_aligned(const uint8_t* w, const float* x, int in_dim, int bpr) {
   const uintptr_t a = (uintptr_t)w;
   if ((((uintptr_t)x) & 15) || (in_dim & 3)) return false;  // float4 staging of x
   if constexpr (F == kQ4_K || F == kQ5_K) return (a & 15u) == 0;
-  else if constexpr (F == kQ2_K || F == kQ3_K) return (a & 3u) == 0;
+  else if constexpr (F == kQ2_K || F == kQ3_K || F == kQ8_K) return (a & 3u) == 0;
   else return (a & 3u) == 0 && (bpr % 2) == 0;  // Q4_0 / Q8_0 pairs, Q6_K dword rows
 }
 
@@ -1648,6 +1679,8 @@ size_t matvec_b1_ext_workspace_bytes(int dtype, const void* w, const float* x, s
       return fast_aligned<kQ2_K>(wb, x, id, id / 256) ? b1_workspace_floats<kQ2_K>((int)out_dim, id / 256) * 4 : 0;
     case kQ3_K:
       return fast_aligned<kQ3_K>(wb, x, id, id / 256) ? b1_workspace_floats<kQ3_K>((int)out_dim, id / 256) * 4 : 0;
+    case kQ8_K:  // whole rows only (see launch_matvec_b1_ext)
+      return 0;
     default: return 0;
   }
 }
@@ -1670,6 +1703,11 @@ hipError_t launch_matvec_b1_ext(int dtype, const uint8_t* w, const float* x, flo
     case kQ3_K:
       if (bpr == 0 || !fast_aligned<kQ3_K>(w, x, id, bpr)) return hipSuccess;
       return b1_dispatch<kQ3_K>(w, x, y, (int)out_dim, bpr, s, ws, wf, used);
+    case kQ8_K:
+      // whole rows of up to 128 units: K-sliced Q8_K rows (4096 x 14336) measured
+      // no faster than mv_ext (20.6 against 19.6 us), 14336 x 4096 16.8 -> 14.3 us
+      if (bpr == 0 || bpr * 4 > 128 || !fast_aligned<kQ8_K>(w, x, id, bpr)) return hipSuccess;
+      return b1_dispatch<kQ8_K>(w, x, y, (int)out_dim, bpr, s, nullptr, 0, used);
     default: return hipSuccess;
   }
 }

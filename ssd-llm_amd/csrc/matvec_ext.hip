@@ -32,7 +32,7 @@ namespace ssdq {
 namespace {
 
 enum : int {
-  kF16 = 1, kQ8_K = 15, kIQ2_XXS = 16, kIQ2_XS = 17, kIQ3_XXS = 18,
+  kF16 = 1, kIQ2_XXS = 16, kIQ2_XS = 17, kIQ3_XXS = 18,
   kIQ4_NL = 20, kIQ3_S = 21, kIQ4_XS = 23, kBF16 = 30
 };
 

@@ -157,10 +157,10 @@ def test_host_twin_new_types():
         assert np.all(y == 0)
 
 
-@pytest.mark.parametrize("dtype", [ssdq.Q5_K, ssdq.Q2_K, ssdq.Q3_K], ids=["Q5_K", "Q2_K", "Q3_K"])
+@pytest.mark.parametrize("dtype", [ssdq.Q5_K, ssdq.Q2_K, ssdq.Q3_K, ssdq.Q8_K], ids=["Q5_K", "Q2_K", "Q3_K", "Q8_K"])
 @pytest.mark.parametrize("out_dim,in_dim", [(14336, 4096), (4096, 14336), (77, 768), (130, 256 * 5)])
 def test_batch1_digit_kernel(dtype, out_dim, in_dim):
-    # batch 1 with aligned weights (Q5_K: 16 bytes, Q2_K / Q3_K: 4) runs the
+    # batch 1 with aligned weights (Q5_K: 16 bytes, Q2_K / Q3_K / Q8_K: 4) runs the
     # digit-plane kernel (K-sliced past 128 units per row; Q3_K rows of an odd
     # block count start 2 bytes off a dword); the byte-addressed float kernel is
     # the cross-check

@@ -408,6 +408,12 @@ __global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ p
   }
 }
 
+#undef GEMM_SEGMENT
+#undef GEMM_FIRST
+#undef GEMM_WEIGHTS
+#undef GEMM_OUT
+#undef GEMM_MATS_PARAMS
+
 }  // namespace
 
 bool gemm_q4k_mfma_ok(const void* w, const void* x) {
@@ -524,5 +530,7 @@ hipError_t launch_gemm_q4k(const uint8_t* const* w, const size_t* n, int count, 
     if (n[i]) e = launch_matvec(kQ4_K, w[i], xf, y[i], n[i], K, M, s);
   return e;
 }
+
+#undef GEMM_MATS_ARGS
 
 }  // namespace ssdq

@@ -1360,7 +1360,7 @@ hipError_t b1_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, 
   // (Four waves sharing each row of 129-256 units, summed in LDS, avoid the
   // slices' partials and second launch, but every workgroup then stages the
   // whole x: 4096 x 14336 Q4_K took 15.6 us against 14.0 us sliced.)
-  // Rows per wave (one unit per lane): the fewest of 2, 5, 6, 8, 10 whose
+  // Rows per wave (one unit per lane): the fewest of 2, 4, 5, 6, 8, 10 whose
   // workgroups (one per CU, 12 row streams each, as run_b1_sit sizes the grid)
   // fit one round, else the fewest rounds x rows.  Rows past a wave's share are
   // still loaded (clamped), so spare capacity costs bandwidth; a second round
@@ -1373,7 +1373,7 @@ hipError_t b1_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, 
     return (n_wg * p.slices + cu - 1) / cu;
   };
   int rsl = 0;
-  for (int cand : {2, 5, 6, 8, 10})
+  for (int cand : {2, 4, 5, 6, 8, 10})
     if (!rsl && rounds(cand) == 1) rsl = cand;
   if (!rsl) {
     rsl = 5;
@@ -1386,6 +1386,9 @@ hipError_t b1_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, 
   else if (p.upl == 1 && rsl == 8)
     e = p.full ? run_b1<F, 1, 8, true>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s)
                : run_b1<F, 1, 8, false>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s);
+  else if (p.upl == 1 && rsl == 4)
+    e = p.full ? run_b1<F, 1, 4, true>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s)
+               : run_b1<F, 1, 4, false>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s);
   else if (p.upl == 1 && rsl == 6)
     e = p.full ? run_b1<F, 1, 6, true>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s)
                : run_b1<F, 1, 6, false>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s);

@@ -395,6 +395,22 @@ __global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ p
                                                      int N, int split) {
   const int mn = M * N;
   const int stride = gridDim.x * blockDim.x;
+  if (!MULTI && (mn & 3) == 0 && ((uintptr_t)y0 & 15) == 0) {  // one matrix: 16-byte loads and stores
+    const int mn4 = mn >> 2;
+    const float4* p4 = reinterpret_cast<const float4*>(part);
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < mn4; i += stride) {
+      float4 s = p4[i];
+      for (int z = 1; z < split; z++) {
+        const float4 v = p4[(size_t)z * mn4 + i];
+        s.x += v.x;
+        s.y += v.y;
+        s.z += v.z;
+        s.w += v.w;
+      }
+      reinterpret_cast<float4*>(y0)[i] = s;
+    }
+    return;
+  }
   for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < mn; i += stride) {
     float s = part[i];
     for (int z = 1; z < split; z++) s += part[(size_t)z * mn + i];

@@ -59,13 +59,15 @@ struct MatvecFuse {
 };
 // One fused launch when the shapes allow it (Q4_0 / Q8_0 / Q4_K / Q6_K, whole
 // rows of at most 128 units, aligned operands); *used = false otherwise.
-// Batch-1 digit-plane kernel for a matvec_ext type that has one (Q5_K, Q2_K, Q3_K, Q8_K); sets
-// *used = false (nothing launched) when the type, alignment or workspace does
-// not fit, and the caller takes launch_matvec_ext.
-size_t matvec_b1_ext_workspace_bytes(int dtype, const void* w, const float* x, size_t out_dim, size_t in_dim);
-hipError_t launch_matvec_b1_ext(int dtype, const uint8_t* w, const float* x, float* y, size_t out_dim,
-                                size_t in_dim, hipStream_t s, void* workspace, size_t workspace_bytes,
-                                bool* used);
+// Digit-plane kernels (mv_b1 at batch 1, mv_bn for batches) for the matvec_ext
+// types that have them (Q5_K, Q2_K, Q3_K, Q8_K); sets *used = false (nothing
+// launched) when the type, alignment or workspace does not fit, and the caller
+// takes launch_matvec_ext.
+size_t matvec_digit_ext_workspace_bytes(int dtype, const void* w, const float* x, size_t out_dim, size_t in_dim,
+                                        size_t batch);
+hipError_t launch_matvec_digit_ext(int dtype, const uint8_t* w, const float* x, float* y, size_t out_dim,
+                                   size_t in_dim, size_t batch, hipStream_t s, void* workspace,
+                                   size_t workspace_bytes, bool* used);
 hipError_t launch_matvec_fused(int dtype, const MatvecFuse& f, int total_rows, const float* x,
                                size_t in_dim, hipStream_t stream, bool* used);
 // Pieces of the unfused decode layer.

@@ -1608,6 +1608,35 @@ hipError_t bn_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, 
   return hipGetLastError();
 }
 
+// The digit-plane kernels alone (mv_b1 at batch 1, mv_bn for chunks of 8 / 4 /
+// 2 rows and mv_b1 for a last single row), for the types whose float path is
+// mv_ext: *used = false when they do not apply (the first chunk decides).
+template <int F>
+hipError_t digit_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, int in_dim, int bpr,
+                          int batch, hipStream_t s, float* ws, size_t ws_floats, bool* used) {
+  *used = false;
+  if (bpr == 0 || !fast_aligned<F>(w, x, in_dim, bpr)) return hipSuccess;
+  if (batch == 1) return b1_dispatch<F>(w, x, y, out_dim, bpr, s, ws, ws_floats, used);
+  int b0 = 0;
+  while (b0 < batch) {
+    const int left = batch - b0;
+    const float* xb = x + (size_t)b0 * in_dim;
+    float* yb = y + (size_t)b0 * out_dim;
+    bool u = false;
+    hipError_t e;
+    int take;
+    if (left >= 8) { take = 8; e = bn_dispatch<F, 8>(w, xb, yb, out_dim, in_dim, bpr, s, ws, ws_floats, &u); }
+    else if (left >= 4) { take = 4; e = bn_dispatch<F, 4>(w, xb, yb, out_dim, in_dim, bpr, s, ws, ws_floats, &u); }
+    else if (left >= 2) { take = 2; e = bn_dispatch<F, 2>(w, xb, yb, out_dim, in_dim, bpr, s, ws, ws_floats, &u); }
+    else { take = 1; e = b1_dispatch<F>(w, xb, yb, out_dim, bpr, s, ws, ws_floats, &u); }
+    if (e != hipSuccess) return e;
+    if (!u) return b0 == 0 ? hipSuccess : hipErrorInvalidValue;
+    b0 += take;
+  }
+  *used = true;
+  return hipSuccess;
+}
+
 template <int F>
 hipError_t fast_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, int in_dim,
                          int bpr, int batch, hipStream_t s, float* ws, size_t ws_floats,
@@ -1674,50 +1703,6 @@ hipError_t fast_dispatch(const uint8_t* w, const float* x, float* y, int out_dim
 
 }  // namespace
 
-size_t matvec_b1_ext_workspace_bytes(int dtype, const void* w, const float* x, size_t out_dim, size_t in_dim) {
-  if (out_dim == 0) return 0;
-  const int id = (int)in_dim;
-  const uint8_t* wb = (const uint8_t*)w;
-  switch (dtype) {
-    case kQ5_K:
-      return fast_aligned<kQ5_K>(wb, x, id, id / 256) ? b1_workspace_floats<kQ5_K>((int)out_dim, id / 256) * 4 : 0;
-    case kQ2_K:
-      return fast_aligned<kQ2_K>(wb, x, id, id / 256) ? b1_workspace_floats<kQ2_K>((int)out_dim, id / 256) * 4 : 0;
-    case kQ3_K:
-      return fast_aligned<kQ3_K>(wb, x, id, id / 256) ? b1_workspace_floats<kQ3_K>((int)out_dim, id / 256) * 4 : 0;
-    case kQ8_K:  // whole rows only (see launch_matvec_b1_ext)
-      return 0;
-    default: return 0;
-  }
-}
-
-hipError_t launch_matvec_b1_ext(int dtype, const uint8_t* w, const float* x, float* y, size_t out_dim,
-                                size_t in_dim, hipStream_t s, void* workspace, size_t workspace_bytes,
-                                bool* used) {
-  *used = false;
-  if (out_dim == 0) return hipSuccess;
-  const int id = (int)in_dim, bpr = id / 256;
-  float* ws = static_cast<float*>(workspace);
-  const size_t wf = workspace_bytes / sizeof(float);
-  switch (dtype) {
-    case kQ5_K:
-      if (bpr == 0 || !fast_aligned<kQ5_K>(w, x, id, bpr)) return hipSuccess;
-      return b1_dispatch<kQ5_K>(w, x, y, (int)out_dim, bpr, s, ws, wf, used);
-    case kQ2_K:
-      if (bpr == 0 || !fast_aligned<kQ2_K>(w, x, id, bpr)) return hipSuccess;
-      return b1_dispatch<kQ2_K>(w, x, y, (int)out_dim, bpr, s, ws, wf, used);
-    case kQ3_K:
-      if (bpr == 0 || !fast_aligned<kQ3_K>(w, x, id, bpr)) return hipSuccess;
-      return b1_dispatch<kQ3_K>(w, x, y, (int)out_dim, bpr, s, ws, wf, used);
-    case kQ8_K:
-      // whole rows of up to 128 units: K-sliced Q8_K rows (4096 x 14336) measured
-      // no faster than mv_ext (20.6 against 19.6 us), 14336 x 4096 16.8 -> 14.3 us
-      if (bpr == 0 || bpr * 4 > 128 || !fast_aligned<kQ8_K>(w, x, id, bpr)) return hipSuccess;
-      return b1_dispatch<kQ8_K>(w, x, y, (int)out_dim, bpr, s, nullptr, 0, used);
-    default: return hipSuccess;
-  }
-}
-
 hipError_t launch_matvec_fused(int dtype, const MatvecFuse& f, int total_rows, const float* x,
                                size_t in_dim, hipStream_t s, bool* used) {
   *used = false;
@@ -1748,6 +1733,42 @@ size_t ws_floats_for(int od, int bpr, size_t batch) {
   size_t n = b1_workspace_floats<F>(od, bpr);  // batch 1, or the last single row of a batch
   if (batch > 1) n = std::max(n, bn_workspace_floats<F>(od, bpr, (int)std::min<size_t>(batch, 8)));
   return n;
+}
+
+size_t matvec_digit_ext_workspace_bytes(int dtype, const void* w, const float* x, size_t out_dim, size_t in_dim,
+                                        size_t batch) {
+  if (out_dim == 0 || batch == 0) return 0;
+  const int od = (int)out_dim, id = (int)in_dim, bpr = id / 256;
+  const uint8_t* wb = (const uint8_t*)w;
+  switch (dtype) {
+    case kQ5_K: return fast_aligned<kQ5_K>(wb, x, id, bpr) ? ws_floats_for<kQ5_K>(od, bpr, batch) * 4 : 0;
+    case kQ2_K: return fast_aligned<kQ2_K>(wb, x, id, bpr) ? ws_floats_for<kQ2_K>(od, bpr, batch) * 4 : 0;
+    case kQ3_K: return fast_aligned<kQ3_K>(wb, x, id, bpr) ? ws_floats_for<kQ3_K>(od, bpr, batch) * 4 : 0;
+    case kQ8_K: return 0;  // whole rows only (see launch_matvec_digit_ext)
+    default: return 0;
+  }
+}
+
+hipError_t launch_matvec_digit_ext(int dtype, const uint8_t* w, const float* x, float* y, size_t out_dim,
+                                   size_t in_dim, size_t batch, hipStream_t s, void* workspace,
+                                   size_t workspace_bytes, bool* used) {
+  *used = false;
+  if (out_dim == 0 || batch == 0) return hipSuccess;
+  const int od = (int)out_dim, id = (int)in_dim, bpr = id / 256, b = (int)batch;
+  float* ws = static_cast<float*>(workspace);
+  const size_t wf = workspace_bytes / sizeof(float);
+  switch (dtype) {
+    case kQ5_K: return digit_dispatch<kQ5_K>(w, x, y, od, id, bpr, b, s, ws, wf, used);
+    case kQ2_K: return digit_dispatch<kQ2_K>(w, x, y, od, id, bpr, b, s, ws, wf, used);
+    case kQ3_K: return digit_dispatch<kQ3_K>(w, x, y, od, id, bpr, b, s, ws, wf, used);
+    case kQ8_K:
+      // rows of up to 128 units without workspace: K-sliced Q8_K rows (4096 x
+      // 14336) measured no faster than mv_ext (20.6 against 19.6 us); 14336 x
+      // 4096 at batch 1: 16.8 -> 14.3 us
+      if (bpr * 4 > 128) return hipSuccess;
+      return digit_dispatch<kQ8_K>(w, x, y, od, id, bpr, b, s, nullptr, 0, used);
+    default: return hipSuccess;
+  }
 }
 
 size_t matvec_workspace_bytes(int dtype, const void* w, const float* x, size_t out_dim,

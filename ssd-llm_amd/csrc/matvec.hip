@@ -1319,9 +1319,12 @@ B1Plan<F> b1_plan(int bpr, int out_dim) {
   const int U = bpr * Geom<F>::bs / FastUnit<F>::E;
   B1Plan<F> p;
   // Rows of 65-128 units run whole with two units per lane (3 rows per wave)
-  // while that fits one round of workgroups; beyond it two K slices of one
-  // unit per lane fit more rows per wave (14336 x 4096 Q6_K: 18.4 -> 15.2 us)
-  if (U <= 64 || (U <= 128 && out_dim <= 3 * 12 * device_cu_count())) {
+  // while that fits one round of workgroups and the kernel fits its registers
+  // (units of at most 10 raw dwords: Q4_0, Q6_K, Q2_K; the others spill at 768
+  // threads); otherwise as two K slices of one unit per lane, which fit more
+  // rows per wave (14336 x 4096 Q6_K: 18.4 -> 15.2 us)
+  constexpr bool two_units_fit = FastUnit<F>::NW <= 10;
+  if (U <= 64 || (U <= 128 && two_units_fit && out_dim <= 3 * 12 * device_cu_count())) {
     p.upl = U <= 64 ? 1 : 2;
     p.slice_bpr = bpr;
     p.full = (U == p.upl * 64);

@@ -117,8 +117,8 @@ def matvec_case(torch, ssdq, synth, dtype, out_dim, in_dim, batch, seed_cfg):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 (multi-GPU sharding is "
-                                   "described in DESIGN.md, not run)"}))
+        print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 (the sharding across GPUs "
+                                   "is designed, not run: the boxes here have one GPU each)"}))
         sys.exit(2)
     import numpy as np
     import torch

@@ -49,11 +49,20 @@ def copies_for(nbytes):
 class Timer:
     """Events on the stream the kernels are launched on (torch's current stream).
 
-    Short kernels (the matvecs take ~10 us) are replayed from HIP graphs of
-    GRAPH_CHUNK captured launches, so the host's per-launch cost (ctypes
-    marshalling, ~15 us) does not set the step time."""
+    Short kernels (the matvecs take ~10 us) are replayed from HIP graphs of up
+    to GRAPH_CHUNK captured launches, so the host's per-launch cost (ctypes
+    marshalling, ~15 us) does not set the step time.  A timed block is exactly
+    `steps` launches (whole replays of the chunk graph, then one replay of a
+    graph of the remainder).  Warm-up runs at least `warmup` launches and at
+    least MIN_WARM_S seconds (the first millisecond after a pause runs up to 5%
+    slow), in whole replays.  After the first timed block, further blocks are
+    timed until STAB_S seconds or STAB_BLOCKS blocks have passed: their median
+    is reported beside the first block."""
 
     GRAPH_CHUNK = 50
+    MIN_WARM_S = 0.05
+    STAB_S = 0.02
+    STAB_BLOCKS = 10
 
     def __init__(self, torch, graph=True):
         self.torch = torch
@@ -61,41 +70,76 @@ class Timer:
         self.e0 = torch.cuda.Event(enable_timing=True)
         self.e1 = torch.cuda.Event(enable_timing=True)
 
-    def _timed(self, fn, reps, warmup):
+    def _block(self, body):
         torch = self.torch
-        for i in range(warmup):
-            fn(i)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         self.e0.record()
-        for i in range(reps):
-            fn(i)
+        body()
         self.e1.record()
         torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-        return self.e0.elapsed_time(self.e1) * 1e-3, wall  # seconds (events), seconds (host)
+        return self.e0.elapsed_time(self.e1) * 1e-3, time.perf_counter() - t0
 
-    def run(self, fn, steps, warmup, graph=None):
-        """Returns (seconds for `steps` steps by events, host wall seconds, steps run)."""
+    def run(self, fn, steps, warmup, graph=None, stability=True):
+        """Times `steps` launches of fn(i).  Returns a dict: t (event seconds of
+        the first timed block), wall (its host seconds), steps, chunk (launches
+        per graph replay, 0 when eager), warm_launches, blocks (further blocks
+        timed) and t_median (their median event seconds)."""
         torch = self.torch
-        if not (self.graph if graph is None else graph):
-            t, wall = self._timed(fn, steps, warmup)
-            return t, wall, steps
-        chunk = min(self.GRAPH_CHUNK, steps)
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):  # the library sizes its workspace for this stream
-            for i in range(2):
-                fn(i)
-        torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=side):
-            for i in range(chunk):
-                fn(i)
-        reps = max(1, steps // chunk)
-        t, wall = self._timed(lambda i: g.replay(), reps, max(1, warmup // chunk))
-        del g
-        return t, wall, reps * chunk
+        use_graph = self.graph if graph is None else graph
+        if not use_graph:
+            def body():
+                for i in range(steps):
+                    fn(i)
+            warm, t0 = 0, time.perf_counter()
+            while warm < warmup or time.perf_counter() - t0 < self.MIN_WARM_S:
+                fn(warm)
+                warm += 1
+            chunk, graphs = 0, None
+        else:
+            chunk = min(self.GRAPH_CHUNK, steps)
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):  # the library sizes its workspace for this stream
+                for i in range(2):
+                    fn(i)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=side):
+                for i in range(chunk):
+                    fn(i)
+            rem = steps % chunk
+            g_rem = None
+            if rem:
+                g_rem = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g_rem, stream=side):
+                    for i in range(rem):
+                        fn(i)
+            graphs = (g, g_rem)
+            full = steps // chunk
+
+            def body():
+                for _ in range(full):
+                    g.replay()
+                if g_rem is not None:
+                    g_rem.replay()
+            warm, t0 = 0, time.perf_counter()
+            while warm < warmup or time.perf_counter() - t0 < self.MIN_WARM_S:
+                g.replay()
+                warm += chunk
+                if warm % (20 * chunk) == 0:
+                    torch.cuda.synchronize()
+            torch.cuda.synchronize()
+        t, wall = self._block(body)
+        extra = []
+        if stability:
+            t1 = time.perf_counter()
+            while len(extra) < self.STAB_BLOCKS and (time.perf_counter() - t1 < self.STAB_S or len(extra) < 3):
+                extra.append(self._block(body)[0])
+        del graphs
+        med = sorted(extra)[len(extra) // 2] if extra else t
+        return {"t": t, "wall": wall, "steps": steps, "chunk": chunk, "warm_launches": warm,
+                "blocks": len(extra), "t_median": med}
 
 
 def matvec_case(torch, ssdq, synth, dtype, out_dim, in_dim, batch, seed_cfg):
@@ -134,8 +178,9 @@ def main():
 
     # ---------------------------------------------------------- headline
     step, algo_bytes, _ = matvec_case(torch, ssdq, synth, ssdq.Q4_K, 14336, 4096, 1, 3)
-    t_ev, wall, steps = timer.run(step, args.steps, args.warmup)
-    sec_per_step = t_ev / steps
+    tm = timer.run(step, args.steps, args.warmup)
+    steps, wall = tm["steps"], tm["wall"]
+    sec_per_step = tm["t"] / steps
     value = algo_bytes / sec_per_step / 1e9
 
     result = {
@@ -156,7 +201,11 @@ def main():
                    "out_dim": 14336, "in_dim": 4096, "batch": 1,
                    "weight_copies": copies_for(14336 * ssdq.row_bytes(ssdq.Q4_K, 4096)),
                    "weights": "GGUF Q4_K", "activations": "f32", "accumulate": "f32",
-                   "launch": "eager" if args.eager else f"hip graph of {Timer.GRAPH_CHUNK} launches"},
+                   "launch": "eager" if args.eager else
+                   f"hip graph replays of {tm['chunk']} launches (remainder in a second graph)",
+                   "warmup_launches_run": tm["warm_launches"],
+                   "stability": {"further_blocks_of_steps": tm["blocks"],
+                                 "median_GB/s": round(algo_bytes * steps / tm["t_median"] / 1e9, 1)}},
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "roofline": {
             "bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -232,7 +281,8 @@ def extras(torch, ssdq, synth, timer, np):
         cases.append((f"{ssdq.TYPE_NAMES[dt].lower()}_matvec_14336x4096_b1", dt, 14336, 4096, 1, 6 + k))
     for name, dt, od, idim, b, cfg in cases:
         step, nbytes, _ = matvec_case(torch, ssdq, synth, dt, od, idim, b, cfg)
-        t, _, n = timer.run(step, 200, 500)
+        tr = timer.run(step, 200, 500)
+        t, n = tr["t_median"], tr["steps"]
         gbs = nbytes / (t / n) / 1e9
         out[name] = {"GB/s": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
                      "us": round(t / n * 1e6, 3)}
@@ -250,9 +300,10 @@ def extras(torch, ssdq, synth, timer, np):
         n = copies_for(nbytes)  # weights rotated over copies larger than 2x the last-level cache
         sets = [base] + [[(dt, w.clone(), r, y) for dt, w, r, y in base] for _ in range(n - 1)]
         x = torch.randn(n_embd, device="cuda")
-        tf, _, nf = timer.run(lambda i: fused(sets[i % n], x), 200, 500)
-        ts, _, ns = timer.run(lambda i: [ssdq.matvec(dt, w, x, y, r, n_embd) for dt, w, r, y in sets[i % n]],
-                              200, 500)
+        tr = timer.run(lambda i: fused(sets[i % n], x), 200, 500)
+        tf, nf = tr["t_median"], tr["steps"]
+        tr = timer.run(lambda i: [ssdq.matvec(dt, w, x, y, r, n_embd) for dt, w, r, y in sets[i % n]], 200, 500)
+        ts, ns = tr["t_median"], tr["steps"]
         del sets, base
         out[name] = {"us": round(tf / nf * 1e6, 3), "GB/s": round(nbytes / (tf / nf) / 1e9, 1),
                      "pct_hbm_peak": round(100 * nbytes / (tf / nf) / 1e9 / HBM_PEAK_GBS, 2),
@@ -288,10 +339,12 @@ def extras(torch, ssdq, synth, timer, np):
     sb_ = ssdq.kv_slot_bytes(bs_, kv_)
     for where, slots_ in (("device", torch.empty(nb_ * sb_, dtype=torch.uint8, device="cuda")),
                           ("pinned_host", torch.empty(nb_ * sb_, dtype=torch.uint8).pin_memory())):
-        t, _, n = timer.run(lambda i: ssdq.kv_swap_out(kc_, ks_, vc_, vs_, ids_, nf_, nb_, bs_, kv_, npool_,
-                                                        slots_), 50, 5)
-        ti, _, ni = timer.run(lambda i: ssdq.kv_swap_in(slots_, ids_, nb_, bs_, kv_, npool_, kc_, ks_, vc_, vs_,
-                                                         None), 50, 5)
+        tr = timer.run(lambda i: ssdq.kv_swap_out(kc_, ks_, vc_, vs_, ids_, nf_, nb_, bs_, kv_, npool_,
+                                                   slots_), 50, 5)
+        t, n = tr["t_median"], tr["steps"]
+        tr = timer.run(lambda i: ssdq.kv_swap_in(slots_, ids_, nb_, bs_, kv_, npool_, kc_, ks_, vc_, vs_,
+                                                  None), 50, 5)
+        ti, ni = tr["t_median"], tr["steps"]
         out[f"kv_swap_out_int8_1024x16x1024_to_{where}"] = {
             "GB/s": round(nb_ * sb_ / (t / n) / 1e9, 1), "us": round(t / n * 1e6, 2),
             "swap_in_GB/s": round(nb_ * sb_ / (ti / ni) / 1e9, 1), "swap_in_us": round(ti / ni * 1e6, 2),
@@ -341,8 +394,8 @@ def extras(torch, ssdq, synth, timer, np):
         for nm, N, K in layer:
             ssdq.gemm_q4k_bf16(W[nm], X[K], Y[nm], M, N, K)
 
-    t, _, _ = timer.run(layer_fused, 5, 1, graph=False)
-    t_sep, _, _ = timer.run(layer_separate, 5, 1, graph=False)
+    t = timer.run(layer_fused, 5, 1, graph=False)["t_median"]
+    t_sep = timer.run(layer_separate, 5, 1, graph=False)["t_median"]
     tfl = flops / (t / 5) / 1e12
     out["prefill_gemm_q4k_layer_m512"] = {"TFLOP/s": round(tfl, 2),
                                           "pct_bf16_peak": round(100 * tfl / BF16_PEAK_TFLOPS, 2),
@@ -357,7 +410,7 @@ def extras(torch, ssdq, synth, timer, np):
     xk = torch.randn(n_rows * dim, device="cuda")
     codes = torch.empty(n_rows * dim, dtype=torch.int8, device="cuda")
     scales = torch.empty(n_rows, device="cuda")
-    t, _, _ = timer.run(lambda i: ssdq.kv_quantize_rows(xk, codes, scales, n_rows, dim), 20, 3, graph=False)
+    t = timer.run(lambda i: ssdq.kv_quantize_rows(xk, codes, scales, n_rows, dim), 20, 3, graph=False)["t_median"]
     qbytes = n_rows * dim * 5 + n_rows * 4
     out["kv_int8_quantize_8x32768x2x1024"] = {"GB/s": round(qbytes / (t / 20) / 1e9, 1),
                                               "pct_hbm_peak": round(100 * qbytes / (t / 20) / 1e9 / HBM_PEAK_GBS, 2),
@@ -374,9 +427,9 @@ def extras(torch, ssdq, synth, timer, np):
     cl = torch.full((n_seq,), ctx, dtype=torch.int32, device="cuda")
     q = torch.randn(n_seq * n_head * hd, device="cuda")
     o = torch.empty_like(q)
-    t, _, _ = timer.run(lambda i: ssdq.paged_attention_int8(q, kc, ks, vc, vs, tables, cl, o, n_seq,
+    t = timer.run(lambda i: ssdq.paged_attention_int8(q, kc, ks, vc, vs, tables, cl, o, n_seq,
                                                             n_head, n_kv, hd, bs, mb, ctx), 50, 5,
-                        graph=False)
+                        graph=False)["t_median"]
     abytes = 536870912 + 2097152 + 131072 + 131072 + 65536
     step_s = t / 50
     out["paged_int8_decode_attention_32k"] = {
@@ -386,40 +439,139 @@ def extras(torch, ssdq, synth, timer, np):
     return out
 
 
-def cpu_baseline(np, synth, ssdq, gpu_sec_per_step):
-    """The CPU oracle (C restatement of matvec_q4_k_cpu, compute.rs:707-750) on this
-    host's cores: single thread like the reference, on a bounded sample."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import ssdq_oracle as o
-    out_dim, in_dim = 14336, 4096
-    w = synth.quant_weights(ssdq.Q4_K, out_dim, in_dim, synth.seed(3, 0))
-    x = synth.normal_f32(in_dim, 1)
-    nbytes = w.size + 4 * (in_dim + out_dim)
-    o.matvec(ssdq.Q4_K, w, x, out_dim, in_dim)  # warm-up
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _timed(fn, min_s):
+    """Seconds per call of fn() over calls adding up to at least min_s (after one warm-up call)."""
+    fn()
     reps, t0 = 0, time.perf_counter()
     while True:
-        o.matvec(ssdq.Q4_K, w, x, out_dim, in_dim)
+        fn()
         reps += 1
         el = time.perf_counter() - t0
-        if el > 10.0:
-            break
-    st = el / reps
-    res = {"value": round(nbytes / st / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-           "sample": f"{reps} single-thread Q4_K matvecs 14336x4096 in {el:.1f} s "
-                     f"({st * 1e3:.1f} ms each) on {os.cpu_count()} visible host cores",
-           "gpu_over_cpu": round(st / gpu_sec_per_step, 1)}
-    # all-cores variant (row shards, tensor_parallel.rs:45-96)
+        if el >= min_s:
+            return el / reps, reps
+
+
+def cpu_baseline(np, synth, ssdq, gpu_sec_per_step):
+    """The CPU oracle (the C restatement of the reference's functions) on this
+    host's cores, for every configuration: single thread like the reference
+    (every matvec_*_cpu and the INT8 quantizer are single-threaded), and all
+    cores (up to 16) with output rows, token rows or (sequence, head) pairs
+    sharded over threads as tensor_parallel.rs:45-96 shards rows.  Each figure is
+    the mean over calls adding up to ~1.5 s (single thread) or ~0.5 s (all
+    cores) on a bounded sample of the configuration's work, scaled to its unit."""
+    from concurrent.futures import ThreadPoolExecutor
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import ssdq_oracle as o
     nt = min(16, os.cpu_count() or 1)
-    o.matvec(ssdq.Q4_K, w, x, out_dim, in_dim, threads=nt)
-    reps2, t0 = 0, time.perf_counter()
-    while True:
-        o.matvec(ssdq.Q4_K, w, x, out_dim, in_dim, threads=nt)
-        reps2 += 1
-        el2 = time.perf_counter() - t0
-        if el2 > 5.0 or reps2 >= 500:
-            break
-    res["all_cores"] = {"value": round(nbytes / (el2 / reps2) / 1e9, 3), "unit": "GB/s", "cores": nt}
-    return res
+    pool = ThreadPoolExecutor(nt)
+    S1, SN = 1.5, 0.5
+    cfgs = {}
+
+    def mv_entry(name, dt, od, idim, batch, cfg, sample):
+        w = synth.quant_weights(dt, od, idim, synth.seed(cfg, 0))
+        x = synth.normal_f32((batch, idim), synth.seed(cfg, 1))
+        nbytes = w.size + 4 * batch * (idim + od)
+
+        def step(threads):
+            for b in range(batch):  # batch_scheduler.rs:242-276: one matvec per row
+                o.matvec(dt, w, x[b], od, idim, threads=threads)
+        t1, r1 = _timed(lambda: step(1), S1)
+        tn, rn = _timed(lambda: step(nt), SN)
+        cfgs[name] = {"unit": "GB/s", "1_thread": round(nbytes / t1 / 1e9, 3),
+                      f"{nt}_threads": round(nbytes / tn / 1e9, 3), "ms_per_step_1_thread": round(t1 * 1e3, 2),
+                      "sample": f"{r1} + {rn} {sample}"}
+        return t1, r1, nbytes
+
+    t_head, r_head, head_bytes = mv_entry("3_q4_k_matvec_14336x4096_b1", ssdq.Q4_K, 14336, 4096, 1, 3,
+                                          "whole Q4_K matvecs 14336x4096")
+    mv_entry("3_q6_k_matvec_4096x14336_b1", ssdq.Q6_K, 4096, 14336, 1, 3, "whole Q6_K matvecs 4096x14336")
+    mv_entry("1_q4_0_matvec_4096x4096_b1", ssdq.Q4_0, 4096, 4096, 1, 1, "whole Q4_0 matvecs 4096x4096")
+    for b in (1, 4, 8):
+        mv_entry(f"2_q8_0_matvec_11008x4096_b{b}", ssdq.Q8_0, 11008, 4096, b, 2,
+                 f"steps of {b} Q8_0 matvecs 11008x4096")
+
+    # config 4: per-token matvecs of the seven Q4_K matrices over widened bf16
+    # rows (transformer.rs:166-196); the sample is T tokens through the layer
+    layer = [(4096, 4096), (1024, 4096), (1024, 4096), (4096, 4096), (14336, 4096), (14336, 4096),
+             (4096, 14336)]
+    ws = [synth.quant_weights(ssdq.Q4_K, n, k, synth.seed(4, i)) for i, (n, k) in enumerate(layer)]
+    T1, TN = 1, 4 * nt
+    xs = {k: synth.f32_to_bf16_bits(synth.normal_f32((TN, k), synth.seed(4, 8 + (k > 4096)))) for k in (4096, 14336)}
+
+    def gemm_tokens(T, threads):
+        for w, (n, k) in zip(ws, layer):
+            o.gemm_q4k_bf16(w, xs[k][:T], T, n, k, threads=threads)
+    flop_tok = 2.0 * sum(n * k for n, k in layer)
+    t1, r1 = _timed(lambda: gemm_tokens(T1, 1), S1)
+    tn, rn = _timed(lambda: gemm_tokens(TN, nt), SN)
+    cfgs["4_prefill_q4k_layer_m512"] = {
+        "unit": "TFLOP/s", "1_thread": round(T1 * flop_tok / t1 / 1e12, 5),
+        f"{nt}_threads": round(TN * flop_tok / tn / 1e12, 5),
+        "ms_per_512_token_layer_1_thread": round(t1 / T1 * 512 * 1e3, 1),
+        "sample": f"{r1} x {T1} token(s) (1 thread) and {rn} x {TN} tokens ({nt} threads) through the seven "
+                  f"matrices; scaled to 512 tokens by token count"}
+    del ws, xs
+
+    # config 5a: INT8 row quantize (block_swap.rs:36-60), rows of 1024
+    dim, rows1 = 1024, 8192
+    kv = synth.normal_f32((rows1 * nt, dim), synth.seed(5, 0))
+    qb_row = 5 * dim + 4
+    t1, r1 = _timed(lambda: o.quantize_rows(kv[:rows1], rows1, dim), S1)
+
+    def quant_all():
+        list(pool.map(lambda i: o.quantize_rows(kv[i * rows1:(i + 1) * rows1], rows1, dim), range(nt)))
+    tn, rn = _timed(quant_all, SN)
+    cfgs["5a_kv_int8_quantize_rows_1024"] = {
+        "unit": "GB/s", "1_thread": round(rows1 * qb_row / t1 / 1e9, 3),
+        f"{nt}_threads": round(nt * rows1 * qb_row / tn / 1e9, 3),
+        "sample": f"{r1} x {rows1} rows (1 thread), {rn} x {nt * rows1} rows ({nt} threads) of the 524,288-row "
+                  f"config; GB/s by 5 B per element + 4 B per row"}
+    del kv
+
+    # config 5b: paged INT8 GQA decode attention at 32k context, one step of
+    # one sequence (32 heads) on one thread; all cores take the 8 sequences
+    n_head, n_kv, hd, bs, ctx = 32, 8, 128, 16, 32768
+    mb = ctx // bs
+    g = np.random.default_rng(5)
+    kc = g.integers(-127, 128, (mb * bs * n_kv * hd,), dtype=np.int8)
+    vc = g.integers(-127, 128, (mb * bs * n_kv * hd,), dtype=np.int8)
+    ks = g.uniform(0.005, 0.03, mb * bs).astype(np.float32)
+    vs = g.uniform(0.005, 0.03, mb * bs).astype(np.float32)
+    tab = synth.block_tables(1, mb, synth.seed(5, 3))
+    q = synth.normal_f32((n_head * hd,), synth.seed(5, 4))
+    cl = np.array([ctx], np.int32)
+
+    def attn_seq():
+        o.paged_attention_int8(q, kc, ks, vc, vs, tab, cl, 1, n_head, n_kv, hd, bs, mb)
+    t1, r1 = _timed(attn_seq, S1)
+
+    def attn_all():
+        list(pool.map(lambda i: attn_seq(), range(8)))
+    tn, rn = _timed(attn_all, SN)
+    step_bytes_seq = 536870912 // 8 + 2097152 // 8
+    cfgs["5b_paged_int8_decode_attention_32k"] = {
+        "unit": "tok/s", "1_thread": round(1.0 / t1, 3), f"{nt}_threads": round(8 / tn, 3),
+        "1_thread_GB/s": round(step_bytes_seq / t1 / 1e9, 3),
+        "sample": f"{r1} single-sequence steps (32 heads, 32768 tokens) on 1 thread: tok/s = 8 / (8 x the "
+                  f"sequence time); {rn} steps of all 8 sequences on {nt} threads"}
+    pool.shutdown()
+
+    return {"value": round(head_bytes / t_head / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{r_head} single-thread Q4_K matvecs 14336x4096 ({t_head * 1e3:.1f} ms each) on "
+                      f"{os.cpu_count()} visible host cores ({_cpu_model()})",
+            "gpu_over_cpu": round(t_head / gpu_sec_per_step, 1),
+            "cpu_model": _cpu_model(), "host_cores_visible": os.cpu_count(), "threads_all_cores": nt,
+            "configs": cfgs}
 
 
 if __name__ == "__main__":

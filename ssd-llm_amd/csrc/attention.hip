@@ -366,7 +366,7 @@ __global__ __launch_bounds__(64 * NWV, HD == 256 ? 1 : 8 / NWV) void paged_attn_
     badi |= __shfl_xor(badi, 32, 64);
     int e = 0;
     if (m > 0.f) (void)frexpf(m, &e);  // m < 2^e
-    const float up = ldexpf(1.0f, 22 - e);
+    const int sh = 22 - e;  // scales the values (2^(22 - e) itself overflows below 2^-105)
     const float qs_row = badi ? __builtin_nanf("") : ldexpf(1.0f, e - 22);
 #pragma unroll
     for (int mi = 0; mi < NMI; mi++) {
@@ -376,7 +376,7 @@ __global__ __launch_bounds__(64 * NWV, HD == 256 ? 1 : 8 / NWV) void paged_attn_
         uint32_t acc = 0;
 #pragma unroll
         for (int b = 0; b < 4; b++) {
-          const int qi = (int)rintf(qv[mi][4 * k + b] * up);       // |qi| <= 2^22
+          const int qi = (int)rintf(ldexpf(qv[mi][4 * k + b], sh));  // |qi| <= 2^22
           const uint32_t u = ((uint32_t)(qi + 0x808080)) ^ 0x808080u;  // balanced digits
           acc |= ((u >> (8 * (qj & 3))) & 0xFFu) << (8 * b);
         }

@@ -11,6 +11,7 @@
 #include <tuple>
 #include <mutex>
 #include <utility>
+#include <vector>
 
 #include "../../include/ssdq.h"
 #include "launch.hpp"
@@ -62,6 +63,10 @@ struct Workspace {
 // decode-layer paths, which call kernels that use slot 0.
 std::mutex g_ws_mu;
 std::map<std::tuple<int, void*, int>, Workspace> g_ws;
+// Buffers replaced by a larger one.  A HIP graph captured earlier on that
+// stream still holds their addresses, so they are never freed on growth: only
+// ssdq_release_workspaces() frees them (device, pointer).
+std::vector<std::pair<int, void*>> g_ws_retired;
 
 hipError_t workspace_get(size_t bytes, hipStream_t stream, void** out, int slot = 0) {
   int dev = 0;
@@ -71,19 +76,18 @@ hipError_t workspace_get(size_t bytes, hipStream_t stream, void** out, int slot 
   Workspace& w = g_ws[std::make_tuple(dev, (void*)stream, slot)];
   if (w.bytes < bytes) {
     // No allocation while the stream is being captured into a graph (it would
-    // invalidate the capture): run the call once on this stream beforehand.
+    // invalidate the capture): run the call once on this stream beforehand,
+    // or reserve with ssdq_reserve_workspace().
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (stream && hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
       return hipErrorStreamCaptureUnsupported;
-    if (w.ptr) {
-      e = hipStreamSynchronize(stream);
-      if (e != hipSuccess) return e;
-      (void)hipFree(w.ptr);
-      w.ptr = nullptr;
-      w.bytes = 0;
-    }
-    e = hipMalloc(&w.ptr, bytes);
+    void* p = nullptr;
+    e = hipMalloc(&p, bytes);
     if (e != hipSuccess) return e;
+    // work already queued on the stream keeps using the old buffer, and so
+    // does any graph captured with it: retire it, do not free it
+    if (w.ptr) g_ws_retired.emplace_back(dev, w.ptr);
+    w.ptr = p;
     w.bytes = bytes;
   }
   *out = w.ptr;
@@ -215,6 +219,34 @@ void ssdq_ctx_destroy(ssdq_ctx* c) {
 }
 
 int ssdq_ctx_device(const ssdq_ctx* c) { return c ? c->device : -1; }
+
+int ssdq_reserve_workspace(size_t bytes, ssdq_stream_t stream) {
+  void* p = nullptr;
+  hipError_t e = workspace_get(bytes ? bytes : 1, (hipStream_t)stream, &p);
+  if (e != hipSuccess) return hip_fail(e, "ssdq_reserve_workspace");
+  return ok();
+}
+
+int ssdq_release_workspaces(void) {
+  std::vector<std::pair<int, void*>> retired;
+  {
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    retired.swap(g_ws_retired);
+  }
+  int cur = 0;
+  if (hipGetDevice(&cur) != hipSuccess) cur = -1;
+  for (auto& r : retired) {
+    hipError_t e = hipSetDevice(r.first);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e == hipSuccess) e = hipFree(r.second);
+    if (e != hipSuccess) {
+      if (cur >= 0) (void)hipSetDevice(cur);
+      return hip_fail(e, "ssdq_release_workspaces");
+    }
+  }
+  if (cur >= 0) (void)hipSetDevice(cur);
+  return ok();
+}
 
 int ssdq_dequant_dev(int dtype, const void* w, size_t n_elements, float* out,
                      ssdq_stream_t stream) {

@@ -10,13 +10,18 @@
 //   P[t,n] = sum over the super-block of X[t,k] * (s*q)[n,k]
 //   Q[t,n] = sum over its 8 sub-blocks of XS[t,sb] * m[n,sb]
 //   Y[t,n] = sum over super-blocks of d*P - dmin*Q            (fp32 FMAs)
-// where XS is the sum of X over a sub-block.  X is bf16, exact in fp16; s*q is
-// an integer <= 945, exact in fp16; so every product inside P is exact and
+// where XS is the sum of X over a sub-block.  Each (row, super-block) of X is
+// first scaled by a power of two into fp16's range (undone on the fp32 result
+// of that super-block), where bf16 values are exact unless they lie more than
+// 2^26 below the super-block's largest magnitude; s*q is an integer <= 945,
+// exact in fp16; so every product inside P is exact and
 // v_mfma_f32_16x16x32_f16 only rounds the fp32 sums of one super-block (the
 // accumulators restart at every super-block).  XS is carried as an fp16
 // hi + lo pair (about 22 bits).  The result differs from the reference's serial
 // fp32 chain by rounding only (measured: closer to the exact sum than the
-// reference itself).
+// reference itself).  Rows whose range does not fit that window (or that hold
+// NaN / infinity, or values beyond 65504) are recomputed in the reference's own
+// fp32 order.
 //
 // A prep kernel writes X as fp16 in MFMA fragment order, plus XS: in a
 // super-block, MFMA step t (32 k values) gives lane group c (lanes
@@ -67,24 +72,67 @@ __global__ __launch_bounds__(256) void widen_bf16_kernel(const uint16_t* __restr
 // consecutive values of a row (coalesced), the tile is reordered in LDS, and
 // the 8 chunks of the super-block, contiguous in xp, are written as one 8 KB
 // run.
+//
+// Range: each (row, super-block) is scaled by a power of two 2^sh so that its
+// largest magnitude lies in [2^9, 2^10); the sub-block sums then stay below
+// 2^15 and every bf16 value at most 2^26 below that maximum is exact in fp16
+// (bf16 has 8 significant bits, fp16 keeps them down to 2^-17).  xe holds
+// 2^-sh per (m16, super-block, row), which the main kernel applies to the
+// super-block's fp32 result.  A (row, super-block) whose values lose more than
+// 2^-20 in total to the fp16 rounding (a range wider than the window), that
+// holds a value beyond fp16's largest finite 65504 (whose products are too
+// large for the fp32 partial sums to resolve the other terms to the
+// tolerance: the reference's own serial chain misses the exact sum there), or
+// that holds a NaN or an infinity, is flagged in fm (bit r of word (m16,
+// super-block)); the main kernel recomputes flagged rows in the reference's
+// order.
+constexpr float kLossLimit = 0x1p-20f;
+
 __global__ __launch_bounds__(512) void gemm_prep_x(const uint16_t* __restrict__ x, _Float16* __restrict__ xp,
-                                                   _Float16* __restrict__ xsp, int M, int K) {
+                                                   _Float16* __restrict__ xsp, float* __restrict__ xe,
+                                                   uint32_t* __restrict__ fm, int M, int K) {
   __shared__ h8 tile[512];
+  __shared__ uint32_t flags[8];
   const int blk = blockIdx.x, m16 = blockIdx.y, nblk = K / 256;
   const int r = threadIdx.x >> 5, p = threadIdx.x & 31;  // row in the tile, 8-value piece of the super-block
   const int sb = p >> 2, q = p & 3;
   const uint4 v = *reinterpret_cast<const uint4*>(x + (size_t)min(16 * m16 + r, M - 1) * K + (size_t)blk * 256 + 8 * p);
   const uint32_t d[4] = {v.x, v.y, v.z, v.w};
-  h8 h;
-  float sum = 0.f;
+  float a[8];
+  float mx = 0.f;
 #pragma unroll
   for (int i = 0; i < 4; i++) {
-    const float a = __uint_as_float(d[i] << 16), b = __uint_as_float(d[i] & 0xFFFF0000u);
-    h[2 * i] = (_Float16)a;
-    h[2 * i + 1] = (_Float16)b;
-    sum += a;
-    sum += b;
+    a[2 * i] = __uint_as_float(d[i] << 16);
+    a[2 * i + 1] = __uint_as_float(d[i] & 0xFFFF0000u);
   }
+  bool bad = false;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    mx = fmaxf(mx, fabsf(a[i]));
+    bad |= !(fabsf(a[i]) < INFINITY);
+  }
+  // the 32 threads of a row are one half of a wave
+#pragma unroll
+  for (int o = 1; o < 32; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  int e = 10;
+  if (mx > 0.f && mx < INFINITY) (void)frexpf(mx, &e);  // mx < 2^e
+  const int sh = 10 - e;
+  h8 h;
+  float sum = 0.f, lost = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const float xs = ldexpf(a[i], sh);  // exact: a power of two, no overflow (|xs| < 2^10)
+    const _Float16 hv = (_Float16)xs;
+    h[i] = hv;
+    lost += fabsf(ldexpf(xs - (float)hv, -sh));  // the difference is exact in fp32
+    sum += xs;
+  }
+#pragma unroll
+  for (int o = 1; o < 32; o <<= 1) {
+    lost += __shfl_xor(lost, o, 64);
+    bad |= __shfl_xor(bad ? 1 : 0, o, 64) != 0;
+  }
+  const bool flag = bad || mx > 65504.0f || !(lost <= kLossLimit);
   const int t = 4 * (sb >> 2) + q, c = sb & 3;
   tile[t * 64 + 16 * c + r] = h;
   // lanes 4i .. 4i+3 hold one sub-block; a + b is commutative, so all four
@@ -96,7 +144,19 @@ __global__ __launch_bounds__(512) void gemm_prep_x(const uint16_t* __restrict__ 
   _Float16* o = xsp + ((size_t)m16 * nblk + blk) * 256;
   if (q == 0) o[r * 8 + sb] = hi;
   if (q == 1) o[(16 + r) * 8 + sb] = lo;
+  const size_t chunk = (size_t)m16 * nblk + blk;
+  if (p == 0) xe[chunk * 16 + r] = ldexpf(1.0f, -sh);
+  // row flags of the tile: each wave holds two rows (lanes 0 and 32)
+  const uint64_t fb = __ballot(flag);
+  if ((threadIdx.x & 63) == 0)
+    flags[threadIdx.x >> 6] = (uint32_t)(fb & 1u) | ((uint32_t)((fb >> 32) & 1u) << 1);
   __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t m = 0;
+#pragma unroll
+    for (int w = 0; w < 8; w++) m |= flags[w] << (2 * w);
+    fm[chunk] = m;
+  }
   reinterpret_cast<h8*>(xp)[((size_t)m16 * (K / 32) + (size_t)blk * 8) * 64 + threadIdx.x] = tile[threadIdx.x];
 }
 
@@ -186,28 +246,95 @@ struct GemmMats {
 #define GEMM_WEIGHTS(sg) ((sg) == 0 ? w0 : (sg) == 1 ? w1 : w2)
 #define GEMM_OUT(sg) ((sg) == 0 ? y0 : (sg) == 1 ? y1 : y2)
 
+// Exact recomputation of one flagged row (see gemm_prep_x): every column of
+// the workgroup's tile gets the reference's serial fp32 sum over the super-blocks
+// b_begin .. b_end - 1 (all of K, or none: 0), in the order of
+// matvec_q4_k_cpu (compute.rs:707-750, elements of bf16 X widened as
+// streamer.rs:108-114 does): one thread per column, pairs of products added
+// before the running sum, no contraction.  The row's bf16 values pass through
+// LDS one super-block at a time (xs, 256 floats).  The result is the oracle's
+// bit for bit.
+template <bool MULTI>
+__device__ __noinline__ void gemm_exact_row(GEMM_MATS_PARAMS, const uint16_t* __restrict__ xraw,
+                                            float* __restrict__ part, float* xs, int row, int n0, int BN, int N,
+                                            int K, int M, int b_begin, int b_end, int nz) {
+#pragma clang fp contract(off)
+  const int tid = threadIdx.x;
+  const int n = n0 + tid;
+  const bool col = tid < BN && n < N;
+  const int sg = col ? GEMM_SEGMENT(n) : 0;
+  const size_t row_bytes = (size_t)(K / 256) * 144;
+  const uint8_t* wr = col ? GEMM_WEIGHTS(sg) + (size_t)(n - GEMM_FIRST(sg)) * row_bytes : nullptr;
+  float sum = 0.0f;
+  for (int b = b_begin; b < b_end; b++) {
+    __syncthreads();
+    if (tid < 256) xs[tid] = __uint_as_float((uint32_t)xraw[(size_t)row * K + (size_t)b * 256 + tid] << 16);
+    __syncthreads();
+    if (col) {
+      const uint8_t* blk = wr + (size_t)b * 144;
+      const float d = f16_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+      const float dmin = f16_to_f32((uint32_t)blk[2] | ((uint32_t)blk[3] << 8));
+      const uint8_t* sc = blk + 4;
+      const uint8_t* qs = blk + 16;
+      for (int sb = 0; sb < 8; sb++) {
+        uint32_t sv, mv;
+        if (sb < 4) {
+          sv = sc[sb] & 63u;
+          mv = sc[sb + 4] & 63u;
+        } else {
+          sv = (uint32_t)(sc[sb - 4] >> 6) | ((uint32_t)(sc[sb + 4] & 15) << 2);
+          mv = (uint32_t)(sc[sb] >> 6) | ((uint32_t)(sc[sb + 4] >> 4) << 2);
+        }
+        const float scale = d * (float)sv;
+        const float mn = dmin * (float)mv;
+        for (int j = 0; j < 16; j++) {
+          const uint32_t bv = qs[sb * 16 + j];
+          const float v0 = scale * (float)(bv & 15u) - mn;
+          const float v1 = scale * (float)(bv >> 4) - mn;
+          const float p0 = v0 * xs[sb * 32 + 2 * j];
+          const float p1 = v1 * xs[sb * 32 + 2 * j + 1];
+          sum = sum + (p0 + p1);
+        }
+      }
+    }
+  }
+  if (col && row < M) {
+    if (nz > 1)
+      part[(size_t)row * N + n] = sum;
+    else
+      GEMM_OUT(sg)[(size_t)row * (GEMM_FIRST(sg + 1) - GEMM_FIRST(sg)) + (n - GEMM_FIRST(sg))] = sum;
+  }
+}
+
 // Workgroup tile (16 MT) x (32 WAVES): each wave owns 32 columns and all
 // 16 MT rows.  K runs in stages of 4 MFMA steps (half a super-block); the X
-// chunks of a stage (MT per step) and the sub-block sums of a super-block are
-// loaded straight into LDS one stage ahead, double-buffered, and the weights
-// of a stage are loaded into registers one stage ahead, so one wait and one
-// barrier per stage cover every load.  The N columns are those of up to three
-// matrices that share X, concatenated (GemmMats).  blockIdx.z selects split z
-// of the K range (split = gridDim.z); with one split the results go to the
-// matrices' own outputs, otherwise split z writes its partial product of the
-// concatenated columns to part + z * M * N.
+// chunks of a stage (MT per step), the sub-block sums and the row scales of a
+// super-block are loaded straight into LDS one stage ahead, double-buffered,
+// and the weights of a stage are loaded into registers one stage ahead, so one
+// wait and one barrier per stage cover every load.  The N columns are those of
+// up to three matrices that share X, concatenated (GemmMats).  blockIdx.z
+// selects split z of the K range (split = gridDim.z); with one split the
+// results go to the matrices' own outputs, otherwise split z writes its partial
+// product of the concatenated columns to part + z * M * N.  Rows that the prep
+// kernel flagged (range wider than the fp16 window, or non-finite values) are
+// not stored from the matrix cores but recomputed by gemm_exact_row.
 template <int MT, int WAVES, bool MULTI>
 __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void gemm_q4k_mfma(GEMM_MATS_PARAMS,
                                                         const _Float16* __restrict__ xp,
                                                         const _Float16* __restrict__ xsp,
+                                                        const float* __restrict__ xe,
+                                                        const uint32_t* __restrict__ fm,
+                                                        const uint16_t* __restrict__ xraw,
                                                         float* __restrict__ part, int M, int N, int K) {
-  static_assert(MT == 8 && (WAVES == 4 || WAVES == 8), "the waves move the 8 X chunks of a step evenly");
+  static_assert(MT == 8 && WAVES == 8, "the waves move the 8 X chunks of a step evenly, wave 4 the row scales");
   constexpr int BM = 16 * MT, BN = 32 * WAVES;
   constexpr int XPW = MT / WAVES;  // X chunks each wave moves per step
   constexpr int CH = MT * 64;  // h8 slots of one step's X in LDS
   __shared__ __align__(16) h8 xa[4 * CH];  // stages 2b (first half of a super-block)
   __shared__ __align__(16) h8 xb[4 * CH];  // stages 2b + 1
   __shared__ __align__(16) h8 xsl[2][MT / 2 * 64];
+  __shared__ __align__(16) f4 xel[2][64];  // row scales 2^-sh of a super-block: [mt][16 rows] (first 512 B)
+  __shared__ uint32_t rowflags[MT];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int c = lane >> 4;  // lane group: k = 8c .. 8c+7 of each step
@@ -218,6 +345,12 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void gemm_q4k_mfma(GEMM_MATS
   part += (size_t)z * M * N;
   const size_t row_bytes = (size_t)nblk * 144;
   const int m16 = m0 >> 4, M16 = (M + 15) >> 4;
+
+  // flag words of this wave's row tile (m16 + wave) over all super-blocks of
+  // K (every split must agree on the flagged rows), requested first and
+  // reduced after the main loop
+  const size_t fbase = (size_t)min(m16 + wave, M16 - 1) * nblk;
+  uint32_t fw0 = fm[fbase + min(lane, nblk - 1)], fw1 = fm[fbase + min(lane + 64, nblk - 1)];
 
   // weight rows of this lane's B fragments (clamped; columns past N are not stored)
   const uint8_t* wrow[NT];
@@ -230,11 +363,14 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void gemm_q4k_mfma(GEMM_MATS
   // this wave moves X chunks XPW wave .. XPW wave + XPW - 1 of every step
   // (row tiles past the padded M are clamped: their rows are never stored);
   // waves 0-3 move the sum chunks of a super-block, wave w chunks 2 w (lanes
-  // 0-31) and 2 w + 1 (lanes 32-63)
+  // 0-31) and 2 w + 1 (lanes 32-63); wave 4 moves the row scales (lane l:
+  // tile (l / 4) % 8, rows 4 (l % 4) .. +3; lanes 32-63 repeat lanes 0-31 into
+  // the unused second half of the buffer)
   const _Float16* xsrc[XPW];
 #pragma unroll
   for (int i = 0; i < XPW; i++) xsrc[i] = xp + (size_t)min(m16 + XPW * wave + i, M16 - 1) * S * 512 + lane * 8;
   const _Float16* ssrc = xsp + (size_t)min(m16 + 2 * (wave & 3) + (lane >> 5), M16 - 1) * nblk * 256 + (lane & 31) * 8;
+  const float* esrc = xe + (size_t)min(m16 + ((lane >> 2) & 7), M16 - 1) * nblk * 16 + (lane & 3) * 4;
   const uint32_t lds_a = lds_offset(xa) + wave * XPW * 1024, lds_b = lds_offset(xb) + wave * XPW * 1024;
   auto stage_x = [&](int g, uint32_t base) {
 #pragma unroll
@@ -245,8 +381,11 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void gemm_q4k_mfma(GEMM_MATS
     }
   };
   auto stage_sums = [&](int b) {
+    const int bb = b_begin + min(b, nb - 1);
     if (wave < 4)
-      dma16(ssrc + (size_t)(b_begin + min(b, nb - 1)) * 256, lds_offset(&xsl[b & 1][0]) + wave * 1024);
+      dma16(ssrc + (size_t)bb * 256, lds_offset(&xsl[b & 1][0]) + wave * 1024);
+    else if (wave == 4)
+      dma16(esrc + (size_t)bb * 16, lds_offset(&xel[b & 1][0]));
   };
 
   // Weights of super-block b: the header (d|dmin, scale bytes 0-3, 4-7, 8-11)
@@ -355,13 +494,14 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void gemm_q4k_mfma(GEMM_MATS
     for (int mt = 0; mt < MT; mt++) {
       const h8 raw = sums[(mt >> 1) * 64 + (mt & 1) * 32 + (lane & 31)];
       const h8 amin = lane < 32 ? raw : h8{};
+      const f4 rs = xel[b & 1][mt * 4 + c];  // 2^-sh of rows 4c .. 4c+3
 #pragma unroll
       for (int j = 0; j < NT; j++) {
         const f4 qm = __builtin_amdgcn_mfma_f32_16x16x32_f16(amin, bmin[j], f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          tot[mt][j][i] = __builtin_fmaf(dd[j], acc[mt][j][i], tot[mt][j][i]);
-          tot[mt][j][i] = __builtin_fmaf(-dm[j], qm[i], tot[mt][j][i]);
+          const float v = __builtin_fmaf(dd[j], acc[mt][j][i], -dm[j] * qm[i]);
+          tot[mt][j][i] = __builtin_fmaf(v, rs[i], tot[mt][j][i]);
         }
       }
     }
@@ -369,9 +509,21 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void gemm_q4k_mfma(GEMM_MATS
   // the last stage's loads (clamped repeats) land before the workgroup's LDS is released
   __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
 
+  // flagged rows of this wave's tile (words past the first 128 super-blocks
+  // are read here)
+  {
+    uint32_t f = (lane < nblk ? fw0 : 0u) | (lane + 64 < nblk ? fw1 : 0u);
+    for (int l = lane + 128; l < nblk; l += 64) f |= fm[fbase + l];
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) f |= __shfl_xor(f, o, 64);
+    if (lane == 0) rowflags[wave] = m16 + wave < M16 ? f : 0u;
+  }
+  __syncthreads();
+
   // C fragment layout: element i of acc[mt][j] is row 4*(lane/16)+i, column lane%16
 #pragma unroll
-  for (int mt = 0; mt < MT; mt++)
+  for (int mt = 0; mt < MT; mt++) {
+    const uint32_t rf = rowflags[mt];
 #pragma unroll
     for (int j = 0; j < NT; j++) {
       const int n = n0 + 32 * wave + 16 * j + (lane & 15);
@@ -383,9 +535,25 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void gemm_q4k_mfma(GEMM_MATS
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int m = m0 + mt * 16 + 4 * c + i;
-        if (m < M) dst[(size_t)m * ld] = tot[mt][j][i];
+        if (m < M && !((rf >> (4 * c + i)) & 1u)) dst[(size_t)m * ld] = tot[mt][j][i];
       }
     }
+  }
+  // exact path for flagged rows (uniform over the workgroup: the flags are in
+  // LDS).  Split 0 computes the whole K range in the reference's order and the
+  // other splits contribute exact zeros, so the split-K sum is that serial
+  // chain itself.
+  const int exact_end = z == 0 ? nblk : 0;
+  for (int mt = 0; mt < MT; mt++) {
+    uint32_t rf = rowflags[mt];
+    while (rf) {
+      const int r = __builtin_ctz(rf);
+      rf &= rf - 1;
+      if (m0 + 16 * mt + r >= M) break;  // padding rows (copies of row M - 1) and beyond
+      gemm_exact_row<MULTI>(w0, w1, w2, y0, y1, y2, start1, start2, xraw, part,
+                            reinterpret_cast<float*>(xa), m0 + 16 * mt + r, n0, BN, N, K, M, 0, exact_end, nz);
+    }
+  }
 }
 
 // Sums split-K partials (M x N, concatenated columns) in a fixed order
@@ -468,10 +636,20 @@ int gemm_split(size_t M, size_t N, size_t K) {
 }
 
 // workspace layout: X in fragment order (M16*K fp16, M16 = M rounded up to
-// 16) | sub-block sums (M16*K/256*16 fp16) | split partials (split*M*N f32)
-size_t prep_bytes(size_t M, size_t K) {
+// 16) | sub-block sums (M16*K/256*16 fp16) | row scales (M16*K/256 f32) |
+// row-flag words (M16/16*K/256 u32, padded to 16 bytes) | split partials
+// (split*M*N f32)
+size_t prep_xe_offset(size_t M, size_t K) {
   const size_t M16 = (M + 15) / 16 * 16;
   return M16 * K * 2 + M16 * (K / 256) * 32;
+}
+size_t prep_fm_offset(size_t M, size_t K) {
+  const size_t M16 = (M + 15) / 16 * 16;
+  return prep_xe_offset(M, K) + M16 * (K / 256) * 4;
+}
+size_t prep_bytes(size_t M, size_t K) {
+  const size_t M16 = (M + 15) / 16 * 16;
+  return prep_fm_offset(M, K) + ((M16 / 16) * (K / 256) * 4 + 15) / 16 * 16;
 }
 
 }  // namespace
@@ -516,12 +694,15 @@ hipError_t launch_gemm_q4k(const uint8_t* const* w, const size_t* n, int count, 
     const int split = gemm_split(M, N, K);
     const size_t need = prep_bytes(M, K) + (split > 1 ? (size_t)split * M * N * sizeof(float) : 0);
     if (workspace_bytes < need) return hipErrorInvalidValue;
-    _Float16* xp = static_cast<_Float16*>(workspace);
+    uint8_t* wsb = static_cast<uint8_t*>(workspace);
+    _Float16* xp = reinterpret_cast<_Float16*>(wsb);
     _Float16* xsp = xp + (M + 15) / 16 * 16 * K;
-    float* part = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + prep_bytes(M, K));
+    float* xe = reinterpret_cast<float*>(wsb + prep_xe_offset(M, K));
+    uint32_t* fm = reinterpret_cast<uint32_t*>(wsb + prep_fm_offset(M, K));
+    float* part = reinterpret_cast<float*>(wsb + prep_bytes(M, K));
     const dim3 pgrid((unsigned)(K / 256), (unsigned)((M + 15) / 16));
     if (pgrid.y > 65535) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(gemm_prep_x, pgrid, dim3(512), 0, s, x, xp, xsp, (int)M, (int)K);
+    hipLaunchKernelGGL(gemm_prep_x, pgrid, dim3(512), 0, s, x, xp, xsp, xe, fm, (int)M, (int)K);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int bm = 16 * kMT;
@@ -529,10 +710,10 @@ hipError_t launch_gemm_q4k(const uint8_t* const* w, const size_t* n, int count, 
     if (grid.y > 65535) return hipErrorInvalidValue;
     if (count > 1)
       hipLaunchKernelGGL((gemm_q4k_mfma<kMT, kWaves, true>), grid, dim3(64 * kWaves), 0, s, GEMM_MATS_ARGS(mats), xp,
-                         xsp, part, (int)M, (int)N, (int)K);
+                         xsp, xe, fm, x, part, (int)M, (int)N, (int)K);
     else
       hipLaunchKernelGGL((gemm_q4k_mfma<kMT, kWaves, false>), grid, dim3(64 * kWaves), 0, s, GEMM_MATS_ARGS(mats), xp,
-                         xsp, part, (int)M, (int)N, (int)K);
+                         xsp, xe, fm, x, part, (int)M, (int)N, (int)K);
     e = hipGetLastError();
     if (e != hipSuccess || split == 1) return e;
     const bool vec = count == 1 && (M * N) % 4 == 0 && ((uintptr_t)y[0] & 15) == 0;

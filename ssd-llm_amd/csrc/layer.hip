@@ -36,10 +36,11 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g
 // 8 elements per thread are kept in registers with their norm weights, so x,
 // the residual and w are all requested before the reduction (one memory round
 // trip); longer vectors take a second pass.
-__global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ res,
+// x, res, hidden_out and out are not __restrict__: out and hidden_out may
+// alias x (the in-place post-attention form).
+__global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* x, const float* res,
                                                        const float* __restrict__ w, float eps,
-                                                       float* __restrict__ hidden_out, float* __restrict__ out,
-                                                       int n) {
+                                                       float* hidden_out, float* out, int n) {
   __shared__ float part[16];
   constexpr int KEEP = 8;
   float hv[KEEP], wv[KEEP];

@@ -408,11 +408,13 @@ __device__ __forceinline__ void stage_store(const XChunks<SIT>& st, int keff, ui
     const int k = c & 3;
     int e = 0;
     if (m > 0.f) (void)frexpf(m, &e);  // m < 2^e
-    const float up = ldexpf(1.0f, 22 - e);
+    // the value is scaled, not multiplied by 2^(22 - e): that factor overflows
+    // for groups whose largest magnitude is below 2^-105
+    const int sh = 22 - e;
     uint32_t u[8];
 #pragma unroll
     for (int j = 0; j < 8; j++) {
-      const int xi = (int)rintf(v[j] * up);           // |xi| <= 2^22
+      const int xi = (int)rintf(ldexpf(v[j], sh));     // |xi| <= 2^22
       u[j] = ((uint32_t)(xi + 0x808080)) ^ 0x808080u;  // bytes 0-2: balanced digits
     }
     bool gbad = bad;
@@ -522,7 +524,7 @@ __device__ __forceinline__ void accumulate_dig(const uint32_t* raw, int u, PL pl
       const float f = digits_value(i0, i1, i2);
       const float xscale = __uint_as_float(pl(h * D::GW + 24));
       const float xsum = __uint_as_float(pl(h * D::GW + 25));
-      acc = fmaf(sc[h] * xscale, f, fmaf(-off[h], xsum, acc));
+      acc = fmaf(sc[h], f * xscale, fmaf(-off[h], xsum, acc));
     }
   } else if constexpr (F == kQ8_0) {
 #pragma unroll
@@ -538,7 +540,7 @@ __device__ __forceinline__ void accumulate_dig(const uint32_t* raw, int u, PL pl
         i2 = dot4(wd, pl(b + 2), i2);
       }
       const float xscale = __uint_as_float(pl(h * D::GW + 24));
-      acc = fmaf(d * xscale, digits_value(i0, i1, i2), acc);
+      acc = fmaf(d, digits_value(i0, i1, i2) * xscale, acc);
     }
   } else if constexpr (F == kQ8_K) {
     const float d = __uint_as_float(raw[0]);
@@ -554,7 +556,7 @@ __device__ __forceinline__ void accumulate_dig(const uint32_t* raw, int u, PL pl
         i2 = dot4(wd, pl(b + 2), i2);
       }
       const float xscale = __uint_as_float(pl(h * D::GW + 24));
-      acc = fmaf(d * xscale, digits_value(i0, i1, i2), acc);
+      acc = fmaf(d, digits_value(i0, i1, i2) * xscale, acc);
     }
   } else if constexpr (F == kQ2_K) {
     // 16 sub-blocks of 16 elements; scale / min = low / high nibble of the
@@ -578,7 +580,7 @@ __device__ __forceinline__ void accumulate_dig(const uint32_t* raw, int u, PL pl
         }
         const float S = d * (float)(scb & 15u), Mn = dmin * (float)(scb >> 4);
         const float xsum = __uint_as_float(pl(h * D::GW + 25 + sb));
-        acc = fmaf(S * xscale, digits_value(i0, i1, i2), fmaf(-Mn, xsum, acc));
+        acc = fmaf(S, digits_value(i0, i1, i2) * xscale, fmaf(-Mn, xsum, acc));
       }
     }
   } else if constexpr (F == kQ3_K) {
@@ -619,7 +621,7 @@ __device__ __forceinline__ void accumulate_dig(const uint32_t* raw, int u, PL pl
         const int sv = (int)((lo4 | (hi2 << 4)) ^ 32u) - 32;  // sign-extended 6 bits
         const float S = d * (float)sv;
         const float xsum = __uint_as_float(pl(h * D::GW + 25 + sb));
-        acc = fmaf(S * xscale, digits_value(i0, i1, i2), fmaf(-4.0f * S, xsum, acc));
+        acc = fmaf(S, digits_value(i0, i1, i2) * xscale, fmaf(-4.0f * S, xsum, acc));
       }
     }
   } else {  // kQ6_K quarter: 6-bit codes + 32 as bytes, two 16-element scale groups
@@ -653,7 +655,7 @@ __device__ __forceinline__ void accumulate_dig(const uint32_t* raw, int u, PL pl
       }
       const float sg = d * (float)(int8_t)((raw[8] >> (8 * h)) & 0xFFu);
       const float xsum = __uint_as_float(pl(25 + h));
-      acc = fmaf(sg * xscale, digits_value(i0, i1, i2), fmaf(-32.0f * sg, xsum, acc));
+      acc = fmaf(sg, digits_value(i0, i1, i2) * xscale, fmaf(-32.0f * sg, xsum, acc));
     }
   }
 }

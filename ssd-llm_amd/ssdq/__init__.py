@@ -49,6 +49,8 @@ SIGNATURES = {
     "ssdq_ctx_create": (_i, [_i, _c.POINTER(_vp)]),
     "ssdq_ctx_destroy": (None, [_vp]),
     "ssdq_ctx_device": (_i, [_vp]),
+    "ssdq_reserve_workspace": (_i, [_sz, _vp]),
+    "ssdq_release_workspaces": (_i, []),
     "ssdq_dequant_dev": (_i, [_i, _vp, _sz, _vp, _vp]),
     "ssdq_matvec_dev": (_i, [_i, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     "ssdq_matvec_generic_dev": (_i, [_i, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
@@ -129,6 +131,14 @@ def _stream(stream=None):
     import torch
     s = stream if stream is not None else torch.cuda.current_stream()
     return ctypes.c_void_p(s.cuda_stream)
+
+
+def reserve_workspace(nbytes, stream=None):
+    return check("ssdq_reserve_workspace", lib().ssdq_reserve_workspace(nbytes, _stream(stream)))
+
+
+def release_workspaces():
+    return check("ssdq_release_workspaces", lib().ssdq_release_workspaces())
 
 
 def dequant(dtype, w, n_elements, out, stream=None):

@@ -27,3 +27,23 @@ def pytest_collection_modifyitems(config, items):
         for item in items:
             if item.get_closest_marker("gpu"):
                 item.add_marker(skip)
+
+
+def pytest_terminal_summary(terminalreporter, exitstatus, config):
+    """Prints how many outputs each tolerance check took against the exact sum
+    instead of the reference's serial fp32 value (helpers.assert_close_attributed)."""
+    try:
+        from helpers import SUBSTITUTIONS
+    except ImportError:
+        return
+    if not SUBSTITUTIONS:
+        return
+    tr = terminalreporter
+    tr.section("exact-sum substitutions (outputs outside tolerance of the fp32 reference)")
+    total = sum(n for _, _, n, _ in SUBSTITUTIONS)
+    outputs = sum(m for _, _, _, m in SUBSTITUTIONS)
+    for test, what, n, m in SUBSTITUTIONS:
+        if n:
+            tr.write_line(f"{n:6d} of {m:9d}  {test} [{what}]")
+    tr.write_line(f"total: {total} of {outputs} outputs in {len(SUBSTITUTIONS)} checks "
+                  f"({sum(1 for s in SUBSTITUTIONS if s[2])} checks used any)")

@@ -1,5 +1,11 @@
 """Shared checks for the parity tests."""
+import os
+
 import numpy as np
+
+# (test id, what, substituted outputs, outputs) of every assert_close_attributed
+# call in this process; tests/conftest.py prints them in the terminal summary.
+SUBSTITUTIONS = []
 
 # Tolerance stated for fp32 outputs of matvec, GEMM and attention:
 # |gpu - ref| <= ATOL + RTOL * |ref|
@@ -49,6 +55,8 @@ def assert_close_attributed(gpu, ref32, exact, what="", max_ill_frac=1e-3):
             f"{what}: {int((~good).sum())} of {gpu.size} outside tolerance; first idx {i}: "
             f"gpu={gpu[i]!r} ref32={ref32[i]!r} exact={exact[i]!r}")
     n_sub = int((~ok_ref).sum())
+    test = os.environ.get("PYTEST_CURRENT_TEST", "?").split(" ")[0]
+    SUBSTITUTIONS.append((test, what, n_sub, int(gpu.size)))
     assert n_sub <= max(1, max_ill_frac * gpu.size), f"{what}: {n_sub} ill-conditioned substitutions"
     return n_sub
 

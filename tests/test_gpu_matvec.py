@@ -170,37 +170,49 @@ def test_repeat_is_deterministic():
 def test_extreme_and_nonfinite_activations(dtype, batch):
     # row 0 normal; row 1 with one NaN (the reference's serial sum is NaN for
     # every output); row 2 with a whole 32-element block scaled by 1e30 and a
-    # 1e3 outlier in another block; row 3 scaled to ~1e-30.  Batch 1 takes
-    # the rows one call at a time.  (x is carried relative to the largest
-    # value of its 32-element block, so values more than ~7 orders below it
-    # are not: the outlier stays within that range.)
+    # 1e3 outlier in another block; row 3 scaled to ~1e-30; row 4 scaled to
+    # ~1e-35 (32-element groups whose largest value is below 2^-105, where
+    # 2^(22 - e) as a factor would overflow).  Batch 1 takes the rows one call
+    # at a time, batch 4 runs rows 0-3 as one batch and row 4 alone.  (x is
+    # carried relative to the largest value of its 32-element block, so values
+    # more than ~7 orders below it are not: the outlier stays within that
+    # range.)
     out_dim, in_dim = 300, 4096
     w = synth.quant_weights(dtype, out_dim, in_dim, 71)
-    x = synth.normal_f32((4, in_dim), 72)
+    x = synth.normal_f32((5, in_dim), 72)
     x[1, 1000] = np.nan
     x[2, 64:96] *= np.float32(1e30)
     x[2, 200] = np.float32(1e3)
     x[3] *= np.float32(1e-30)
+    x[4] *= np.float32(1e-35)
+    assert np.abs(x[4]).max() < 2.0 ** -105
     announce("matvec extreme activations", ssdq.TYPE_NAMES[dtype], batch)
     if batch == 4:
-        y, rc = run(dtype, w, x, out_dim, in_dim, 4)
+        y, rc = run(dtype, w, x[:4], out_dim, in_dim, 4)
         assert rc == 0
-        y = y.reshape(4, out_dim)
+        y4, rc = run(dtype, w, x[4], out_dim, in_dim, 1)
+        assert rc == 0
+        y = np.concatenate([y.reshape(4, out_dim), y4.reshape(1, out_dim)])
     else:
         rows = []
-        for b in range(4):
+        for b in range(5):
             yb, rc = run(dtype, w, x[b], out_dim, in_dim, 1)
             assert rc == 0
             rows.append(yb)
         y = np.stack(rows)
-    ref, exact = reference(dtype, w, x, out_dim, in_dim, 4)
-    ref, exact = ref.reshape(4, out_dim), exact.reshape(4, out_dim)
+    ref, exact = reference(dtype, w, x, out_dim, in_dim, 5)
+    ref, exact = ref.reshape(5, out_dim), exact.reshape(5, out_dim)
     assert np.all(np.isnan(ref[1])) and np.all(np.isnan(y[1]))
     for b in (0, 2):
         assert_close_attributed(y[b], ref[b], exact[b], f"row {b}")
-    # row 3: relative agreement (the absolute 1e-4 term says nothing at 1e-30)
-    scale = np.abs(exact[3]).max()
-    assert np.all(np.abs(y[3] - exact[3]) <= 1e-3 * scale)
+    # rows 3, 4: relative agreement (the absolute 1e-4 term says nothing at
+    # these magnitudes); the exact sums are double precision, so they hold the
+    # 1e-35-scaled outputs (~1e-33, fp32 subnormal) without underflow
+    for b in (3, 4):
+        assert np.all(np.isfinite(y[b])), f"row {b}: non-finite output"
+        scale = np.abs(exact[b]).max()
+        assert scale > 0
+        assert np.all(np.abs(y[b] - exact[b]) <= 1e-3 * scale), f"row {b}"
 
 
 LONG_ROWS = [  # batch-1 rows of 129-256 units (K slices summed in slice order)

@@ -273,6 +273,23 @@ int ssdq_paged_attention_int8_dev(const float* q, const int8_t* k_codes, const f
                                   float* out, size_t n_seq, size_t n_head, size_t n_head_kv,
                                   size_t head_dim, size_t block_size, size_t max_blocks_per_seq,
                                   size_t max_ctx, ssdq_stream_t stream);
+/* The same paged INT8 decode attention, allocating nothing: no counterpart in
+ * the reference. It is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Arguments, kernels and results are those of
+ * ssdq_paged_attention_int8_dev; the split partials live in a static device
+ * array of 16 MiB that each GPU the library runs on holds until the process
+ * ends. A call whose partials need more (n_seq * n_head * splits *
+ * (head_dim + 2) * 4 bytes; config 5, 8 x 32 heads at 32k context, needs
+ * 4.3 MB) fails with SSDQ_ERR_INVALID_ARG and launches nothing. All calls on
+ * one GPU share that array: calls that overlap in time on one GPU (different
+ * streams, or host threads) race and must be serialized by the caller. */
+int ssdq_paged_attention_int8_noalloc_dev(const float* q, const int8_t* k_codes, const float* k_scales,
+                                          const int8_t* v_codes, const float* v_scales,
+                                          const int32_t* block_tables, const int32_t* ctx_lens, float* out,
+                                          size_t n_seq, size_t n_head, size_t n_head_kv, size_t head_dim,
+                                          size_t block_size, size_t max_blocks_per_seq, size_t max_ctx,
+                                          ssdq_stream_t stream);
 /* MetalCompute::flash_attention_f32 (compute.rs:217-258) / MetalGpu::
  * flash_attention_f32 (gpu.rs:547-599): q [n_head, head_dim], k/v flattened
  * [seq_len, n_head_kv, head_dim] f32, positions [window_start,

@@ -19,6 +19,7 @@
 // unnormalised acc[head_dim]; every K/V byte of the split is read once for all
 // G heads.  Pass 2 merges the splits with the usual log-sum-exp rescaling.
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "common.hpp"
@@ -718,6 +719,50 @@ hipError_t launch_paged_attn(const PagedAttnArgs& a, void* workspace, hipStream_
     default:
       return hipErrorInvalidValue;
   }
+}
+
+// Scratch of the allocation-free entry point (ssdq_paged_attention_int8_noalloc_dev):
+// the split partials of paged attention live in this file-scope device array,
+// which every GPU the library runs on holds until the process ends.  Host code
+// never passes the array's name to a kernel (on the host it is only a stand-in
+// for the symbol): it uses the device address hipGetSymbolAddress returns for
+// the current device, looked up once per device.
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+hipError_t scratch_address(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return hipSuccess;
+}
+}  // namespace
+
+hipError_t launch_paged_attn_noalloc(const PagedAttnArgs& a, hipStream_t s, size_t* need) {
+  const size_t bytes = paged_attn_workspace_bytes(a, nullptr);
+  if (need) *need = bytes;
+  if (bytes > kNoAllocScratchBytes) return hipErrorInvalidValue;
+  void* p = nullptr;
+  hipError_t e = scratch_address(&p);
+  if (e != hipSuccess) return e;
+  // every (sequence, head, split) record the combine reads is written by the
+  // split kernel of the same call (empty splits write m = -inf, l = 0): the
+  // scratch needs no clearing
+  return launch_paged_attn(a, p, s);
 }
 
 size_t flash_attn_f32_workspace_bytes(int n_head, int n_head_kv, int head_dim, int len,

@@ -623,14 +623,13 @@ int ssdq_paged_kv_append_dev(const float* k, const float* v, const int32_t* slot
 
 static bool head_dim_ok(size_t hd) { return hd == 64 || hd == 128 || hd == 256; }
 
-int ssdq_paged_attention_int8_dev(const float* q, const int8_t* k_codes, const float* k_scales,
-                                  const int8_t* v_codes, const float* v_scales,
-                                  const int32_t* block_tables, const int32_t* ctx_lens,
-                                  float* out, size_t n_seq, size_t n_head, size_t n_head_kv,
-                                  size_t head_dim, size_t block_size, size_t max_blocks_per_seq,
-                                  size_t max_ctx, ssdq_stream_t stream) {
-  const char* fn = "ssdq_paged_attention_int8_dev";
-  if (n_seq == 0 || n_head == 0) return ok();
+// Argument checks shared by the paged-attention entry points; 0 with *a filled
+// in, or the failure status.
+static int paged_attention_args(const char* fn, const float* q, const int8_t* k_codes, const float* k_scales,
+                                const int8_t* v_codes, const float* v_scales, const int32_t* block_tables,
+                                const int32_t* ctx_lens, float* out, size_t n_seq, size_t n_head,
+                                size_t n_head_kv, size_t head_dim, size_t block_size,
+                                size_t max_blocks_per_seq, size_t max_ctx, ssdq::PagedAttnArgs* a) {
   if (!q || !k_codes || !k_scales || !v_codes || !v_scales || !block_tables || !ctx_lens || !out)
     return fail(SSDQ_ERR_INVALID_ARG, "%s: NULL pointer", fn);
   if (!head_dim_ok(head_dim)) return fail(SSDQ_ERR_UNSUPPORTED, "%s: head_dim %zu not in {64,128,256}", fn, head_dim);
@@ -643,15 +642,51 @@ int ssdq_paged_attention_int8_dev(const float* q, const int8_t* k_codes, const f
   if (!fits_int(n_seq) || n_seq > 65535 || n_head_kv > 65535 || !fits_int(max_ctx) ||
       !fits_int(n_seq * max_blocks_per_seq))
     return fail(SSDQ_ERR_INVALID_ARG, "%s: dimensions too large", fn);
-  ssdq::PagedAttnArgs a{q, k_codes, k_scales, v_codes, v_scales, block_tables, ctx_lens, out,
-                        (int)n_seq, (int)n_head, (int)n_head_kv, (int)head_dim, (int)block_size,
-                        (int)max_blocks_per_seq, (int)(max_ctx ? max_ctx : 1)};
+  *a = ssdq::PagedAttnArgs{q, k_codes, k_scales, v_codes, v_scales, block_tables, ctx_lens, out,
+                           (int)n_seq, (int)n_head, (int)n_head_kv, (int)head_dim, (int)block_size,
+                           (int)max_blocks_per_seq, (int)(max_ctx ? max_ctx : 1)};
+  return SSDQ_OK;
+}
+
+int ssdq_paged_attention_int8_dev(const float* q, const int8_t* k_codes, const float* k_scales,
+                                  const int8_t* v_codes, const float* v_scales,
+                                  const int32_t* block_tables, const int32_t* ctx_lens,
+                                  float* out, size_t n_seq, size_t n_head, size_t n_head_kv,
+                                  size_t head_dim, size_t block_size, size_t max_blocks_per_seq,
+                                  size_t max_ctx, ssdq_stream_t stream) {
+  const char* fn = "ssdq_paged_attention_int8_dev";
+  if (n_seq == 0 || n_head == 0) return ok();
+  ssdq::PagedAttnArgs a;
+  int rc = paged_attention_args(fn, q, k_codes, k_scales, v_codes, v_scales, block_tables, ctx_lens, out, n_seq,
+                                n_head, n_head_kv, head_dim, block_size, max_blocks_per_seq, max_ctx, &a);
+  if (rc != SSDQ_OK) return rc;
   hipStream_t s = (hipStream_t)stream;
   const size_t wsb = ssdq::paged_attn_workspace_bytes(a, nullptr);
   void* ws = nullptr;
   hipError_t e = workspace_get(wsb, s, &ws);
   if (e != hipSuccess) return hip_fail(e, "ssdq_paged_attention_int8_dev: workspace");
   e = ssdq::launch_paged_attn(a, ws, s);
+  if (e != hipSuccess) return hip_fail(e, fn);
+  return ok();
+}
+
+int ssdq_paged_attention_int8_noalloc_dev(const float* q, const int8_t* k_codes, const float* k_scales,
+                                          const int8_t* v_codes, const float* v_scales,
+                                          const int32_t* block_tables, const int32_t* ctx_lens, float* out,
+                                          size_t n_seq, size_t n_head, size_t n_head_kv, size_t head_dim,
+                                          size_t block_size, size_t max_blocks_per_seq, size_t max_ctx,
+                                          ssdq_stream_t stream) {
+  const char* fn = "ssdq_paged_attention_int8_noalloc_dev";
+  if (n_seq == 0 || n_head == 0) return ok();
+  ssdq::PagedAttnArgs a;
+  int rc = paged_attention_args(fn, q, k_codes, k_scales, v_codes, v_scales, block_tables, ctx_lens, out, n_seq,
+                                n_head, n_head_kv, head_dim, block_size, max_blocks_per_seq, max_ctx, &a);
+  if (rc != SSDQ_OK) return rc;
+  size_t need = 0;
+  hipError_t e = ssdq::launch_paged_attn_noalloc(a, (hipStream_t)stream, &need);
+  if (need > ssdq::kNoAllocScratchBytes)
+    return fail(SSDQ_ERR_INVALID_ARG, "%s: the call needs %zu bytes of scratch, the static maximum is %zu", fn,
+                need, ssdq::kNoAllocScratchBytes);
   if (e != hipSuccess) return hip_fail(e, fn);
   return ok();
 }

@@ -116,6 +116,11 @@ struct PagedAttnArgs {
 // Bytes of device workspace the split-KV attention needs for these shapes.
 size_t paged_attn_workspace_bytes(const PagedAttnArgs& a, int* n_splits_out);
 hipError_t launch_paged_attn(const PagedAttnArgs& a, void* workspace, hipStream_t stream);
+// Paged attention with its split partials in the library's static device
+// scratch (kNoAllocScratchBytes per device): allocates nothing.  *need gets the
+// scratch the call requires; hipErrorInvalidValue when that exceeds the maximum.
+constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
+hipError_t launch_paged_attn_noalloc(const PagedAttnArgs& a, hipStream_t stream, size_t* need);
 
 size_t flash_attn_f32_workspace_bytes(int n_head, int n_head_kv, int head_dim, int len,
                                       int* n_splits_out);

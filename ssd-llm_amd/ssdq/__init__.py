@@ -70,6 +70,8 @@ SIGNATURES = {
     "ssdq_paged_kv_append_dev": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _vp]),
     "ssdq_paged_attention_int8_dev": (
         _i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _vp]),
+    "ssdq_paged_attention_int8_noalloc_dev": (
+        _i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _vp]),
     "ssdq_flash_attention_f32_dev": (_i, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _vp]),
     "ssdq_flash_attention_f32": (_i, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _vp]),
     "ssdq_dequantize_to_f32": (_i, [_vp, _i, _vp, _sz, _sz, _vp]),
@@ -242,6 +244,18 @@ def paged_attention_int8(q, k_codes, k_scales, v_codes, v_scales, block_tables, 
                          max_ctx, stream=None):
     return check("ssdq_paged_attention_int8_dev",
                  lib().ssdq_paged_attention_int8_dev(
+                     _ptr(q), _ptr(k_codes), _ptr(k_scales), _ptr(v_codes), _ptr(v_scales),
+                     _ptr(block_tables), _ptr(ctx_lens), _ptr(out), n_seq, n_head, n_head_kv,
+                     head_dim, block_size, max_blocks_per_seq, max_ctx, _stream(stream)))
+
+
+def paged_attention_int8_noalloc(q, k_codes, k_scales, v_codes, v_scales, block_tables, ctx_lens, out,
+                                 n_seq, n_head, n_head_kv, head_dim, block_size, max_blocks_per_seq,
+                                 max_ctx, stream=None):
+    """paged_attention_int8 with its partials in the library's static device
+    scratch (16 MiB per GPU): allocates nothing; overlapping calls on one GPU race."""
+    return check("ssdq_paged_attention_int8_noalloc_dev",
+                 lib().ssdq_paged_attention_int8_noalloc_dev(
                      _ptr(q), _ptr(k_codes), _ptr(k_scales), _ptr(v_codes), _ptr(v_scales),
                      _ptr(block_tables), _ptr(ctx_lens), _ptr(out), n_seq, n_head, n_head_kv,
                      head_dim, block_size, max_blocks_per_seq, max_ctx, _stream(stream)))

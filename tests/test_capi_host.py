@@ -82,3 +82,14 @@ def test_cpp_host_mirror_header_compiles():
     r = subprocess.run(["g++", "-std=c++17", "-fsyntax-only", "-Wall", "-Wextra", "-x", "c++", hdr],
                        capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
+
+
+def test_noalloc_attention_rejects_oversized_partials_before_launch():
+    # 4096 sequences x 64 heads need >= 136 MB of split partials against the
+    # 16 MiB static scratch: rejected from the arguments alone, before any HIP
+    # launch (the dummy, never-dereferenced pointers are 256-aligned)
+    lib = ssdq.lib()
+    p = ctypes.c_void_p(256)
+    rc = lib.ssdq_paged_attention_int8_noalloc_dev(p, p, p, p, p, p, p, p, 4096, 64, 8, 128, 16, 64, 1024, None)
+    assert rc == -1
+    assert "scratch" in ssdq.last_error()

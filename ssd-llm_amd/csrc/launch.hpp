@@ -129,6 +129,12 @@ hipError_t launch_flash_attn_f32(const float* q, const float* k, const float* v,
                                  int window_start, int window_end, void* workspace,
                                  hipStream_t stream);
 
+// Q8_0 matvec of 2-8 activation rows on the matrix cores (matvec_mfma.hip);
+// hipErrorNotSupported when the shape or alignment does not fit it.
+bool q8_mfma_supported(const void* w, const float* x, size_t in_dim, size_t batch);
+hipError_t launch_q8_mfma(const uint8_t* w, const float* x, float* y, size_t out_dim, size_t in_dim, size_t batch,
+                          hipStream_t s);
+
 // Prefill GEMM: Y_i[M,n_i] f32 = X[M,K] bf16 x W_i[n_i,K] Q4_K (reference
 // layout) for count = 1..3 matrices sharing X, computed as one GEMM.
 hipError_t launch_gemm_q4k(const uint8_t* const* w, const size_t* n, int count, const uint16_t* x,

@@ -1657,7 +1657,8 @@ hipError_t fast_dispatch(const uint8_t* w, const float* x, float* y, int out_dim
     if (e != hipSuccess || *used) return e;
   } else {
     // chunks of 8 / 4 / 2 activation rows on mv_bn, a last single row on mv_b1
-    // (the first chunk decides: every chunk has the same row geometry)
+    // (the first chunk decides: every chunk has the same row geometry); Q8_0
+    // chunks of 2-8 rows at K = 1024 / 2048 / 4096 run on the matrix cores
     int b0 = 0;
     while (b0 < batch) {
       const int left = batch - b0;
@@ -1666,7 +1667,13 @@ hipError_t fast_dispatch(const uint8_t* w, const float* x, float* y, int out_dim
       bool u = false;
       hipError_t e;
       int take;
-      if (left >= 8) { take = 8; e = bn_dispatch<F, 8>(w, xb, yb, out_dim, in_dim, bpr, s, ws, ws_floats, &u); }
+      if (F == kQ8_0 && left >= 2 && q8_mfma_supported(w, xb, in_dim, std::min(left, 8))) {
+        take = std::min(left, 8);
+        e = launch_q8_mfma(w, xb, yb, out_dim, in_dim, take, s);
+        u = e == hipSuccess;
+        if (e == hipErrorNotSupported) e = hipSuccess;
+      }
+      else if (left >= 8) { take = 8; e = bn_dispatch<F, 8>(w, xb, yb, out_dim, in_dim, bpr, s, ws, ws_floats, &u); }
       else if (left >= 4) { take = 4; e = bn_dispatch<F, 4>(w, xb, yb, out_dim, in_dim, bpr, s, ws, ws_floats, &u); }
       else if (left >= 2) { take = 2; e = bn_dispatch<F, 2>(w, xb, yb, out_dim, in_dim, bpr, s, ws, ws_floats, &u); }
       else { take = 1; e = b1_dispatch<F>(w, xb, yb, out_dim, bpr, s, ws, ws_floats, &u); }

@@ -215,6 +215,43 @@ def test_extreme_and_nonfinite_activations(dtype, batch):
         assert np.all(np.abs(y[b] - exact[b]) <= 1e-3 * scale), f"row {b}"
 
 
+Q8_MFMA = [  # (out_dim, in_dim, batch): Q8_0 batches of 2-8 on the matrix cores
+    (11008, 4096, 2), (11008, 4096, 3), (11008, 4096, 5), (11008, 4096, 6), (11008, 4096, 7),
+    (4097, 4096, 8), (1000, 2048, 3), (17, 1024, 5), (4096, 1024, 8), (16, 4096, 2), (300, 4096, 12),
+]
+
+
+@pytest.mark.parametrize("out_dim,in_dim,batch", Q8_MFMA)
+def test_q8_0_small_batch_matrix_cores(out_dim, in_dim, batch):
+    # ragged row groups (out_dim not a multiple of 16), every batch size 2-8,
+    # K = 1024 / 2048 / 4096, and a batch of 12 (one chunk of 8 on the matrix
+    # cores, then 4)
+    w = synth.quant_weights(Q8_0, out_dim, in_dim, 800 + batch + out_dim)
+    x = synth.normal_f32((batch, in_dim), 900 + batch)
+    announce("q8_0 small batch", out_dim, in_dim, batch)
+    y, rc = run(Q8_0, w, x, out_dim, in_dim, batch)
+    assert rc == 0
+    ref, exact = reference(Q8_0, w, x, out_dim, in_dim, batch)
+    n = assert_close_attributed(y, ref, exact, f"q8_0 {out_dim}x{in_dim} B={batch}")
+    # run-to-run bit identity (fixed summation order)
+    y2, _ = run(Q8_0, w, x, out_dim, in_dim, batch)
+    assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
+
+
+def test_q8_0_small_batch_misaligned_x_takes_other_kernel():
+    # x at a 4-byte offset cannot feed the 16-byte loads: the digit-plane kernel runs
+    out_dim, in_dim, batch = 500, 4096, 4
+    w = synth.quant_weights(Q8_0, out_dim, in_dim, 77)
+    x = synth.normal_f32((batch, in_dim), 78)
+    buf = torch.empty(batch * in_dim + 1, dtype=torch.float32, device="cuda")
+    buf[1:].copy_(torch.from_numpy(x.ravel()).cuda())
+    y = empty_dev(out_dim * batch, torch.float32)
+    announce("q8_0 small batch misaligned")
+    assert ssdq.matvec(Q8_0, to_dev(w), buf[1:], y, out_dim, in_dim, batch) == 0
+    ref, exact = reference(Q8_0, w, x, out_dim, in_dim, batch)
+    assert_close_attributed(from_dev(y), ref, exact, "q8_0 misaligned x")
+
+
 LONG_ROWS = [  # batch-1 rows of 129-256 units (K slices summed in slice order)
     (Q4_K, 77, 256 * 36), (Q4_K, 1000, 256 * 64), (Q4_K, 4096, 14336),
     (Q4_0, 300, 64 * 144), (Q4_0, 64, 64 * 256), (Q8_0, 129, 64 * 192), (Q8_0, 4096, 14336),

@@ -36,7 +36,14 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--profile-pass", action="store_true",
                     help="short run for hardware-counter passes: a Q8_0 dequant of known size (the "
-                         "counter calibration), then 20 headline matvec launches; prints no JSON")
+                         "counter calibration), then a few launches of every configuration's kernels; "
+                         "prints no JSON")
+    ap.add_argument("--ceiling", action="store_true",
+                    help="plain streaming-read bandwidth versus size and the cost of an empty launch "
+                         "(libssdq_probe.so), timed like the matvecs; prints one JSON line")
+    ap.add_argument("--hipblaslt", action="store_true",
+                    help="torch's fp16 GEMM (hipBLASLt) of the config-4 layer shapes on already "
+                         "dequantized weights, for comparison with the Q4_K prefill GEMM; prints one JSON line")
     ap.add_argument("--eager", action="store_true",
                     help="launch every matvec step from Python instead of replaying captured HIP graphs")
     return ap.parse_args()
@@ -174,6 +181,12 @@ def main():
     if args.profile_pass:
         profile_pass(torch, ssdq, synth)
         return
+    if args.ceiling:
+        print(json.dumps(read_ceiling(torch)))
+        return
+    if args.hipblaslt:
+        print(json.dumps(hipblaslt_layer(torch)))
+        return
     timer = Timer(torch, graph=not args.eager)
 
     # ---------------------------------------------------------- headline
@@ -227,26 +240,190 @@ CAL_ELEMS = 1 << 26  # Q8_0 dequant calibration: 71,303,168 B read, 268,435,456 
 
 
 def profile_pass(torch, ssdq, synth):
-    """Launch sequence profiled with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE.
+    """Launch sequence profiled with rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE, SQ_*).
 
-    Dispatches, in order: 3 x dequant_kernel (Q8_0, CAL_ELEMS elements: a plain
-    streaming kernel whose bytes are known exactly, used to scale the counters
-    to bytes), then 20 x the headline Q4_K 14336x4096 matvec over rotating
-    weight copies."""
+    Dispatches, in order (each section on its own weight copies, so every
+    launch streams from HBM):
+      3 x dequant_kernel (Q8_0, CAL_ELEMS elements): a plain streaming kernel
+          whose bytes are known exactly, used to scale the counters to bytes;
+      20 x the headline Q4_K 14336x4096 batch-1 matvec (config 3);
+      20 x Q4_0 4096x4096 and 20 x Q4_0 14336x4096 (config 1, north-star shape);
+      20 x Q8_0 11008x4096 at B = 1, 4 and 8 (config 2);
+      20 x Q6_K 4096x14336 (config 3; K slices + slice_reduce_kernel);
+      3 x the config-4 prefill GEMM layer (q/k/v and gate/up fused, o, down);
+      3 x INT8 quantize of 8 x 32768 x {K, V} rows of 1024 (config 5a);
+      5 x paged INT8 decode attention, 8 x 32k context (config 5b)."""
     nb = CAL_ELEMS // 32
     raw = torch.randint(0, 256, (nb * 34,), dtype=torch.uint8, device="cuda")
     raw.view(nb, 34)[:, 0:2] = torch.tensor([0x00, 0x3C], dtype=torch.uint8, device="cuda")  # d = 1.0
     out = torch.empty(CAL_ELEMS, device="cuda")
-    step, algo_bytes, _ = matvec_case(torch, ssdq, synth, ssdq.Q4_K, 14336, 4096, 1, 3)
     torch.cuda.synchronize()
     for _ in range(3):
         ssdq.dequant(ssdq.Q8_0, raw, CAL_ELEMS, out)
     torch.cuda.synchronize()
-    for i in range(20):
-        step(i)
+    del raw, out
+    print(f"profile pass: calibration read {nb * 34} B write {CAL_ELEMS * 4} B", flush=True)
+    for name, dt, od, idim, b, cfg in [("q4k_matvec_14336x4096", ssdq.Q4_K, 14336, 4096, 1, 3),
+                                       ("q4_0_matvec_4096x4096", ssdq.Q4_0, 4096, 4096, 1, 1),
+                                       ("q4_0_matvec_14336x4096", ssdq.Q4_0, 14336, 4096, 1, 1),
+                                       ("q8_0_matvec_11008x4096_b1", ssdq.Q8_0, 11008, 4096, 1, 2),
+                                       ("q8_0_matvec_11008x4096_b4", ssdq.Q8_0, 11008, 4096, 4, 2),
+                                       ("q8_0_matvec_11008x4096_b8", ssdq.Q8_0, 11008, 4096, 8, 2),
+                                       ("q6_k_matvec_4096x14336", ssdq.Q6_K, 4096, 14336, 1, 3)]:
+        step, algo_bytes, _ = matvec_case(torch, ssdq, synth, dt, od, idim, b, cfg)
+        step(0)
+        torch.cuda.synchronize()
+        for i in range(20):
+            step(i)
+        torch.cuda.synchronize()
+        print(f"profile pass: {name} x20, algorithmic bytes {algo_bytes}", flush=True)
+        del step
+        torch.cuda.empty_cache()
+    layer_fused, flops = gemm_layer(torch, ssdq, synth)
+    layer_fused(0)
     torch.cuda.synchronize()
-    print(f"profile pass done: calibration read {nb * 34} B write {CAL_ELEMS * 4} B; "
-          f"headline algorithmic bytes {algo_bytes}", flush=True)
+    for i in range(3):
+        layer_fused(i)
+    torch.cuda.synchronize()
+    print(f"profile pass: prefill GEMM layer x3, {flops:.0f} FLOP per layer", flush=True)
+    del layer_fused
+    torch.cuda.empty_cache()
+    n_rows, dim = 8 * 32768 * 2, 1024
+    xk = torch.randn(n_rows * dim, device="cuda")
+    codes = torch.empty(n_rows * dim, dtype=torch.int8, device="cuda")
+    scales = torch.empty(n_rows, device="cuda")
+    for _ in range(3):
+        ssdq.kv_quantize_rows(xk, codes, scales, n_rows, dim)
+    torch.cuda.synchronize()
+    print(f"profile pass: kv quantize x3, algorithmic bytes {n_rows * dim * 5 + n_rows * 4}", flush=True)
+    del xk
+    attn = attention_case(torch, ssdq, synth, codes, scales)
+    for i in range(5):
+        attn(i)
+    torch.cuda.synchronize()
+    print("profile pass: paged attention x5, algorithmic bytes 539295744", flush=True)
+
+
+def gemm_layer(torch, ssdq, synth):
+    """The config-4 layer as the bench runs it: q/k/v and gate/up each one GEMM
+    over shared X (multi entry point), o and down alone.  Returns (fn, FLOP)."""
+    layer = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
+             ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]
+    M = 512
+    W, Y = {}, {}
+    flops = 0
+    for i, (nm, N, K) in enumerate(layer):
+        W[nm] = torch.from_numpy(synth.quant_weights(ssdq.Q4_K, N, K, synth.seed(4, i))).cuda()
+        Y[nm] = torch.empty(M * N, device="cuda")
+        flops += 2.0 * M * N * K
+    X = {4096: torch.randn(M, 4096, device="cuda").to(torch.bfloat16).view(torch.int16),
+         14336: torch.randn(M, 14336, device="cuda").to(torch.bfloat16).view(torch.int16)}
+    dims = {nm: (N, K) for nm, N, K in layer}
+    groups = [("q", "k", "v"), ("o",), ("gate", "up"), ("down",)]
+
+    def layer_fused(i):
+        for g in groups:
+            K = dims[g[0]][1]
+            ssdq.gemm_q4k_bf16_multi([W[n] for n in g], X[K], [Y[n] for n in g], M, [dims[n][0] for n in g], K)
+
+    def layer_separate(i):
+        for nm, N, K in layer:
+            ssdq.gemm_q4k_bf16(W[nm], X[K], Y[nm], M, N, K)
+
+    layer_fused.separate = layer_separate
+    return layer_fused, flops
+
+
+def attention_case(torch, ssdq, synth, codes, scales):
+    """Config 5b on an INT8 pool (codes [2 * 8 * 32768, 1024]: K rows, then V rows)."""
+    n_seq, n_head, n_kv, hd, bs, ctx = 8, 32, 8, 128, 16, 32768
+    mb = ctx // bs
+    kc = codes[: n_seq * mb * bs * n_kv * hd]
+    vc = codes[n_seq * mb * bs * n_kv * hd:]
+    ks = scales[: n_seq * mb * bs]
+    vs = scales[n_seq * mb * bs:]
+    tables = torch.from_numpy(synth.block_tables(n_seq, mb, synth.seed(5, 3))).cuda()
+    cl = torch.full((n_seq,), ctx, dtype=torch.int32, device="cuda")
+    q = torch.randn(n_seq * n_head * hd, device="cuda")
+    o = torch.empty_like(q)
+    return lambda i: ssdq.paged_attention_int8(q, kc, ks, vc, vs, tables, cl, o, n_seq, n_head, n_kv, hd, bs, mb,
+                                               ctx)
+
+
+def _probe_lib():
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(ROOT, "ssd-llm_amd", "libssdq_probe.so"))
+    lib.ssdq_probe_read.restype = ctypes.c_int
+    lib.ssdq_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                    ctypes.c_void_p]
+    lib.ssdq_probe_empty.restype = ctypes.c_int
+    lib.ssdq_probe_empty.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    return lib
+
+
+def read_ceiling(torch):
+    """Plain streaming reads (16-byte loads, 4 in flight per thread, one
+    contiguous slice per workgroup) of buffers from 4 MB to 512 MB, each rotated
+    over copies larger than twice the last-level cache and timed like the
+    matvecs (graph replays); the best of several launch shapes per size.  Also
+    the time per launch of an empty kernel (256 x 256 and 256 x 768 threads)."""
+    lib = _probe_lib()
+    timer = Timer(torch)
+    sink = torch.zeros(65536, dtype=torch.int32, device="cuda")
+    stream = lambda: torch.cuda.current_stream().cuda_stream
+    out = {"read": [], "empty_kernel_us": {}}
+    for mb in (4, 8, 16, 33.1, 48, 64, 128, 256, 512):
+        nbytes = int(mb * 1e6) // 16 * 16 if mb == 33.1 else int(mb * (1 << 20))
+        if mb == 33.1:
+            nbytes = 33103872  # the headline matvec's algorithmic bytes
+        n = copies_for(nbytes)
+        bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1) for _ in range(n)]
+        best = None
+        for grid, block in ((256, 768), (512, 512), (1024, 256), (2048, 256), (2048, 512), (4096, 256)):
+            def step(i, grid=grid, block=block):
+                rc = lib.ssdq_probe_read(bufs[i % n].data_ptr(), nbytes, sink.data_ptr(), grid, block, stream())
+                if rc != 0:
+                    raise RuntimeError(f"ssdq_probe_read: hip error {rc}")
+            tr = timer.run(step, 200, 200)
+            us = tr["t_median"] / tr["steps"] * 1e6
+            if best is None or us < best[0]:
+                best = (us, grid, block)
+        out["read"].append({"bytes": nbytes, "us": round(best[0], 3), "GB/s": round(nbytes / best[0] / 1e3, 1),
+                            "pct_hbm_peak": round(100 * nbytes / best[0] / 1e3 / HBM_PEAK_GBS, 2),
+                            "grid": best[1], "block": best[2]})
+        del bufs
+        torch.cuda.empty_cache()
+    for grid, block in ((256, 256), (256, 768)):
+        tr = timer.run(lambda i: lib.ssdq_probe_empty(grid, block, stream()), 200, 200)
+        out["empty_kernel_us"][f"{grid}x{block}"] = round(tr["t_median"] / tr["steps"] * 1e6, 3)
+    return out
+
+
+def hipblaslt_layer(torch):
+    """torch.matmul in fp16 (hipBLASLt) over the config-4 layer: X [512, K] fp16
+    times already-dequantized fp16 weights [K, N] for the seven matrices (4x the
+    Q4_K weight bytes), timed as a whole layer with HIP events."""
+    M = 512
+    layer = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
+             ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]
+    W = {nm: torch.randn(K, N, device="cuda", dtype=torch.float16) * 0.02 for nm, N, K in layer}
+    X = {K: torch.randn(M, K, device="cuda", dtype=torch.float16) for K in (4096, 14336)}
+    Y = {}
+    flops = sum(2.0 * M * N * K for _, N, K in layer)
+
+    def run(i):
+        for nm, N, K in layer:
+            Y[nm] = torch.matmul(X[K], W[nm])
+    timer = Timer(torch)
+    tr = timer.run(run, 20, 10, graph=False)
+    t = tr["t_median"] / tr["steps"]
+    per = {}
+    for nm, N, K in layer:
+        tr1 = timer.run(lambda i, nm=nm, K=K: torch.matmul(X[K], W[nm]), 20, 10, graph=False)
+        per[nm] = round(tr1["t_median"] / tr1["steps"] * 1e6, 2)
+    return {"what": "torch.matmul fp16 (hipBLASLt), config-4 layer shapes, M = 512, dequantized fp16 weights",
+            "ms_per_layer": round(t * 1e3, 4), "TFLOP/s": round(flops / t / 1e12, 1),
+            "pct_bf16_peak": round(100 * flops / t / 1e12 / BF16_PEAK_TFLOPS, 2), "us_per_matrix": per}
 
 
 def traffic_from_profiles(key):
@@ -371,38 +548,16 @@ def extras(torch, ssdq, synth, timer, np):
     # config 4: one Llama-3-8B layer of Q4_K prefill GEMMs at M = 512.  q/k/v
     # and gate/up read the same X and run as one GEMM each (multi entry point);
     # the seven separate GEMMs are timed as well.
-    layer = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
-             ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]
-    M = 512
-    W, Y = {}, {}
-    flops = 0
-    for i, (nm, N, K) in enumerate(layer):
-        W[nm] = torch.from_numpy(synth.quant_weights(ssdq.Q4_K, N, K, synth.seed(4, i))).cuda()
-        Y[nm] = torch.empty(M * N, device="cuda")
-        flops += 2.0 * M * N * K
-    X = {4096: torch.randn(M, 4096, device="cuda").to(torch.bfloat16).view(torch.int16),
-         14336: torch.randn(M, 14336, device="cuda").to(torch.bfloat16).view(torch.int16)}
-    dims = {nm: (N, K) for nm, N, K in layer}
-    groups = [("q", "k", "v"), ("o",), ("gate", "up"), ("down",)]
-
-    def layer_fused(i):
-        for g in groups:
-            K = dims[g[0]][1]
-            ssdq.gemm_q4k_bf16_multi([W[n] for n in g], X[K], [Y[n] for n in g], M, [dims[n][0] for n in g], K)
-
-    def layer_separate(i):
-        for nm, N, K in layer:
-            ssdq.gemm_q4k_bf16(W[nm], X[K], Y[nm], M, N, K)
-
+    layer_fused, flops = gemm_layer(torch, ssdq, synth)
     t = timer.run(layer_fused, 5, 1, graph=False)["t_median"]
-    t_sep = timer.run(layer_separate, 5, 1, graph=False)["t_median"]
+    t_sep = timer.run(layer_fused.separate, 5, 1, graph=False)["t_median"]
     tfl = flops / (t / 5) / 1e12
     out["prefill_gemm_q4k_layer_m512"] = {"TFLOP/s": round(tfl, 2),
                                           "pct_bf16_peak": round(100 * tfl / BF16_PEAK_TFLOPS, 2),
                                           "ms_per_layer": round(t / 5 * 1e3, 3),
                                           "ms_per_layer_seven_separate_gemms": round(t_sep / 5 * 1e3, 3),
                                           "note": "q/k/v and gate/up each one GEMM over shared X"}
-    del W, Y, X
+    del layer_fused
     torch.cuda.empty_cache()
 
     # config 5a: INT8 quantize of 8 x 32768 tokens x {K, V} x 1024
@@ -417,19 +572,8 @@ def extras(torch, ssdq, synth, timer, np):
                                               "us": round(t / 20 * 1e6, 1)}
     del xk
     # config 5b: paged INT8 GQA decode attention, reusing the quantized pool
-    n_seq, n_head, n_kv, hd, bs, ctx = 8, 32, 8, 128, 16, 32768
-    mb = ctx // bs
-    kc = codes[: n_seq * mb * bs * n_kv * hd]
-    vc = codes[n_seq * mb * bs * n_kv * hd:]
-    ks = scales[: n_seq * mb * bs]
-    vs = scales[n_seq * mb * bs:]
-    tables = torch.from_numpy(synth.block_tables(n_seq, mb, synth.seed(5, 3))).cuda()
-    cl = torch.full((n_seq,), ctx, dtype=torch.int32, device="cuda")
-    q = torch.randn(n_seq * n_head * hd, device="cuda")
-    o = torch.empty_like(q)
-    t = timer.run(lambda i: ssdq.paged_attention_int8(q, kc, ks, vc, vs, tables, cl, o, n_seq,
-                                                            n_head, n_kv, hd, bs, mb, ctx), 50, 5,
-                        graph=False)["t_median"]
+    n_seq = 8
+    t = timer.run(attention_case(torch, ssdq, synth, codes, scales), 50, 5, graph=False)["t_median"]
     abytes = 536870912 + 2097152 + 131072 + 131072 + 65536
     step_s = t / 50
     out["paged_int8_decode_attention_32k"] = {

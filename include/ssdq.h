@@ -305,6 +305,106 @@ int ssdq_flash_attention_f32(ssdq_ctx* ctx, const float* q, const float* k, cons
                              size_t n_head, size_t n_head_kv, size_t head_dim, size_t seq_len,
                              size_t window_start, size_t window_end, float* out);
 
+/* ------------------------------------------------ resident weight store */
+/* Raw GGUF tensor bytes kept in HBM, uploaded once and found by name.
+ * Replaces SsdStreamer::load_layer / load_tensor_f32 (src/ssd/streamer.rs:
+ * 33-66), which re-read a layer's tensors and dequantize them to f32 on every
+ * load (Q4_K to zeros, streamer.rs:119-123): the quantized blocks stay as the
+ * file holds them and the dev functions decode them in place. Tensors are
+ * placed 256-byte aligned in device arenas of at least 256 MiB. A store
+ * belongs to one device; its calls are thread-safe. */
+typedef struct ssdq_weights ssdq_weights;
+/* device: a HIP ordinal, -1 for the current device. SSDQ_ERR_NO_DEVICE when
+ * there is none. */
+int ssdq_weights_create(int device, ssdq_weights** out);
+/* Waits for the device, then frees every tensor of the store. */
+void ssdq_weights_destroy(ssdq_weights* w);
+/* Uploads one tensor (TensorInfo, src/model/gguf.rs:216-222): its GGUF name,
+ * GgmlType id, dims as GGUF lists them (dims[0] is the row length; a matrix
+ * is {in_dim, out_dim}), and data_len bytes from host memory (e.g. the mapped
+ * file at the tensor's offset, GgufLoader::get_tensor_data). For the types
+ * this library knows, dims[0] must be a whole number of blocks and data_len
+ * the size dims and type give. Synchronous. A name already resident, or a
+ * size mismatch: SSDQ_ERR_INVALID_ARG. */
+int ssdq_weights_put(ssdq_weights* w, const char* name, int dtype, const uint64_t* dims, size_t n_dims,
+                     const void* data, size_t data_len);
+/* The device address of a resident tensor, NULL when absent (Option, as
+ * find_tensor_in_layer returns, transformer.rs:552-559). The out pointers may
+ * be NULL; dims gets 4 entries (1 past n_dims). */
+const void* ssdq_weights_find(const ssdq_weights* w, const char* name, int* dtype, uint64_t* dims,
+                              size_t* n_dims, size_t* n_bytes);
+size_t ssdq_weights_count(const ssdq_weights* w);
+/* tensor bytes resident (CachedLayer::size_bytes summed, in file bytes) */
+size_t ssdq_weights_bytes(const ssdq_weights* w);
+int ssdq_weights_device(const ssdq_weights* w);
+
+/* ------------------------------------------------------ decoder layer */
+/* One layer's shape. n_head * head_dim is the query width, n_head_kv *
+ * head_dim the key / value width (the reference sets head_dim = n_embd /
+ * n_head, transformer.rs:295). rope_theta: DEFAULT_ROPE_THETA for Llama;
+ * norm_eps: 1e-5 in the reference (transformer.rs:577, 351). */
+typedef struct ssdq_layer_config {
+  size_t n_embd;
+  size_t n_head;
+  size_t n_head_kv;
+  size_t head_dim; /* 64, 128 or 256 */
+  size_t n_ff;
+  float rope_theta;
+  float norm_eps;
+} ssdq_layer_config;
+
+/* Regions of the layer's scratch buffer, in floats of the named step's output:
+ * attention input (normed), q, k, v (after RoPE), attention, output
+ * projection, FFN input (normed), silu(gate) * up, gate and up (used when
+ * their types differ), down projection, widened norm weights (F16 / BF16 norms). */
+#define SSDQ_LAYER_ATTN_IN 0
+#define SSDQ_LAYER_Q 1
+#define SSDQ_LAYER_K 2
+#define SSDQ_LAYER_V 3
+#define SSDQ_LAYER_ATTN 4
+#define SSDQ_LAYER_ATTN_OUT 5
+#define SSDQ_LAYER_FFN_IN 6
+#define SSDQ_LAYER_FFN_H 7
+#define SSDQ_LAYER_FFN_GATE 8
+#define SSDQ_LAYER_FFN_UP 9
+#define SSDQ_LAYER_FFN_OUT 10
+#define SSDQ_LAYER_NORM_W 11
+#define SSDQ_LAYER_N_STAGES 12
+/* Bytes of scratch ssdq_decode_layer_dev needs (0 for a bad config);
+ * offsets (NULL, or SSDQ_LAYER_N_STAGES entries) gets each region's byte
+ * offset. After a call each region holds that step's output for the token. */
+size_t ssdq_decode_layer_scratch_bytes(const ssdq_layer_config* cfg, size_t* offsets);
+
+/* One decoder layer for one token, from the store's tensors
+ * "blk.{layer}.{attn_norm, attn_q, attn_k, attn_v, attn_output, ffn_norm,
+ * ffn_gate, ffn_up, ffn_down}.weight": the per-layer body of forward_pass
+ * (src/inference/transformer.rs:319-397) with multi_head_attention_fused_rope
+ * (src/inference/attention.rs:172-240) over the paged INT8 cache and the
+ * dense SwiGLU FFN (transformer.rs:470-481, feed_forward.rs:16-71):
+ *   x = rms_norm(hidden, attn_norm)
+ *   q, k, v = Wq x, Wk x, Wv x; RoPE(q, k) at `position`  (ssdq_qkv_rope_dev)
+ *   pool row slot_mapping[0] = int8(k), int8(v)            (ssdq_paged_kv_append_dev)
+ *   a = attention of q over ctx_len[0] tokens              (ssdq_paged_attention_int8_dev)
+ *   hidden += Wo a; f = rms_norm(hidden, ffn_norm)         (ssdq_matvec_dev, ssdq_rmsnorm_dev)
+ *   hidden += W_down (silu(W_gate f) * (W_up f))           (ssdq_swiglu_dev, ssdq_matvec_dev)
+ * As in the reference: no attn_norm -> x = hidden; any of the four attention
+ * tensors absent -> the layer leaves hidden unchanged; no ffn_norm -> f =
+ * hidden after the residual add; any FFN tensor absent -> no FFN. MoE layers
+ * (ffn_gate_inp) are not on this path. hidden: n_embd floats on the device,
+ * updated in place. The pool arguments are those of the paged append and
+ * attention above for one sequence (block_table: max_blocks_per_seq entries;
+ * slot_mapping and ctx_len: one int32 each, in device memory). scratch: NULL
+ * for the library's per-stream workspace, or a 256-byte aligned buffer of
+ * ssdq_decode_layer_scratch_bytes(cfg) bytes. Shapes of every tensor are
+ * checked before anything is launched. Status: the worst of the steps
+ * (SSDQ_WARN_UNSUPPORTED_ZEROED when a projection's type is unsupported and
+ * its output was zero-filled, as the reference's matvec does). */
+int ssdq_decode_layer_dev(const ssdq_weights* w, uint32_t layer, const ssdq_layer_config* cfg, float* hidden,
+                          size_t position, int8_t* k_codes, float* k_scales, int8_t* v_codes, float* v_scales,
+                          size_t block_size, const int32_t* block_table, size_t max_blocks_per_seq,
+                          const int32_t* slot_mapping, const int32_t* ctx_len, size_t max_ctx, void* scratch,
+                          size_t scratch_bytes, ssdq_stream_t stream);
+
 /* -------------------------------------------------------------- testing */
 /* Forces the byte-addressed matvec kernel that unaligned weights take, so the
  * fallback can be checked on aligned inputs. Same contract as ssdq_matvec_dev. */

@@ -60,7 +60,9 @@ struct Workspace {
   size_t bytes = 0;
 };
 // slot 0: the kernels' own scratch; slot 1: intermediates of the unfused
-// decode-layer paths, which call kernels that use slot 0.
+// decode-layer paths, which call kernels that use slot 0; slot 2: the
+// activations of ssdq_decode_layer_dev, which calls entry points that use
+// slots 0 and 1.
 std::mutex g_ws_mu;
 std::map<std::tuple<int, void*, int>, Workspace> g_ws;
 // Buffers replaced by a larger one.  A HIP graph captured earlier on that
@@ -97,6 +99,19 @@ hipError_t workspace_get(size_t bytes, hipStream_t stream, void** out, int slot 
 }  // namespace
 
 namespace ssdq {
+
+int api_fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+int api_hip_fail(hipError_t e, const char* what) { return hip_fail(e, what); }
+int api_ok() { return ok(); }
+hipError_t api_workspace(size_t bytes, hipStream_t stream, void** out, int slot) {
+  return workspace_get(bytes, stream, out, slot);
+}
 
 int device_cu_count() {
   static std::mutex mu;

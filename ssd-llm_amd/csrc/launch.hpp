@@ -75,6 +75,8 @@ hipError_t launch_matvec_fused(int dtype, const MatvecFuse& f, int total_rows, c
 hipError_t launch_rope(float* v, int n, int head_dim, int position, const RopeFreq& freq, hipStream_t stream);
 // h = silu(g) * u
 hipError_t launch_swiglu(const float* g, const float* u, float* h, int n, hipStream_t stream);
+// h += a (n floats)
+hipError_t launch_residual_add(float* h, const float* a, int n, hipStream_t stream);
 // hsum = x + residual (residual may be null; hidden_out may be null), then
 // out = hsum * inv_rms * w with inv_rms = 1 / sqrt(mean(hsum^2) + eps).
 hipError_t launch_rmsnorm(const float* x, const float* residual, const float* w, float eps,
@@ -144,5 +146,13 @@ size_t gemm_q4k_workspace_bytes(const void* const* w, const size_t* n, int count
                                 size_t K);
 
 int device_cu_count();
+
+// The C ABI's status plumbing, for entry points defined outside capi.cpp:
+// api_fail records the thread's last error message and returns code;
+// api_workspace hands out the per-(device, stream, slot) grow-only workspace.
+int api_fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int api_hip_fail(hipError_t e, const char* what);
+int api_ok();
+hipError_t api_workspace(size_t bytes, hipStream_t stream, void** out, int slot);
 
 }  // namespace ssdq

@@ -32,6 +32,13 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g
   }
 }
 
+// h += a: the FFN residual add of the decoder layer (transformer.rs:378-380).
+__global__ __launch_bounds__(256) void residual_add_kernel(float* __restrict__ h, const float* __restrict__ a,
+                                                           int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) h[i] += a[i];
+}
+
 // One workgroup: the whole vector (n is a hidden size, a few thousand).  Up to
 // 8 elements per thread are kept in registers with their norm weights, so x,
 // the residual and w are all requested before the reduction (one memory round
@@ -95,6 +102,12 @@ hipError_t launch_rope(float* v, int n, int head_dim, int position, const RopeFr
 hipError_t launch_swiglu(const float* g, const float* u, float* h, int n, hipStream_t s) {
   if (n <= 0) return hipSuccess;
   hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, g, u, h, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_residual_add(float* h, const float* a, int n, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(residual_add_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, h, a, n);
   return hipGetLastError();
 }
 

@@ -10,6 +10,9 @@
 //   flash_attention_f32(..) -> Option<Vec<f32>>  flash_attention_f32(..) -> std::optional
 //   dequantize_to_f32(..) -> Result<Vec<f32>>    dequantize_to_f32(..) (throws ssdq::Error)
 //   quantize_vectors_int8 / dequantize_vectors_int8
+//   SsdStreamer::load_layer -> CachedLayer        ResidentWeights::load_layer (tensors stay in HBM)
+//   find_tensor_in_layer(..) -> Option<&Vec<f32>> ResidentWeights::find_tensor_in_layer -> std::optional
+//   forward_pass's per-layer body                 forward_layer (device buffers, paged INT8 KV)
 // Differences, all deliberate: a context is created once and reused (the
 // reference builds a MetalCompute per forward pass, transformer.rs:301-302);
 // a short weight or activation slice raises ssdq::Error where the reference
@@ -155,5 +158,110 @@ class GpuCompute {
   explicit GpuCompute(ssdq_ctx* c) : ctx_(c, detail::CtxDeleter()) {}
   std::shared_ptr<ssdq_ctx> ctx_;  // shared: copies of a GpuCompute use one context
 };
+
+// TensorInfo (src/model/gguf.rs:216-222): what the GGUF parser lists for a
+// tensor; offset is from the start of the file's data section.
+struct TensorInfo {
+  std::string name;
+  std::vector<uint64_t> dimensions;  // row length first
+  int dtype = 0;                     // GgmlType id
+  uint64_t offset = 0;
+  uint64_t size_bytes = 0;
+};
+
+// SsdStreamer::load_layer (src/ssd/streamer.rs:43-66) with the tensors kept
+// as their raw GGUF bytes in HBM (uploaded once) instead of dequantized f32
+// vectors per load; find_tensor_in_layer (transformer.rs:552-559) returns
+// the resident tensor.
+class ResidentWeights {
+ public:
+  struct Tensor {
+    const void* data;  // device address
+    int dtype;
+    std::vector<uint64_t> dims;
+    size_t bytes;
+  };
+
+  // std::nullopt when no usable GPU exists (as GpuCompute::create)
+  static std::optional<ResidentWeights> create(int device = -1) {
+    ssdq_weights* w = nullptr;
+    if (ssdq_weights_create(device, &w) != SSDQ_OK) return std::nullopt;
+    return ResidentWeights(w);
+  }
+
+  // load_tensor_f32 without the dequantization: the tensor's bytes at
+  // data_section + offset (the mapped file, GgufLoader::get_tensor_data)
+  void put(const TensorInfo& t, const uint8_t* data_section) {
+    detail::check("ssdq_weights_put",
+                  ssdq_weights_put(w_.get(), t.name.c_str(), t.dtype, t.dimensions.data(), t.dimensions.size(),
+                                   data_section + t.offset, t.size_bytes));
+  }
+
+  // load_layer: every tensor named "blk.{layer_idx}." (GgufFile::layer_tensors,
+  // gguf.rs:410-416); returns the bytes made resident (CachedLayer::size_bytes)
+  size_t load_layer(const std::vector<TensorInfo>& tensors, const uint8_t* data_section, uint32_t layer_idx) {
+    const std::string prefix = "blk." + std::to_string(layer_idx) + ".";
+    size_t total = 0;
+    for (const auto& t : tensors) {
+      if (t.name.compare(0, prefix.size(), prefix) != 0) continue;
+      put(t, data_section);
+      total += t.size_bytes;
+    }
+    return total;
+  }
+
+  std::optional<Tensor> find(const std::string& name) const {
+    int dt = 0;
+    uint64_t dims[4];
+    size_t nd = 0, nb = 0;
+    const void* p = ssdq_weights_find(w_.get(), name.c_str(), &dt, dims, &nd, &nb);
+    if (!p) return std::nullopt;
+    return Tensor{p, dt, std::vector<uint64_t>(dims, dims + nd), nb};
+  }
+
+  std::optional<Tensor> find_tensor_in_layer(const std::string& suffix, uint32_t layer_idx) const {
+    return find("blk." + std::to_string(layer_idx) + "." + suffix);
+  }
+
+  size_t size() const { return ssdq_weights_count(w_.get()); }
+  size_t size_bytes() const { return ssdq_weights_bytes(w_.get()); }
+  ssdq_weights* raw() const { return w_.get(); }
+
+ private:
+  struct Deleter {
+    void operator()(ssdq_weights* w) const { ssdq_weights_destroy(w); }
+  };
+  explicit ResidentWeights(ssdq_weights* w) : w_(w, Deleter()) {}
+  std::shared_ptr<ssdq_weights> w_;
+};
+
+// One sequence's view of a layer's paged INT8 KV pool (device memory):
+// PagedKvCache's block table and the pool rows of PhysicalBlock
+// (src/inference/paged_attention.rs:34-35, 113-123).
+struct PagedKvView {
+  int8_t* k_codes;
+  float* k_scales;
+  int8_t* v_codes;
+  float* v_scales;
+  size_t block_size;
+  const int32_t* block_table;  // max_blocks_per_seq entries
+  size_t max_blocks_per_seq;
+  const int32_t* slot_mapping;  // 1 entry: the pool row of this token
+  const int32_t* ctx_len;       // 1 entry: tokens after the append
+  size_t max_ctx;
+};
+
+// One layer of forward_pass (transformer.rs:319-397) for one token on device
+// buffers: hidden (n_embd floats) is updated in place.  Returns the status
+// (SSDQ_WARN_UNSUPPORTED_ZEROED passes, as the reference's zeros do).
+inline int forward_layer(const ResidentWeights& w, uint32_t layer_idx, const ssdq_layer_config& cfg,
+                         float* hidden, size_t position, const PagedKvView& kv, void* stream = nullptr,
+                         void* scratch = nullptr, size_t scratch_bytes = 0) {
+  return detail::check("ssdq_decode_layer_dev",
+                       ssdq_decode_layer_dev(w.raw(), layer_idx, &cfg, hidden, position, kv.k_codes, kv.k_scales,
+                                             kv.v_codes, kv.v_scales, kv.block_size, kv.block_table,
+                                             kv.max_blocks_per_seq, kv.slot_mapping, kv.ctx_len, kv.max_ctx,
+                                             scratch, scratch_bytes, stream));
+}
 
 }  // namespace ssdq

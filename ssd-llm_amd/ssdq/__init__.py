@@ -39,6 +39,20 @@ class SsdqError(RuntimeError):
 _c = ctypes
 _vp, _sz, _i = _c.c_void_p, _c.c_size_t, _c.c_int
 
+
+
+class LayerConfig(ctypes.Structure):
+    """ssdq_layer_config: one decoder layer's shape."""
+    _fields_ = [("n_embd", _sz), ("n_head", _sz), ("n_head_kv", _sz), ("head_dim", _sz), ("n_ff", _sz),
+                ("rope_theta", _c.c_float), ("norm_eps", _c.c_float)]
+
+
+# scratch regions of ssdq_decode_layer_dev (SSDQ_LAYER_*)
+LAYER_STAGES = ("attn_in", "q", "k", "v", "attn", "attn_out", "ffn_in", "ffn_h", "ffn_gate", "ffn_up",
+                "ffn_out", "norm_w")
+
+_u64p = _c.POINTER(_c.c_uint64)
+
 # name -> (restype, argtypes); mirrors include/ssdq.h
 SIGNATURES = {
     "ssdq_abi_version": (_i, []),
@@ -77,6 +91,16 @@ SIGNATURES = {
     "ssdq_dequantize_to_f32": (_i, [_vp, _i, _vp, _sz, _sz, _vp]),
     "ssdq_quantize_vectors_int8": (_i, [_vp, _vp, _sz, _sz, _vp, _vp]),
     "ssdq_dequantize_vectors_int8": (_i, [_vp, _vp, _vp, _sz, _sz, _vp]),
+    "ssdq_weights_create": (_i, [_i, _c.POINTER(_vp)]),
+    "ssdq_weights_destroy": (None, [_vp]),
+    "ssdq_weights_put": (_i, [_vp, _c.c_char_p, _i, _u64p, _sz, _vp, _sz]),
+    "ssdq_weights_find": (_vp, [_vp, _c.c_char_p, _c.POINTER(_i), _u64p, _c.POINTER(_sz), _c.POINTER(_sz)]),
+    "ssdq_weights_count": (_sz, [_vp]),
+    "ssdq_weights_bytes": (_sz, [_vp]),
+    "ssdq_weights_device": (_i, [_vp]),
+    "ssdq_decode_layer_scratch_bytes": (_sz, [_c.POINTER(LayerConfig), _c.POINTER(_sz)]),
+    "ssdq_decode_layer_dev": (_i, [_vp, _c.c_uint32, _c.POINTER(LayerConfig), _vp, _sz, _vp, _vp, _vp, _vp, _sz,
+                                   _vp, _sz, _vp, _vp, _sz, _vp, _sz, _vp]),
 }
 
 _lib = None
@@ -344,3 +368,92 @@ class Context:
                                             window_end, out.ctypes.data)
         check("ssdq_flash_attention_f32", rc)
         return out
+
+
+# ------------------------------------------------- resident weights + layer
+
+class WeightStore:
+    """GGUF tensors resident in HBM (ssdq_weights_*), uploaded once, found by
+    name: the replacement of SsdStreamer::load_layer (src/ssd/streamer.rs:43-66),
+    which dequantizes every tensor of a layer to f32 on each load."""
+
+    def __init__(self, device: int = -1):
+        h = _vp()
+        check("ssdq_weights_create", lib().ssdq_weights_create(device, ctypes.byref(h)))
+        self._h = h
+
+    @property
+    def handle(self):
+        return self._h
+
+    def put(self, name: str, dtype: int, dims, data) -> int:
+        """dims as GGUF lists them (row length first); data: the raw bytes
+        (bytes, or a numpy array whose buffer is the tensor's bytes).
+        Returns the bytes uploaded."""
+        import numpy as np
+        buf = np.ascontiguousarray(np.frombuffer(data, np.uint8) if isinstance(data, (bytes, bytearray))
+                                   else data).view(np.uint8).ravel()
+        d = (_c.c_uint64 * len(dims))(*[int(v) for v in dims])
+        check("ssdq_weights_put", lib().ssdq_weights_put(self._h, name.encode(), dtype, d, len(dims),
+                                                         buf.ctypes.data, buf.nbytes))
+        return buf.nbytes
+
+    def load_layer(self, tensors, layer_idx: int) -> int:
+        """Uploads the tensors of one layer (GgufFile::layer_tensors: names
+        starting "blk.{layer_idx}.", gguf.rs:410-416) from (name, dtype, dims,
+        data) tuples; returns the bytes made resident (CachedLayer::size_bytes)."""
+        prefix = f"blk.{layer_idx}."
+        return sum(self.put(name, dtype, dims, data) for name, dtype, dims, data in tensors
+                   if name.startswith(prefix))
+
+    def find(self, name: str):
+        """(device address, dtype, dims, bytes) or None."""
+        dt, nd, nb = _i(), _sz(), _sz()
+        dims = (_c.c_uint64 * 4)()
+        p = lib().ssdq_weights_find(self._h, name.encode(), ctypes.byref(dt), dims, ctypes.byref(nd),
+                                    ctypes.byref(nb))
+        if not p:
+            return None
+        return p, dt.value, tuple(dims[:nd.value]), nb.value
+
+    def __len__(self):
+        return lib().ssdq_weights_count(self._h)
+
+    @property
+    def nbytes(self) -> int:
+        return lib().ssdq_weights_bytes(self._h)
+
+    def close(self):
+        if getattr(self, "_h", None) and self._h.value:
+            lib().ssdq_weights_destroy(self._h)
+            self._h = _vp()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def layer_config(n_embd, n_head, n_head_kv, head_dim, n_ff, rope_theta, norm_eps=1e-5) -> LayerConfig:
+    return LayerConfig(n_embd, n_head, n_head_kv, head_dim, n_ff, rope_theta, norm_eps)
+
+
+def decode_layer_scratch(cfg: LayerConfig):
+    """(bytes, {stage name: byte offset}) of ssdq_decode_layer_dev's scratch."""
+    offs = (_sz * len(LAYER_STAGES))()
+    n = lib().ssdq_decode_layer_scratch_bytes(ctypes.byref(cfg), offs)
+    if n == 0:
+        raise SsdqError("ssdq_decode_layer_scratch_bytes", -1, "bad layer config")
+    return n, dict(zip(LAYER_STAGES, offs))
+
+
+def decode_layer(store: WeightStore, layer: int, cfg: LayerConfig, hidden, position, k_codes, k_scales, v_codes,
+                 v_scales, block_size, block_table, max_blocks_per_seq, slot_mapping, ctx_len, max_ctx,
+                 scratch=None, stream=None):
+    nbytes = scratch.numel() * scratch.element_size() if scratch is not None else 0
+    return check("ssdq_decode_layer_dev",
+                 lib().ssdq_decode_layer_dev(store.handle, layer, ctypes.byref(cfg), _ptr(hidden), position,
+                                             _ptr(k_codes), _ptr(k_scales), _ptr(v_codes), _ptr(v_scales),
+                                             block_size, _ptr(block_table), max_blocks_per_seq, _ptr(slot_mapping),
+                                             _ptr(ctx_len), max_ctx, _ptr(scratch), nbytes, _stream(stream)))

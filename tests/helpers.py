@@ -3,6 +3,8 @@ import os
 
 import numpy as np
 
+import ssdq_oracle as o
+
 # (test id, what, substituted outputs, outputs) of every assert_close_attributed
 # call in this process; tests/conftest.py prints them in the terminal summary.
 SUBSTITUTIONS = []
@@ -94,3 +96,58 @@ def from_dev(t):
 def announce(*what):
     """Names the case on stdout before a GPU step (flushed, so it survives a crash)."""
     print("[gpu case]", *what, flush=True)
+
+
+# ---------------------------------------------- propagated tolerance bounds
+# RoPE and SwiGLU combine two projections, and a small output can come from
+# large inputs (a rotated pair near cancellation; silu(g) ~ 100 times u ~
+# 0.007), so their outputs are held to the projection tolerance propagated
+# through the epilogue, against the composition in double precision over the
+# exact projections:
+#   RoPE    |d o| <= tol(o) + |cos| tol(a0) + |sin| tol(a1)
+#   SwiGLU  |d h| <= tol(h) + |silu(g)| tol(u) + |silu'(g) u| tol(g)
+
+def rope_double(v, head_dim, position, theta):
+    """RoPE in double precision with the oracle's own fp32 cos / sin of each
+    pair's angle (rotating (1, 0) returns them), applied to exact values."""
+    cs = np.empty((head_dim // 2, 2))
+    for i in range(head_dim // 2):
+        e = np.zeros(head_dim, np.float32)
+        e[2 * i] = 1.0
+        r = o.rope_multi_head(e, head_dim, 1, position, theta)
+        cs[i] = r[2 * i], r[2 * i + 1]
+    v = np.asarray(v, np.float64).copy()
+    i = (np.arange(0, len(v), 2) % head_dim) // 2
+    c, s = cs[i, 0], cs[i, 1]
+    a0, a1 = v[0::2].copy(), v[1::2].copy()
+    v[0::2], v[1::2] = a0 * c - a1 * s, a0 * s + a1 * c
+    return v
+
+
+def assert_propagated(gpu, exact, extra, what):
+    gpu = np.asarray(gpu, np.float64)
+    bound = tol(exact) + extra
+    bad = np.abs(gpu - exact) > bound
+    assert not bad.any(), (f"{what}: {int(bad.sum())} of {gpu.size} outside; first {int(np.argmax(bad))}: "
+                           f"gpu={gpu[bad][0]!r} exact={exact[bad][0]!r} bound={bound[bad][0]!r}")
+
+
+def rope_bound(a_exact, head_dim, position, theta):
+    """tol(a0) |cos| + tol(a1) |sin| for each rotated output"""
+    r = rope_double(np.ones_like(a_exact), head_dim, position, theta)  # (c - s, s + c) per pair
+    c = (r[0::2] + r[1::2]) / 2
+    s = (r[1::2] - r[0::2]) / 2
+    t0, t1 = tol(a_exact[0::2]), tol(a_exact[1::2])
+    out = np.empty_like(a_exact, dtype=np.float64)
+    out[0::2] = np.abs(c) * t0 + np.abs(s) * t1
+    out[1::2] = np.abs(s) * t0 + np.abs(c) * t1
+    return out
+
+
+def swiglu_propagated(g, u):
+    """(silu(g) * u in double, the propagated part of its bound) for exact g, u"""
+    g = np.asarray(g, np.float64)
+    u = np.asarray(u, np.float64)
+    sig = 0.5 * (1 + np.tanh(0.5 * g))  # the logistic function, without overflow
+    dsilu = sig * (1 + g * (1 - sig))
+    return g * sig * u, np.abs(g * sig) * tol(u) + np.abs(dsilu * u) * tol(g)

@@ -93,3 +93,33 @@ def test_noalloc_attention_rejects_oversized_partials_before_launch():
     rc = lib.ssdq_paged_attention_int8_noalloc_dev(p, p, p, p, p, p, p, p, 4096, 64, 8, 128, 16, 64, 1024, None)
     assert rc == -1
     assert "scratch" in ssdq.last_error()
+
+
+def test_weight_store_and_layer_layout_on_the_host():
+    lib = ssdq.lib()
+    try:
+        import torch
+        gpu = torch.cuda.is_available()
+    except ImportError:
+        gpu = False
+    if not gpu:
+        h = ctypes.c_void_p()
+        assert lib.ssdq_weights_create(-1, ctypes.byref(h)) == -4 and not h.value
+    # NULL store / hidden state: argument errors before any HIP call
+    cfg = ssdq.layer_config(4096, 32, 8, 128, 14336, 500000.0)
+    assert lib.ssdq_decode_layer_dev(None, 0, ctypes.byref(cfg), None, 0, *([None] * 4), 16, None, 1, None, None,
+                                     16, None, 0, None) == -1
+    assert lib.ssdq_weights_find(None, b"blk.0.attn_q.weight", None, None, None, None) is None
+    assert lib.ssdq_weights_count(None) == 0 and lib.ssdq_weights_device(None) == -1
+    # the scratch layout: one 256-byte aligned region per step, in order
+    n, offs = ssdq.decode_layer_scratch(cfg)
+    sizes = dict(attn_in=4096, q=4096, k=1024, v=1024, attn=4096, attn_out=4096, ffn_in=4096, ffn_h=14336,
+                 ffn_gate=14336, ffn_up=14336, ffn_out=4096, norm_w=8192)
+    at = 0
+    for name in ssdq.LAYER_STAGES:
+        assert offs[name] == at and at % 256 == 0
+        at += -(-4 * sizes[name] // 256) * 256
+    assert n == at
+    # head sizes outside the attention kernels', and n_head not a multiple of n_head_kv
+    for bad in (ssdq.layer_config(4096, 32, 8, 96, 14336, 1e4), ssdq.layer_config(4096, 30, 8, 128, 14336, 1e4)):
+        assert lib.ssdq_decode_layer_scratch_bytes(ctypes.byref(bad), None) == 0

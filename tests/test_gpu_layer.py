@@ -24,49 +24,13 @@ import torch
 
 import ssdq
 import ssdq_oracle as o
-from helpers import announce, assert_close, assert_close_attributed, empty_dev, from_dev, to_dev, tol
+from helpers import (announce, assert_close, assert_close_attributed, assert_propagated, empty_dev, from_dev,
+                     rope_bound, rope_double, swiglu_propagated, to_dev, tol)
 from ssdq import synth
 
 pytestmark = pytest.mark.gpu
 
 Q4_K, Q6_K, Q8_0, Q4_0, Q5_K = ssdq.Q4_K, ssdq.Q6_K, ssdq.Q8_0, ssdq.Q4_0, ssdq.Q5_K
-
-
-def rope_double(v, head_dim, position, theta):
-    """RoPE in double precision with the oracle's own fp32 cos / sin of each
-    pair's angle (rotating (1, 0) returns them), applied to exact values."""
-    cs = np.empty((head_dim // 2, 2))
-    for i in range(head_dim // 2):
-        e = np.zeros(head_dim, np.float32)
-        e[2 * i] = 1.0
-        r = o.rope_multi_head(e, head_dim, 1, position, theta)
-        cs[i] = r[2 * i], r[2 * i + 1]
-    v = np.asarray(v, np.float64).copy()
-    i = (np.arange(0, len(v), 2) % head_dim) // 2
-    c, s = cs[i, 0], cs[i, 1]
-    a0, a1 = v[0::2].copy(), v[1::2].copy()
-    v[0::2], v[1::2] = a0 * c - a1 * s, a0 * s + a1 * c
-    return v
-
-
-def assert_propagated(gpu, exact, extra, what):
-    gpu = np.asarray(gpu, np.float64)
-    bound = tol(exact) + extra
-    bad = np.abs(gpu - exact) > bound
-    assert not bad.any(), (f"{what}: {int(bad.sum())} of {gpu.size} outside; first {int(np.argmax(bad))}: "
-                           f"gpu={gpu[bad][0]!r} exact={exact[bad][0]!r} bound={bound[bad][0]!r}")
-
-
-def rope_bound(a_exact, head_dim, position, theta):
-    """tol(a0) |cos| + tol(a1) |sin| for each rotated output"""
-    r = rope_double(np.ones_like(a_exact), head_dim, position, theta)  # (c - s, s + c) per pair
-    c = (r[0::2] + r[1::2]) / 2
-    s = (r[1::2] - r[0::2]) / 2
-    t0, t1 = tol(a_exact[0::2]), tol(a_exact[1::2])
-    out = np.empty_like(a_exact, dtype=np.float64)
-    out[0::2] = np.abs(c) * t0 + np.abs(s) * t1
-    out[1::2] = np.abs(s) * t0 + np.abs(c) * t1
-    return out
 
 
 QKV = [
@@ -121,10 +85,7 @@ def test_swiglu(dtype, n_embd):
     ref = o.swiglu(dtype, wg, wu, x, n_ff, n_embd)
     g = o.matvec_exact(dtype, wg, x, n_ff, n_embd)
     u = o.matvec_exact(dtype, wu, x, n_ff, n_embd)
-    sig = 0.5 * (1 + np.tanh(0.5 * g))  # the logistic function, without overflow
-    ex = g * sig * u
-    dsilu = sig * (1 + g * (1 - sig))
-    extra = np.abs(g * sig) * tol(u) + np.abs(dsilu * u) * tol(g)
+    ex, extra = swiglu_propagated(g, u)
     assert_propagated(from_dev(h), ex, extra, "swiglu")
     # most outputs also sit within the plain tolerance of the fp32 reference
     assert np.mean(np.abs(from_dev(h) - ref) <= tol(ref)) > 0.99

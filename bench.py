@@ -334,6 +334,68 @@ def gemm_layer(torch, ssdq, synth):
     return layer_fused, flops
 
 
+def decode_layer_case(torch, ssdq, synth, timer, ctx=4096):
+    """One Llama-3-8B decoder layer for one token from resident weights
+    (ssdq_decode_layer_dev): Q4_K projections, Q6_K down, `ctx` earlier tokens
+    in the layer's paged INT8 pool (block 16).  Layers are rotated over copies
+    larger than twice the last-level cache.  Algorithmic bytes: the layer's
+    weight bytes, the K/V codes and scales of ctx + 1 tokens, and the block
+    table; the activations (tens of KB) are left out."""
+    import numpy as np
+    n_embd, n_head, n_kv, hd, n_ff, bs = 4096, 32, 8, 128, 14336, 16
+    kv_dim = n_kv * hd
+    types = {"attn_q": ssdq.Q4_K, "attn_k": ssdq.Q4_K, "attn_v": ssdq.Q4_K, "attn_output": ssdq.Q4_K,
+             "ffn_gate": ssdq.Q4_K, "ffn_up": ssdq.Q4_K, "ffn_down": ssdq.Q6_K}
+    t = synth.decoder_layer(n_embd, n_head, n_kv, hd, n_ff, types, synth.seed(7, 0))
+    g = synth.rng(synth.seed(7, 20))
+    norms = [(0.5 + g.random(n_embd)).astype(np.float32) for _ in range(2)]
+    wbytes = sum(v[2].nbytes for v in t.values()) + 2 * 4 * n_embd
+    max_blocks = (ctx + 1 + bs - 1) // bs
+    kvbytes = (ctx + 1) * (2 * kv_dim + 8) + 4 * max_blocks
+    n = copies_for(wbytes)
+    store = ssdq.WeightStore()
+    for layer in range(n):
+        for name, (dt, dims, raw) in t.items():
+            store.put(f"blk.{layer}.{name}.weight", dt, dims, raw)
+        store.put(f"blk.{layer}.attn_norm.weight", ssdq.F32, (n_embd,), norms[0])
+        store.put(f"blk.{layer}.ffn_norm.weight", ssdq.F32, (n_embd,), norms[1])
+    # per layer: a pool of max_blocks physical blocks behind a shuffled table,
+    # the earlier tokens' codes random, scales ~ U[0.01, 0.03]
+    pools = []
+    for layer in range(n):
+        rows = max_blocks * bs
+        pools.append((torch.randint(-127, 128, (rows * kv_dim,), dtype=torch.int8, device="cuda"),
+                      torch.rand(rows, device="cuda") * 0.02 + 0.01,
+                      torch.randint(-127, 128, (rows * kv_dim,), dtype=torch.int8, device="cuda"),
+                      torch.rand(rows, device="cuda") * 0.02 + 0.01,
+                      torch.from_numpy(g.permutation(max_blocks).astype(np.int32)).cuda()))
+    tables = [p[4].cpu().numpy() for p in pools]
+    slots = [torch.tensor([int(tb[ctx // bs]) * bs + ctx % bs], dtype=torch.int32, device="cuda") for tb in tables]
+    ctx_len = torch.tensor([ctx + 1], dtype=torch.int32, device="cuda")
+    cfg = ssdq.layer_config(n_embd, n_head, n_kv, hd, n_ff, 500000.0, 1e-5)
+    sbytes, _ = ssdq.decode_layer_scratch(cfg)
+    scratch = torch.zeros(sbytes, dtype=torch.uint8, device="cuda")
+    hidden = torch.randn(n_embd, device="cuda")
+
+    def step(i):
+        layer = i % n
+        kc, ks, vc, vs, bt = pools[layer]
+        ssdq.decode_layer(store, layer, cfg, hidden, ctx, kc, ks, vc, vs, bs, bt, max_blocks, slots[layer],
+                          ctx_len, max_blocks * bs, scratch=scratch)
+
+    tr = timer.run(step, 100, 200)
+    per = tr["t_median"] / tr["steps"]
+    nbytes = wbytes + kvbytes
+    ok = bool(torch.isfinite(hidden).all())
+    del pools, scratch
+    store.close()
+    torch.cuda.empty_cache()
+    return {"us": round(per * 1e6, 2), "GB/s": round(nbytes / per / 1e9, 1),
+            "pct_hbm_peak": round(100 * nbytes / per / 1e9 / HBM_PEAK_GBS, 2), "bytes": nbytes,
+            "layers_rotated": n, "context": ctx, "hidden_finite": ok,
+            "note": "ssdq_decode_layer_dev: 9 steps, 10 kernel launches (the residual add folded into the down projection), one HIP graph replay per 50 layers"}
+
+
 def attention_case(torch, ssdq, synth, codes, scales):
     """Config 5b on an INT8 pool (codes [2 * 8 * 32768, 1024]: K rows, then V rows)."""
     n_seq, n_head, n_kv, hd, bs, ctx = 8, 32, 8, 128, 16, 32768
@@ -504,6 +566,7 @@ def extras(torch, ssdq, synth, timer, np):
     layer_case("decode_qkv_rope_q4k_4096", [(ssdq.Q4_K, 4096), (ssdq.Q4_K, 1024), (ssdq.Q4_K, 1024)], qkv)
     layer_case("decode_swiglu_q4k_14336x4096", [(ssdq.Q4_K, 14336), (ssdq.Q4_K, 14336)], swi)
     layer_case("decode_output_head_rmsnorm_q6k_128256x4096", [(ssdq.Q6_K, 128256)], head)
+    out["decode_layer_llama3_8b_q4k_ctx4096"] = decode_layer_case(torch, ssdq, synth, timer)
 
     # INT8 KV swap slots: 1024 blocks of 16 tokens x 1024 (one layer of a 16k-token
     # context) gathered into the reference's slot format and scattered back

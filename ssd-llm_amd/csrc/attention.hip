@@ -540,53 +540,89 @@ __global__ __launch_bounds__(64 * NWV, HD == 256 ? 1 : 8 / NWV) void paged_attn_
   }
 }
 
-// Log-sum-exp merge of the split partials of one (sequence, head): the split
-// maxima and weights are reduced once in LDS, then every thread sums its
-// dimension over the splits with independent loads.
+// Log-sum-exp merge of the split partials of one (sequence, head).  The block
+// is CG groups of HD threads: thread (g, d) folds splits g, g + CG, g + 2 CG,
+// ... into a running (max, sum, acc[d]), a chunk of 8 splits at a time with
+// the next chunk's loads issued before the current one is folded (indices
+// clamped, so every load is unconditional; splits past the end are masked
+// after loading).  The CG running triples are then merged through LDS.  One
+// memory round trip for up to 8 CG splits, where a max / weights / sum pass
+// over the partials would take three.
 constexpr int kMaxSplits = 1024;
 
 template <int HD>
-__global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ partial,
-                                                           int n_splits, int n_head,
-                                                           float* __restrict__ out) {
-  __shared__ float w_s[kMaxSplits];
-  __shared__ float red[256 / 64];
-  const int h = blockIdx.x, seq = blockIdx.y, tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+constexpr int combine_groups() {
+  return HD >= 256 ? 2 : 512 / HD;
+}
+
+template <int HD>
+__global__ __launch_bounds__(HD * combine_groups<HD>()) void attn_combine_kernel(const float* __restrict__ partial,
+                                                                               int n_splits, int n_head,
+                                                                               float* __restrict__ out) {
+  constexpr int CG = combine_groups<HD>(), CH = 8;
+  __shared__ float m_s[CG], l_s[CG];
+  __shared__ float a_s[CG][HD];
+  const int h = blockIdx.x, seq = blockIdx.y;
+  const int d = threadIdx.x % HD, g = threadIdx.x / HD;
   const float* rec = partial + ((size_t)seq * n_head + h) * n_splits * (HD + 2);
-  // 1. global maximum of the split maxima
-  float m = -INFINITY;
-  for (int s = tid; s < n_splits; s += 256) m = fmaxf(m, rec[(size_t)s * (HD + 2)]);
-  m = wave_max(m);
-  if (lane == 0) red[wave] = m;
-  __syncthreads();
-  const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  __syncthreads();
-  // 2. split weights exp(m_s - M) and the total l
-  float l = 0.f;
-  for (int s = tid; s < n_splits; s += 256) {
-    const float ms = rec[(size_t)s * (HD + 2)];
-    const float w = (M == -INFINITY || ms == -INFINITY) ? 0.f : __expf(ms - M);
-    w_s[s] = w;
-    l = fmaf(w, rec[(size_t)s * (HD + 2) + 1], l);
-  }
-  l = wave_sum(l);
-  if (lane == 0) red[wave] = l;
-  __syncthreads();
-  const float L = (red[0] + red[1]) + (red[2] + red[3]);
-  // 3. out[d] = sum_s w_s acc_s[d] / L
-  for (int d = tid; d < HD; d += 256) {
-    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-    int s = 0;
-    for (; s + 4 <= n_splits; s += 4) {
-      a0 = fmaf(w_s[s], rec[(size_t)s * (HD + 2) + 2 + d], a0);
-      a1 = fmaf(w_s[s + 1], rec[(size_t)(s + 1) * (HD + 2) + 2 + d], a1);
-      a2 = fmaf(w_s[s + 2], rec[(size_t)(s + 2) * (HD + 2) + 2 + d], a2);
-      a3 = fmaf(w_s[s + 3], rec[(size_t)(s + 3) * (HD + 2) + 2 + d], a3);
+  float M = -INFINITY, L = 0.f, A = 0.f;
+  float mc[CH], lc[CH], ac[CH];
+  auto load = [&](float (&m)[CH], float (&l)[CH], float (&a)[CH], int c0) {
+#pragma unroll
+    for (int u = 0; u < CH; u++) {
+      const int sp = g + (c0 + u) * CG;
+      const float* r = rec + (size_t)min(sp, n_splits - 1) * (HD + 2);
+      m[u] = r[0];
+      l[u] = r[1];
+      a[u] = r[2 + d];
     }
-    for (; s < n_splits; s++) a0 = fmaf(w_s[s], rec[(size_t)s * (HD + 2) + 2 + d], a0);
-    const float a = (a0 + a1) + (a2 + a3);
-    out[((size_t)seq * n_head + h) * HD + d] = L > 0.f ? a * (1.0f / L) : 0.f;
+#pragma unroll
+    for (int u = 0; u < CH; u++)
+      if (g + (c0 + u) * CG >= n_splits) m[u] = -INFINITY;
+  };
+  const int per = g < n_splits ? (n_splits - g + CG - 1) / CG : 0;  // this group's splits
+  load(mc, lc, ac, 0);
+  for (int c0 = 0; c0 < per; c0 += CH) {
+    float mn[CH], ln[CH], an[CH];
+    load(mn, ln, an, c0 + CH);
+    float cm = M;
+#pragma unroll
+    for (int u = 0; u < CH; u++) cm = fmaxf(cm, mc[u]);
+    const float f = cm == -INFINITY ? 1.f : __expf(M - cm);
+    L *= f;
+    A *= f;
+#pragma unroll
+    for (int u = 0; u < CH; u++) {
+      const float w = mc[u] == -INFINITY ? 0.f : __expf(mc[u] - cm);
+      L = fmaf(w, lc[u], L);
+      A = fmaf(w, ac[u], A);
+    }
+    M = cm;
+#pragma unroll
+    for (int u = 0; u < CH; u++) {
+      mc[u] = mn[u];
+      lc[u] = ln[u];
+      ac[u] = an[u];
+    }
+  }
+  if (d == 0) {
+    m_s[g] = M;  // every thread of the group holds the same M and L
+    l_s[g] = L;
+  }
+  a_s[g][d] = A;
+  __syncthreads();
+  if (g == 0) {
+    float mx = m_s[0];
+#pragma unroll
+    for (int i = 1; i < CG; i++) mx = fmaxf(mx, m_s[i]);
+    float lt = 0.f, at = 0.f;
+#pragma unroll
+    for (int i = 0; i < CG; i++) {
+      const float w = m_s[i] == -INFINITY ? 0.f : __expf(m_s[i] - mx);
+      lt = fmaf(w, l_s[i], lt);
+      at = fmaf(w, a_s[i][d], at);
+    }
+    out[((size_t)seq * n_head + h) * HD + d] = lt > 0.f ? at * (1.0f / lt) : 0.f;
   }
 }
 
@@ -609,7 +645,7 @@ hipError_t run_attn(const float* q, Src src, const int32_t* tables, const int32_
                      pe, split_len, n_splits, partial);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3(n_head, n_seq), dim3(256), 0, s, partial,
+  hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3(n_head, n_seq), dim3(HD * combine_groups<HD>()), 0, s, partial,
                      n_splits, n_head, out);
   return hipGetLastError();
 }
@@ -687,7 +723,7 @@ hipError_t run_paged_mfma(const PagedAttnArgs& a, float* part, hipStream_t s) {
     e0 = go(std::integral_constant<int, 4>{}, a.n_head_kv % 4 == 0);
   }
   if (e0 != hipSuccess) return e0;
-  hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3(a.n_head, a.n_seq), dim3(256), 0, s, part,
+  hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3(a.n_head, a.n_seq), dim3(HD * combine_groups<HD>()), 0, s, part,
                      n_splits, a.n_head, a.out);
   return hipGetLastError();
 }

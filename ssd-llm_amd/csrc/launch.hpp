@@ -18,6 +18,12 @@ hipError_t launch_dequant(int dtype, const uint8_t* w, size_t n_blocks, float* o
 hipError_t launch_matvec(int dtype, const uint8_t* w, const float* x, float* y, size_t out_dim,
                          size_t in_dim, size_t batch, hipStream_t stream, void* workspace = nullptr,
                          size_t workspace_bytes = 0);
+// acc[r] += sum_k W[r,k] x[k] (batch 1; Q4_0 / Q8_0 / Q4_K / Q6_K), with y
+// receiving the plain product: the residual add of a decoder layer folded
+// into the K-sliced matvec's slice reduction (acc = acc + y, the same fp32 add
+// as a separate residual kernel).  acc may not alias x or y.
+hipError_t launch_matvec_acc(int dtype, const uint8_t* w, const float* x, float* acc, float* y, size_t out_dim,
+                             size_t in_dim, hipStream_t s, void* workspace, size_t workspace_bytes);
 // Device workspace launch_matvec uses for these operands (batch-1 K slices).
 size_t matvec_workspace_bytes(int dtype, const void* w, const float* x, size_t out_dim,
                               size_t in_dim, size_t batch);

@@ -874,9 +874,11 @@ __global__ __launch_bounds__(768) void mv_b1(const uint8_t* __restrict__ w,
   }
 }
 
-__global__ __launch_bounds__(256) void slice_reduce_kernel(const float* __restrict__ part,
-                                                           float* __restrict__ y, int n,
-                                                           int slices) {
+// With res non-null, y = res + (the slice sum), the residual add of a decoder
+// layer (y may alias res: each thread reads its element before writing it),
+// and the slice sum itself also goes to sum_out.
+__global__ __launch_bounds__(256) void slice_reduce_kernel(const float* __restrict__ part, float* y, int n,
+                                                           int slices, const float* res, float* sum_out) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   // Eight slice loads are in flight together (addresses clamped, so the
@@ -890,7 +892,12 @@ __global__ __launch_bounds__(256) void slice_reduce_kernel(const float* __restri
     for (int k = 0; k < 8; k++)
       if (z0 + k < slices) s = z0 + k == 0 ? v[k] : s + v[k];
   }
-  y[i] = s;
+  if (res) {
+    y[i] = res[i] + s;
+    sum_out[i] = s;
+  } else {
+    y[i] = s;
+  }
 }
 
 // Small batches (NB = 2..8 activation rows) on the digit-plane scheme.  The
@@ -1352,9 +1359,11 @@ size_t b1_workspace_floats(int out_dim, int bpr) {
   return p.slices > 1 ? (size_t)p.slices * out_dim : 0;
 }
 
+// acc non-null: acc += W x instead of y = W x, with y as scratch for the
+// unsliced plan (K-sliced rows add acc in the slice reduction itself).
 template <int F>
 hipError_t b1_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, int bpr,
-                       hipStream_t s, float* ws, size_t ws_floats, bool* used) {
+                       hipStream_t s, float* ws, size_t ws_floats, bool* used, float* acc = nullptr) {
   const int U = bpr * Geom<F>::bs / FastUnit<F>::E;
   if (U == 0) return hipSuccess;
   const B1Plan<F> p = b1_plan<F>(bpr, out_dim);
@@ -1410,9 +1419,10 @@ hipError_t b1_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, 
     *used = false;
     return hipSuccess;
   }
-  if (e != hipSuccess || p.slices == 1) return e;
+  if (e != hipSuccess) return e;
+  if (p.slices == 1) return acc ? launch_residual_add(acc, y, out_dim, s) : hipSuccess;
   hipLaunchKernelGGL(slice_reduce_kernel, dim3((unsigned)((out_dim + 255) / 256)), dim3(256), 0, s,
-                     ws, y, out_dim, p.slices);
+                     ws, acc ? acc : y, out_dim, p.slices, (const float*)acc, y);
   return hipGetLastError();
 }
 
@@ -1609,7 +1619,7 @@ hipError_t bn_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, 
   if (p.slices == 1) return hipSuccess;
   const int n = NB * out_dim;
   hipLaunchKernelGGL(slice_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, ws, y, n,
-                     p.slices);
+                     p.slices, nullptr, nullptr);
   return hipGetLastError();
 }
 
@@ -1797,6 +1807,32 @@ size_t matvec_workspace_bytes(int dtype, const void* w, const float* x, size_t o
     default: break;
   }
   return n * sizeof(float);
+}
+
+hipError_t launch_matvec_acc(int dtype, const uint8_t* w, const float* x, float* acc, float* y, size_t out_dim,
+                             size_t in_dim, hipStream_t s, void* workspace, size_t workspace_bytes) {
+  if (out_dim == 0) return hipSuccess;
+  bool used = false;
+  hipError_t e = hipSuccess;
+  const int od = (int)out_dim, id = (int)in_dim;
+  float* ws = static_cast<float*>(workspace);
+  const size_t wf = workspace_bytes / sizeof(float);
+  auto go = [&](auto f_c, int bpr) {
+    constexpr int F = decltype(f_c)::value;
+    if (bpr == 0 || !fast_aligned<F>(w, x, id, bpr)) return hipSuccess;
+    return b1_dispatch<F>(w, x, y, od, bpr, s, ws, wf, &used, acc);
+  };
+  switch (dtype) {
+    case kQ4_0: e = go(std::integral_constant<int, kQ4_0>{}, id / 32); break;
+    case kQ8_0: e = go(std::integral_constant<int, kQ8_0>{}, id / 32); break;
+    case kQ4_K: e = go(std::integral_constant<int, kQ4_K>{}, id / 256); break;
+    case kQ6_K: e = go(std::integral_constant<int, kQ6_K>{}, id / 256); break;
+    default: return hipErrorInvalidValue;
+  }
+  if (e != hipSuccess || used) return e;
+  e = launch_matvec(dtype, w, x, y, out_dim, in_dim, 1, s, workspace, workspace_bytes);
+  if (e != hipSuccess) return e;
+  return launch_residual_add(acc, y, od, s);
 }
 
 hipError_t launch_matvec(int dtype, const uint8_t* w, const float* x, float* y, size_t out_dim,

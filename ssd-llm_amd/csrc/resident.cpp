@@ -419,9 +419,21 @@ int ssdq_decode_layer_dev(const ssdq_weights* w, uint32_t layer, const ssdq_laye
       if ((e = ssdq::launch_swiglu(gate, up, h, (int)n_ff, s)) != hipSuccess)
         return api_hip_fail(e, "ssdq_decode_layer_dev: swiglu");
     }
-    if (take(ssdq_matvec_dev(t_d->dtype, t_d->dev, h, fo, n_embd, n_ff, 1, stream))) return worst;
-    if ((e = ssdq::launch_residual_add(hidden, fo, (int)n_embd, s)) != hipSuccess)
-      return api_hip_fail(e, "ssdq_decode_layer_dev: residual");
+    const int dd = t_d->dtype;
+    if (dd == SSDQ_TYPE_Q4_0 || dd == SSDQ_TYPE_Q8_0 || dd == SSDQ_TYPE_Q4_K || dd == SSDQ_TYPE_Q6_K) {
+      // hidden += W_down h inside the K-sliced matvec's slice reduction (fo
+      // still receives W_down h)
+      const size_t wsb = ssdq::matvec_workspace_bytes(dd, t_d->dev, h, n_embd, n_ff, 1);
+      void* ws = nullptr;
+      if (wsb && (e = ssdq::api_workspace(wsb, s, &ws, 0)) != hipSuccess)
+        return api_hip_fail(e, "ssdq_decode_layer_dev: workspace");
+      e = ssdq::launch_matvec_acc(dd, (const uint8_t*)t_d->dev, h, hidden, fo, n_embd, n_ff, s, ws, wsb);
+      if (e != hipSuccess) return api_hip_fail(e, "ssdq_decode_layer_dev: down projection");
+    } else {
+      if (take(ssdq_matvec_dev(dd, t_d->dev, h, fo, n_embd, n_ff, 1, stream))) return worst;
+      if ((e = ssdq::launch_residual_add(hidden, fo, (int)n_embd, s)) != hipSuccess)
+        return api_hip_fail(e, "ssdq_decode_layer_dev: residual");
+    }
   }
   if (worst == SSDQ_OK) api_ok();
   return worst;

@@ -129,3 +129,40 @@ def slot_mapping(tables: np.ndarray, ctx_lens, block_size: int) -> np.ndarray:
 # Seeds per configuration (stable across tests and the benchmark)
 def seed(config: int, tensor: int) -> int:
     return 0x55D00000 + 16 * config + tensor
+
+
+# byte offsets of the f16 super-block scales (d, dmin) inside one block
+SCALE_FIELDS = {Q4_0: (0,), Q8_0: (0,), Q4_K: (0, 2), Q5_K: (0, 2), Q6_K: (208,)}
+
+
+def signed_blocks(dtype: int, raw: np.ndarray, shift: int, seed: int) -> np.ndarray:
+    """The same blocks with their f16 scales times +-2^-shift, the sign drawn
+    per block and shared by the block's scales (which negates every element
+    of the block).  quant_weights' Q4_K blocks have a positive mean element;
+    with random signs the weights are zero-mean, as trained ones are, so that
+    chained projections of O(1) inputs stay O(1) (a decoder layer)."""
+    bb = BLOCK[dtype][1]
+    b = raw.reshape(-1, bb).copy()
+    sign = np.where(rng(seed).random(len(b)) < 0.5, -1.0, 1.0).astype(np.float16)
+    for off in SCALE_FIELDS[dtype]:
+        f = np.ascontiguousarray(b[:, off:off + 2]).view(np.float16)[:, 0]
+        b[:, off:off + 2] = (f * (sign * np.float16(2.0 ** -shift)))[:, None].view(np.uint8)
+    return b.ravel()
+
+
+def decoder_layer(n_embd: int, n_head: int, n_kv: int, head_dim: int, n_ff: int, types: dict, seed: int):
+    """Projections of one decoder layer as {GGUF suffix: (dtype, (in, out), raw)}
+    with zero-mean blocks scaled so that each projection maps O(1) inputs to
+    O(1) outputs (attn_k one more power of two down: the softmax spreads over
+    a few to a few tens of positions)."""
+    q_dim, kv_dim = n_head * head_dim, n_kv * head_dim
+    shapes = {"attn_q": (n_embd, q_dim), "attn_k": (n_embd, kv_dim), "attn_v": (n_embd, kv_dim),
+              "attn_output": (q_dim, n_embd), "ffn_gate": (n_embd, n_ff), "ffn_up": (n_embd, n_ff),
+              "ffn_down": (n_ff, n_embd)}
+    out = {}
+    for i, (name, (k_in, n_out)) in enumerate(shapes.items()):
+        dt = types[name]
+        shift = int(np.ceil(np.log2(k_in) / 2)) + (1 if name == "attn_k" else 0)
+        out[name] = (dt, (k_in, n_out), signed_blocks(dt, quant_weights(dt, n_out, k_in, seed + i), shift,
+                                                      seed + 100 + i))
+    return out

@@ -44,43 +44,14 @@ BLOCK = 16
 E2E_RTOL = 1e-4  # end-to-end bar, relative to the outputs' term scale
 
 
-# byte offsets of the f16 super-block scales (d, dmin) inside one block
-SCALE_FIELDS = {Q4_K: (0, 2), Q6_K: (208,), Q8_0: (0,), Q5_K: (0, 2)}
-
-
-def scale_blocks(dtype, raw, shift, seed):
-    """The same blocks with their f16 scales times +-2^-shift, the sign drawn
-    per block and shared by d and dmin (which negates every element of the
-    block).  Synthetic Q4_K blocks have a positive mean element; with random
-    signs the weights are zero-mean, as trained ones are, and a projection of
-    an O(1) input stays O(1) instead of carrying a common offset that grows
-    layer step by layer step."""
-    b = raw.reshape(-1, ssdq.type_size(dtype)).copy()
-    sign = np.where(synth.rng(seed).random(len(b)) < 0.5, -1.0, 1.0).astype(np.float16)
-    for off in SCALE_FIELDS[dtype]:
-        f = np.ascontiguousarray(b[:, off:off + 2]).view(np.float16)[:, 0]
-        b[:, off:off + 2] = (f * (sign * np.float16(2.0 ** -shift)))[:, None].view(np.uint8)
-    return b.ravel()
-
-
 class Layer:
     """Synthetic weights of one layer: {suffix: (dtype, dims, raw)}."""
 
     def __init__(self, n_embd, n_head, n_kv, hd, n_ff, types, seed, norm_type=F32, drop=()):
         self.n_embd, self.n_head, self.n_kv, self.hd, self.n_ff = n_embd, n_head, n_kv, hd, n_ff
-        q_dim, kv_dim = n_head * hd, n_kv * hd
-        shapes = {"attn_q": (n_embd, q_dim), "attn_k": (n_embd, kv_dim), "attn_v": (n_embd, kv_dim),
-                  "attn_output": (q_dim, n_embd), "ffn_gate": (n_embd, n_ff), "ffn_up": (n_embd, n_ff),
-                  "ffn_down": (n_ff, n_embd)}
-        self.t = {}
-        for i, (name, (k_in, n_out)) in enumerate(shapes.items()):
-            dt = types[name]
-            # outputs ~ sqrt(k_in) 2^-shift times the input's rms (q . k /
-            # sqrt(hd) then spreads the softmax over a few to a few tens of
-            # positions)
-            shift = int(np.ceil(np.log2(k_in) / 2)) + (1 if name == "attn_k" else 0)
-            self.t[name] = (dt, (k_in, n_out), scale_blocks(dt, synth.quant_weights(dt, n_out, k_in, seed + i),
-                                                            shift, seed + 100 + i))
+        # zero-mean blocks (a random sign per block), scaled so that each
+        # projection maps O(1) inputs to O(1) outputs
+        self.t = synth.decoder_layer(n_embd, n_head, n_kv, hd, n_ff, types, seed)
         g = synth.rng(seed + 50)
         for name in ("attn_norm", "ffn_norm"):
             w = (0.5 + g.random(n_embd)).astype(np.float32)

@@ -874,6 +874,69 @@ __global__ __launch_bounds__(768) void mv_b1(const uint8_t* __restrict__ w,
   }
 }
 
+// Batch-1 matvec as long per-wave row streams, for matrices that would take
+// more than one round of mv_b1 workgroups: one workgroup per CU and K slice,
+// wave w of workgroup b a run of consecutive rows (any length, balanced to one
+// row), one unit per lane, D rows in flight in a rolling window of registers
+// (the loop is unrolled by D so every window index is a constant).  Loads past
+// the run repeat its last row (cached, results not stored).  Each row's sum is
+// reduced and stored as soon as it is done.
+template <int F, int D, bool FULL, int SIT>
+__global__ __launch_bounds__(768) void mv_b1s(const uint8_t* __restrict__ w, const float* __restrict__ x,
+                                              float* __restrict__ y, int out_dim, int row_bpr, int slice_bpr) {
+  using FU = FastUnit<F>;
+  using DG = Dig<F>;
+  constexpr int NW = FU::NW, US = DG::US;
+  extern __shared__ uint4 lds4[];
+  uint32_t* lds = reinterpret_cast<uint32_t*>(lds4);
+  const int blk0 = blockIdx.y * slice_bpr;
+  const int bpr = min(slice_bpr, row_bpr - blk0);
+  w += (size_t)blk0 * Geom<F>::bb;
+  x += (size_t)blk0 * Geom<F>::bs;
+  y += (size_t)blockIdx.y * out_dim;
+  const int keff = bpr * Geom<F>::bs;
+  const int U = keff / FU::E;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const size_t row_bytes = (size_t)row_bpr * Geom<F>::bb;
+  const long n_streams = (long)gridDim.x * (blockDim.x >> 6), gs = (long)blockIdx.x * (blockDim.x >> 6) + wave;
+  const int r_begin = (int)(gs * out_dim / n_streams);
+  const int n_rows = (int)((gs + 1) * out_dim / n_streams) - r_begin;
+  const int r_last = r_begin + max(n_rows, 1) - 1;
+  const int u = FULL ? lane : min(lane, U - 1);  // partial rows: the spare lanes repeat the last unit
+
+  uint32_t buf[D][NW];
+  auto load_row = [&](int rr, uint32_t* b) { load_unit<F>(w + (size_t)min(r_begin + rr, r_last) * row_bytes, u, b); };
+
+  XChunks<SIT> st;
+  stage_load<SIT>(x, keff, st, blockDim.x);
+#pragma unroll
+  for (int i = 0; i < D; i++) load_row(i, buf[i]);
+  {
+    constexpr int N = D * loads_per_unit<F>();  // wait for x only
+    static_assert(N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+  }
+  stage_store<F, SIT>(st, keff, lds, blockDim.x);
+  lds_barrier();
+  uint32_t pr[US];
+#pragma unroll
+  for (int t = 0; t < US; t += 4) {
+    const uint4 v = lds4[(size_t)u * (US / 4) + t / 4];
+    pr[t] = v.x; pr[t + 1] = v.y; pr[t + 2] = v.z; pr[t + 3] = v.w;
+  }
+  const bool live = FULL || lane < U;
+  for (int r0 = 0; r0 < n_rows; r0 += D) {
+#pragma unroll
+    for (int i = 0; i < D; i++) {
+      float a = 0.f;
+      accumulate_dig<F>(buf[i], u, [&](int t) { return pr[t]; }, a);
+      load_row(r0 + i + D, buf[i]);
+      a = wave_sum_l63(live ? a : 0.f);
+      if (lane == 63 && r0 + i < n_rows) y[r_begin + r0 + i] = a;
+    }
+  }
+}
+
 // With res non-null, y = res + (the slice sum), the residual add of a decoder
 // layer (y may alias res: each thread reads its element before writing it),
 // and the slice sum itself also goes to sum_out.
@@ -1353,6 +1416,33 @@ B1Plan<F> b1_plan(int bpr, int out_dim) {
   return p;
 }
 
+// mv_b1s launch: one workgroup of 12 waves per CU and K slice (at least one
+// row per wave), two rows in flight per wave.
+template <int F, bool FULL>
+hipError_t run_b1s(const uint8_t* w, const float* x, float* y, int out_dim, int row_bpr, int slice_bpr,
+                   int slices, hipStream_t s) {
+  const int U = slice_bpr * Geom<F>::bs / FastUnit<F>::E;
+  const size_t lds = (size_t)U * Dig<F>::US * sizeof(uint32_t);
+  if (lds > (size_t)lds_limit()) return hipErrorNotSupported;
+  const int sit = (slice_bpr * Geom<F>::bs / 8 + 767) / 768;
+  const long n_wg = std::max<long>(1, std::min<long>(device_cu_count() / slices, (out_dim + 11) / 12));
+  auto go = [&](auto kern) {
+    hipError_t e = set_lds_attr(kern, lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kern, dim3((unsigned)n_wg, (unsigned)slices), dim3(768), lds, s, w, x, y, out_dim, row_bpr,
+                       slice_bpr);
+    return hipGetLastError();
+  };
+  switch (sit) {
+    case 0:
+    case 1: return go(mv_b1s<F, 2, FULL, 1>);
+    case 2: return go(mv_b1s<F, 2, FULL, 2>);
+    case 3:
+    case 4: return go(mv_b1s<F, 2, FULL, 4>);
+    default: return hipErrorNotSupported;
+  }
+}
+
 template <int F>
 size_t b1_workspace_floats(int out_dim, int bpr) {
   const B1Plan<F> p = b1_plan<F>(bpr, out_dim);
@@ -1389,6 +1479,23 @@ hipError_t b1_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, 
   int rsl = 0;
   for (int cand : {2, 4, 5, 6, 8, 10})
     if (!rsl && rounds(cand) == 1) rsl = cand;
+  // Rows cut into 2-4 K slices of one unit per lane, and matrices that take
+  // more than one round of mv_b1 workgroups, run as long per-wave row streams
+  // (mv_b1s), kernel alone: 4096 x 14336 Q4_K 12.9 -> 9.5 us, 8192 x 8192 Q4_K
+  // 11.3 -> 9.8 us, 14336 x 4096 Q6_K 14.1 -> 12.9 us, 28672 x 8192 Q4_K 30.2 ->
+  // 25.6 us.  Whole rows that fit one round (14336 x 4096 Q4_K: 8.4 against
+  // 9.2 us) and rows of 7 slices (4096 x 14336 Q6_K: no gain) stay on mv_b1.
+  if (p.upl == 1 && ((p.slices > 1 && p.slices <= 4) || !rsl)) {
+    e = p.full ? run_b1s<F, true>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, s)
+               : run_b1s<F, false>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, s);
+    if (e != hipErrorNotSupported) {
+      if (e != hipSuccess) return e;
+      if (p.slices == 1) return acc ? launch_residual_add(acc, y, out_dim, s) : hipSuccess;
+      hipLaunchKernelGGL(slice_reduce_kernel, dim3((unsigned)((out_dim + 255) / 256)), dim3(256), 0, s,
+                         ws, acc ? acc : y, out_dim, p.slices, (const float*)acc, y);
+      return hipGetLastError();
+    }
+  }
   if (!rsl) {
     rsl = 5;
     for (int cand : {8, 10})

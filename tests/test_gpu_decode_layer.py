@@ -371,3 +371,95 @@ def test_decode_layer_rejects_mismatched_shapes_before_launch():
             store.put("blk.9.x.weight", Q4_K, (1024, 8), L.w("attn_q")[:100])
     finally:
         store.close()
+
+
+def test_decode_layer_graph_replay_matches_eager():
+    """The layer captured into a HIP graph (after an eager call on the capture
+    stream sizes its workspaces) and replayed, with eager work between the
+    replays: every replay leaves the hidden state and the pool bit-identical
+    to an eager call on the same inputs."""
+    L = Layer(1024, 8, 2, 128, 2816, Q4KM, 4600)
+    cfg = ssdq.layer_config(1024, 8, 2, 128, 2816, 10000.0, EPS)
+    pool = Pool(256, 50, 8, 8, (1.0, 1.0), 4601).upload()
+    hidden0 = synth.rng(4602).standard_normal(1024).astype(np.float32)
+    pos = 50
+    store = ssdq.WeightStore()
+    side = torch.cuda.Stream()
+    try:
+        L.upload(store, 0)
+        h = to_dev(hidden0)
+        h_in = to_dev(hidden0)
+        bt = to_dev(pool.table)
+        sm = to_dev(np.array([pool.slot(pos)], np.int32))
+        cl = to_dev(np.array([pos + 1], np.int32))
+        kc, ks, vc, vs = pool.dev
+
+        def call():
+            return ssdq.decode_layer(store, 0, cfg, h, pos, kc, ks, vc, vs, BLOCK, bt, pool.max_blocks, sm, cl,
+                                     pool.max_blocks * BLOCK, stream=side)
+
+        announce("decode layer: eager reference on the capture stream")
+        torch.cuda.synchronize()
+        with torch.cuda.stream(side):
+            assert call() == 0
+        side.synchronize()
+        ref_h = from_dev(h)
+        ref_pool = pool.from_device()
+        g = torch.cuda.CUDAGraph()
+        h.copy_(h_in)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=side):
+            assert call() == 0
+        torch.cuda.synchronize()
+        for rep in range(3):
+            announce("decode layer: graph replay", rep)
+            h.copy_(h_in)
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert bits_equal(from_dev(h), ref_h), f"replay {rep}: hidden state"
+            for a, b in zip(pool.from_device(), ref_pool):
+                assert bits_equal(a, b), f"replay {rep}: pool"
+            # unrelated eager work on the capture stream between replays
+            with torch.cuda.stream(side):
+                ssdq.rmsnorm(h_in, None, h_in, 1e-5, None, torch.empty_like(h_in), 1024, stream=side)
+            side.synchronize()
+        del g
+        torch.cuda.synchronize()
+    finally:
+        store.close()
+
+
+def test_two_decoder_layers_chained():
+    """Layers 0 and 1 (different weights, one pool each) applied in turn to one
+    token, against the oracle's composition chained the same way; each layer's
+    output held to the end-to-end bar against the oracle run from the device's
+    own input to that layer."""
+    shape = dict(n_embd=2048, n_head=16, n_kv=4, hd=128, n_ff=5632)
+    layers = [Layer(shape["n_embd"], shape["n_head"], shape["n_kv"], shape["hd"], shape["n_ff"], Q4KM, 4700 + 100 * i)
+              for i in range(2)]
+    cfg = ssdq.layer_config(2048, 16, 4, 128, 5632, 500000.0, EPS)
+    nbytes, offs = ssdq.decode_layer_scratch(cfg)
+    scratch = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+    ctx = 123
+    pools = [Pool(512, ctx, 16, 24, (1.0, 1.0), 4800 + i).upload() for i in range(2)]
+    ref_pools = [Pool(512, ctx, 16, 24, (1.0, 1.0), 4800 + i) for i in range(2)]
+    hid = synth.rng(4900).standard_normal(2048).astype(np.float32)
+    store = ssdq.WeightStore()
+    try:
+        for i, L in enumerate(layers):
+            L.upload(store, i)
+        assert len(store) == 18
+        steps = step_sizes(layers[0])
+        h_dev_in = hid
+        for i, L in enumerate(layers):
+            announce("two layers: layer", i)
+            out, got = run_gpu_layer(store, i, cfg, h_dev_in, ctx, pools[i], scratch, offs, steps)
+            ref, st = oracle_layer(L, h_dev_in, ctx, ref_pools[i], 500000.0)
+            scale = term_scale(L, h_dev_in, st)
+            err = np.abs(out.astype(np.float64) - ref)
+            assert np.all(err <= ATOL + E2E_RTOL * scale), f"layer {i}: {int((err > ATOL + E2E_RTOL * scale).sum())}"
+            print(f"layer {i}: max |gpu - ref| / term scale = {np.max(err / scale):.2e}")
+            h_dev_in = out
+    finally:
+        store.close()

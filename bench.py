@@ -44,6 +44,9 @@ def parse():
     ap.add_argument("--hipblaslt", action="store_true",
                     help="torch's fp16 GEMM (hipBLASLt) of the config-4 layer shapes on already "
                          "dequantized weights, for comparison with the Q4_K prefill GEMM; prints one JSON line")
+    ap.add_argument("--layer", action="store_true",
+                    help="only the decoder-layer case (one Llama-3-8B layer from resident weights, "
+                         "ssdq_decode_layer_dev), for a kernel trace of its steps; prints one JSON line")
     ap.add_argument("--eager", action="store_true",
                     help="launch every matvec step from Python instead of replaying captured HIP graphs")
     return ap.parse_args()
@@ -188,6 +191,9 @@ def main():
         print(json.dumps(hipblaslt_layer(torch)))
         return
     timer = Timer(torch, graph=not args.eager)
+    if args.layer:
+        print(json.dumps({"decode_layer_llama3_8b_q4k_ctx4096": decode_layer_case(torch, ssdq, synth, timer)}))
+        return
 
     # ---------------------------------------------------------- headline
     step, algo_bytes, _ = matvec_case(torch, ssdq, synth, ssdq.Q4_K, 14336, 4096, 1, 3)
@@ -393,7 +399,9 @@ def decode_layer_case(torch, ssdq, synth, timer, ctx=4096):
     return {"us": round(per * 1e6, 2), "GB/s": round(nbytes / per / 1e9, 1),
             "pct_hbm_peak": round(100 * nbytes / per / 1e9 / HBM_PEAK_GBS, 2), "bytes": nbytes,
             "layers_rotated": n, "context": ctx, "hidden_finite": ok,
-            "note": "ssdq_decode_layer_dev: 9 steps, 10 kernel launches (the residual add folded into the down projection), one HIP graph replay per 50 layers"}
+            "note": "ssdq_decode_layer_dev: 9 steps in 8 kernel launches (the two RMSNorms folded into the QKV and "
+                    "SwiGLU launches, the residual add into the down projection's slice reduction), one HIP graph "
+                    "replay per 50 layers"}
 
 
 def attention_case(torch, ssdq, synth, codes, scales):

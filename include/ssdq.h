@@ -356,7 +356,9 @@ typedef struct ssdq_layer_config {
 /* Regions of the layer's scratch buffer, in floats of the named step's output:
  * attention input (normed), q, k, v (after RoPE), attention, output
  * projection, FFN input (normed), silu(gate) * up, gate and up (used when
- * their types differ), down projection, widened norm weights (F16 / BF16 norms). */
+ * their types differ), down projection, widened norm weights (F16 / BF16
+ * norms), hidden + attention output (when the FFN norm is folded into the
+ * SwiGLU launch). */
 #define SSDQ_LAYER_ATTN_IN 0
 #define SSDQ_LAYER_Q 1
 #define SSDQ_LAYER_K 2
@@ -369,7 +371,8 @@ typedef struct ssdq_layer_config {
 #define SSDQ_LAYER_FFN_UP 9
 #define SSDQ_LAYER_FFN_OUT 10
 #define SSDQ_LAYER_NORM_W 11
-#define SSDQ_LAYER_N_STAGES 12
+#define SSDQ_LAYER_HIDDEN_MID 12
+#define SSDQ_LAYER_N_STAGES 13
 /* Bytes of scratch ssdq_decode_layer_dev needs (0 for a bad config);
  * offsets (NULL, or SSDQ_LAYER_N_STAGES entries) gets each region's byte
  * offset. After a call each region holds that step's output for the token. */

@@ -109,6 +109,10 @@ int api_fail(int code, const char* fmt, ...) {
 }
 int api_hip_fail(hipError_t e, const char* what) { return hip_fail(e, what); }
 int api_ok() { return ok(); }
+void api_rope_freqs(RopeFreq* r, int head_dim, float theta) {
+  for (int i = 0; i < 128; i++)
+    r->f[i] = i < head_dim / 2 ? 1.0f / powf(theta, 2.0f * (float)i / (float)head_dim) : 0.0f;
+}
 hipError_t api_workspace(size_t bytes, hipStream_t stream, void** out, int slot) {
   return workspace_get(bytes, stream, out, slot);
 }
@@ -439,10 +443,7 @@ int ssdq_kv_swap_in_dev(const void* slots, const int32_t* block_ids, size_t n_bl
 namespace {
 // 1 / theta^(2i/head_dim) with the C library's powf, the call the reference's
 // rope_f32_multi_head makes (compute.rs:494)
-void rope_freqs(ssdq::RopeFreq* r, int head_dim, float theta) {
-  for (int i = 0; i < 128; i++)
-    r->f[i] = i < head_dim / 2 ? 1.0f / powf(theta, 2.0f * (float)i / (float)head_dim) : 0.0f;
-}
+void rope_freqs(ssdq::RopeFreq* r, int head_dim, float theta) { ssdq::api_rope_freqs(r, head_dim, theta); }
 }  // namespace
 
 int ssdq_rmsnorm_dev(const float* x, const float* residual, const float* weight, float eps,

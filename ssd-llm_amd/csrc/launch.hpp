@@ -18,12 +18,13 @@ hipError_t launch_dequant(int dtype, const uint8_t* w, size_t n_blocks, float* o
 hipError_t launch_matvec(int dtype, const uint8_t* w, const float* x, float* y, size_t out_dim,
                          size_t in_dim, size_t batch, hipStream_t stream, void* workspace = nullptr,
                          size_t workspace_bytes = 0);
-// acc[r] += sum_k W[r,k] x[k] (batch 1; Q4_0 / Q8_0 / Q4_K / Q6_K), with y
-// receiving the plain product: the residual add of a decoder layer folded
-// into the K-sliced matvec's slice reduction (acc = acc + y, the same fp32 add
-// as a separate residual kernel).  acc may not alias x or y.
+// acc[r] = acc_in[r] + sum_k W[r,k] x[k] (batch 1; Q4_0 / Q8_0 / Q4_K / Q6_K;
+// acc_in null: acc itself), with y receiving the plain product: the residual
+// add of a decoder layer folded into the K-sliced matvec's slice reduction
+// (the same fp32 add as a separate residual kernel).  acc may not alias x or y.
 hipError_t launch_matvec_acc(int dtype, const uint8_t* w, const float* x, float* acc, float* y, size_t out_dim,
-                             size_t in_dim, hipStream_t s, void* workspace, size_t workspace_bytes);
+                             size_t in_dim, hipStream_t s, void* workspace, size_t workspace_bytes,
+                             const float* acc_in = nullptr);
 // Device workspace launch_matvec uses for these operands (batch-1 K slices).
 size_t matvec_workspace_bytes(int dtype, const void* w, const float* x, size_t out_dim,
                               size_t in_dim, size_t batch);
@@ -62,6 +63,15 @@ struct MatvecFuse {
   unsigned rope_mask;
   int head_dim, position;
   RopeFreq freq;
+  // RMSNorm of x in the kernel's staging (the norm-fused variants): x' = (x +
+  // norm_res) * inv_rms * norm_w, inv_rms = 1 / sqrt(mean((x + norm_res)^2) +
+  // norm_eps); workgroup 0 writes x + norm_res to hidden_out and x' to xn_out
+  // (either may be null).  norm_w null: no norm.
+  const float* norm_w;
+  const float* norm_res;
+  float norm_eps;
+  float* hidden_out;
+  float* xn_out;
 };
 // One fused launch when the shapes allow it (Q4_0 / Q8_0 / Q4_K / Q6_K, whole
 // rows of at most 128 units, aligned operands); *used = false otherwise.
@@ -83,6 +93,8 @@ hipError_t launch_rope(float* v, int n, int head_dim, int position, const RopeFr
 hipError_t launch_swiglu(const float* g, const float* u, float* h, int n, hipStream_t stream);
 // h += a (n floats)
 hipError_t launch_residual_add(float* h, const float* a, int n, hipStream_t stream);
+// out = a + b (n floats; out may alias a or b)
+hipError_t launch_add(float* out, const float* a, const float* b, int n, hipStream_t stream);
 // hsum = x + residual (residual may be null; hidden_out may be null), then
 // out = hsum * inv_rms * w with inv_rms = 1 / sqrt(mean(hsum^2) + eps).
 hipError_t launch_rmsnorm(const float* x, const float* residual, const float* w, float eps,
@@ -160,5 +172,7 @@ int api_fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)
 int api_hip_fail(hipError_t e, const char* what);
 int api_ok();
 hipError_t api_workspace(size_t bytes, hipStream_t stream, void** out, int slot);
+// theta^(-2i/head_dim) with the C library's powf, as the reference computes them
+void api_rope_freqs(RopeFreq* r, int head_dim, float theta);
 
 }  // namespace ssdq

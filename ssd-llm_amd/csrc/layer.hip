@@ -32,11 +32,11 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g
   }
 }
 
-// h += a: the FFN residual add of the decoder layer (transformer.rs:378-380).
-__global__ __launch_bounds__(256) void residual_add_kernel(float* __restrict__ h, const float* __restrict__ a,
-                                                           int n) {
+// out = a + b: the FFN residual add of the decoder layer (transformer.rs:378-380);
+// out may alias a or b (each thread reads its element before writing it).
+__global__ __launch_bounds__(256) void residual_add_kernel(float* out, const float* a, const float* b, int n) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) h[i] += a[i];
+  if (i < n) out[i] = a[i] + b[i];
 }
 
 // One workgroup: the whole vector (n is a hidden size, a few thousand).  Up to
@@ -105,11 +105,13 @@ hipError_t launch_swiglu(const float* g, const float* u, float* h, int n, hipStr
   return hipGetLastError();
 }
 
-hipError_t launch_residual_add(float* h, const float* a, int n, hipStream_t s) {
+hipError_t launch_add(float* out, const float* a, const float* b, int n, hipStream_t s) {
   if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(residual_add_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, h, a, n);
+  hipLaunchKernelGGL(residual_add_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, out, a, b, n);
   return hipGetLastError();
 }
+
+hipError_t launch_residual_add(float* h, const float* a, int n, hipStream_t s) { return launch_add(h, h, a, n, s); }
 
 hipError_t launch_rmsnorm(const float* x, const float* residual, const float* w, float eps, float* hidden_out,
                           float* out, int n, hipStream_t s) {

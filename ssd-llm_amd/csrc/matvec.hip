@@ -677,6 +677,54 @@ template <int F> constexpr int loads_per_unit() {
 // 14336 x 4096 Q4_K: depth 1 9.8 us, 2 8.5 us, 3 9.2 us, 5 11.2 us)
 template <int RMAX> constexpr int kB1Depth = RMAX < 2 ? RMAX : 2;
 
+// RMSNorm of the staged x (the norm-fused decode-layer launches): h = x (+ the
+// residual), x' = h * inv_rms * w with inv_rms = 1 / sqrt(mean(h^2) + eps),
+// the sum of squares reduced over the workgroup (each workgroup computes the
+// same value: the same data in the same order).  Workgroup 0 writes h and x'.
+template <int SIT, bool RES>
+__device__ __forceinline__ void stage_norm(XChunks<SIT>& st, const XChunks<SIT>& st_r, const XChunks<SIT>& st_w,
+                                           int keff, const MatvecFuse& fu) {
+  __shared__ float part[16];
+  const int nchunk = keff >> 3;
+  float q = 0.f;
+#pragma unroll
+  for (int it = 0; it < SIT; it++)
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      if (RES) st.v[it][j] = st.v[it][j] + st_r.v[it][j];
+      q = fmaf(st.v[it][j], st.v[it][j], q);  // chunks past the end are zeros
+    }
+  q = wave_sum(q);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  if (lane == 0) part[wave] = q;
+  __syncthreads();
+  float t = 0.f;
+  for (int i = 0; i < nw; i++) t += part[i];
+  const float inv = 1.0f / sqrtf(t / (float)keff + fu.norm_eps);
+#pragma unroll
+  for (int it = 0; it < SIT; it++) {
+    const int c = it * (int)blockDim.x + (int)threadIdx.x;
+    const bool live = c < nchunk;
+    float h[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      h[j] = st.v[it][j];
+      st.v[it][j] = h[j] * inv * st_w.v[it][j];
+    }
+    if (blockIdx.x == 0 && live) {
+      if (fu.hidden_out) {
+        *reinterpret_cast<float4*>(fu.hidden_out + 8 * c) = make_float4(h[0], h[1], h[2], h[3]);
+        *reinterpret_cast<float4*>(fu.hidden_out + 8 * c + 4) = make_float4(h[4], h[5], h[6], h[7]);
+      }
+      if (fu.xn_out) {
+        const float* v = st.v[it];
+        *reinterpret_cast<float4*>(fu.xn_out + 8 * c) = make_float4(v[0], v[1], v[2], v[3]);
+        *reinterpret_cast<float4*>(fu.xn_out + 8 * c + 4) = make_float4(v[4], v[5], v[6], v[7]);
+      }
+    }
+  }
+}
+
 // Decode-layer fusion of the batch-1 kernel (FUSE = true).  Up to three
 // weight matrices of one type and row length share x ("segments", virtual
 // rows concatenated; for SwiGLU the rows of gate and up alternate).  Row runs
@@ -686,7 +734,8 @@ template <int RMAX> constexpr int kB1Depth = RMAX < 2 ? RMAX : 2;
 // every workgroup's first weight rows.)
 // The plain kernel takes an empty argument in the fuse descriptor's place.
 struct NoFuse {};
-// FUSE: 0 plain; 2 segments in row pairs with the RoPE / SwiGLU epilogue.
+// FUSE: 0 plain; 2 segments in row pairs with the RoPE / SwiGLU epilogue; 3
+// and 4 the same with an RMSNorm of x (4: of x + a residual) in the staging.
 template <int FUSE> using FuseArg = typename std::conditional<FUSE != 0, MatvecFuse, NoFuse>::type;
 
 __device__ __forceinline__ int fuse_seg(const MatvecFuse& f, int v, int& r) {
@@ -727,7 +776,7 @@ __global__ __launch_bounds__(768) void mv_b1(const uint8_t* __restrict__ w,
                                              const float* __restrict__ x, float* __restrict__ y,
                                              int out_dim, int row_bpr, int slice_bpr, int ks,
                                              bool interleave, FuseArg<FUSE> fu) {
-  static_assert(FUSE != 2 || RMAX % 2 == 0, "fused rows come in pairs");
+  static_assert(FUSE < 2 || RMAX % 2 == 0, "fused rows come in pairs");
   using FU = FastUnit<F>;
   using D = Dig<F>;
   constexpr int NW = FU::NW, US = D::US;
@@ -749,7 +798,7 @@ __global__ __launch_bounds__(768) void mv_b1(const uint8_t* __restrict__ w,
   // Rows of a stream are either one contiguous run or, interleaved, rows
   // gs, gs + n_streams, ... (all waves then sweep the matrix together).
   int r_begin, r_step, n_rows;  // n_rows <= RMAX either way
-  if (FUSE == 2) {  // runs of row pairs
+  if (FUSE >= 2) {  // runs of row pairs
     const long P = out_dim / 2;
     const long p0 = gs * P / n_streams, p1 = (gs + 1) * P / n_streams;
     r_begin = (int)(2 * p0);
@@ -770,7 +819,7 @@ __global__ __launch_bounds__(768) void mv_b1(const uint8_t* __restrict__ w,
   auto load_row = [&](int rr) {
     const int row = max(0, min(r_begin + rr * r_step, out_dim - 1));
     const uint8_t* rp;
-    if constexpr (FUSE == 2) {
+    if constexpr (FUSE >= 2) {
       int r;
       const int sg = fuse_seg(fu, row, r);
       rp = (sg == 0 ? fu.w0 : sg == 1 ? fu.w1 : fu.w2) + (size_t)r * row_bytes;
@@ -786,6 +835,11 @@ __global__ __launch_bounds__(768) void mv_b1(const uint8_t* __restrict__ w,
 
   XChunks<SIT> st;
   stage_load<SIT>(x, keff, st, blockDim.x);  // 1.
+  [[maybe_unused]] XChunks<SIT> st_r, st_w;
+  if constexpr (FUSE >= 3) {  // the norm's operands, also before any weight
+    if constexpr (FUSE == 4) stage_load<SIT>(fu.norm_res, keff, st_r, blockDim.x);
+    stage_load<SIT>(fu.norm_w, keff, st_w, blockDim.x);
+  }
 #pragma unroll
   for (int rr = 0; rr < kB1Depth<RMAX>; rr++) load_row(rr);
   {
@@ -794,6 +848,7 @@ __global__ __launch_bounds__(768) void mv_b1(const uint8_t* __restrict__ w,
     static_assert(N < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
   }
+  if constexpr (FUSE >= 3) stage_norm<SIT, FUSE == 4>(st, st_r, st_w, keff, fu);
   stage_store<F, SIT>(st, keff, lds, blockDim.x);
   lds_barrier();
 
@@ -825,7 +880,7 @@ __global__ __launch_bounds__(768) void mv_b1(const uint8_t* __restrict__ w,
   }
 #pragma unroll
   for (int rr = 0; rr < RMAX; rr++) acc[rr] = wave_sum_l63(acc[rr]);
-  if constexpr (FUSE == 2) {
+  if constexpr (FUSE >= 2) {
     if (lane == 63) {
 #pragma unroll
       for (int rr = 0; rr < RMAX; rr += 2) {
@@ -1449,11 +1504,13 @@ size_t b1_workspace_floats(int out_dim, int bpr) {
   return p.slices > 1 ? (size_t)p.slices * out_dim : 0;
 }
 
-// acc non-null: acc += W x instead of y = W x, with y as scratch for the
-// unsliced plan (K-sliced rows add acc in the slice reduction itself).
+// acc non-null: acc = acc_in + W x (acc_in null: acc itself) instead of y =
+// W x, with y receiving W x (K-sliced rows add acc_in in the slice reduction).
 template <int F>
 hipError_t b1_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, int bpr,
-                       hipStream_t s, float* ws, size_t ws_floats, bool* used, float* acc = nullptr) {
+                       hipStream_t s, float* ws, size_t ws_floats, bool* used, float* acc = nullptr,
+                       const float* acc_in = nullptr) {
+  if (acc && !acc_in) acc_in = acc;
   const int U = bpr * Geom<F>::bs / FastUnit<F>::E;
   if (U == 0) return hipSuccess;
   const B1Plan<F> p = b1_plan<F>(bpr, out_dim);
@@ -1490,9 +1547,9 @@ hipError_t b1_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, 
                : run_b1s<F, false>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, s);
     if (e != hipErrorNotSupported) {
       if (e != hipSuccess) return e;
-      if (p.slices == 1) return acc ? launch_residual_add(acc, y, out_dim, s) : hipSuccess;
+      if (p.slices == 1) return acc ? launch_add(acc, acc_in, y, out_dim, s) : hipSuccess;
       hipLaunchKernelGGL(slice_reduce_kernel, dim3((unsigned)((out_dim + 255) / 256)), dim3(256), 0, s,
-                         ws, acc ? acc : y, out_dim, p.slices, (const float*)acc, y);
+                         ws, acc ? acc : y, out_dim, p.slices, acc_in, y);
       return hipGetLastError();
     }
   }
@@ -1527,9 +1584,9 @@ hipError_t b1_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, 
     return hipSuccess;
   }
   if (e != hipSuccess) return e;
-  if (p.slices == 1) return acc ? launch_residual_add(acc, y, out_dim, s) : hipSuccess;
+  if (p.slices == 1) return acc ? launch_add(acc, acc_in, y, out_dim, s) : hipSuccess;
   hipLaunchKernelGGL(slice_reduce_kernel, dim3((unsigned)((out_dim + 255) / 256)), dim3(256), 0, s,
-                     ws, acc ? acc : y, out_dim, p.slices, (const float*)acc, y);
+                     ws, acc ? acc : y, out_dim, p.slices, acc_in, y);
   return hipGetLastError();
 }
 
@@ -1571,7 +1628,7 @@ hipError_t run_fused(const MatvecFuse& f, const float* x, int vrows, int bpr, hi
     if (it != rs_cache.end()) rs = it->second;
   }
   if (rs == 0) {
-    auto probe = mv_b1<F, UPL, RMAX, true, 2, MODE>;
+    auto probe = mv_b1<F, UPL, RMAX, true, MODE >= 3 ? 1 : 2, MODE>;
     hipError_t e = set_lds_attr(probe, lds);
     if (e != hipSuccess) return e;
     rs = 1;
@@ -1589,6 +1646,7 @@ hipError_t run_fused(const MatvecFuse& f, const float* x, int vrows, int bpr, hi
   const int sit = (nchunk + 64 * rs - 1) / (64 * rs);
   hipError_t e;
   if (sit <= 1) e = run_fused_sit<F, UPL, RMAX, 1, MODE>(f, x, vrows, bpr, rs, lds, s);
+  else if constexpr (MODE >= 3) return hipSuccess;  // the norm-fused forms stage x in one chunk per thread
   else if (sit <= 2) e = run_fused_sit<F, UPL, RMAX, 2, MODE>(f, x, vrows, bpr, rs, lds, s);
   else return hipSuccess;  // x too long to stage in two chunks per thread
   if (e == hipErrorNotSupported) return hipSuccess;  // more rows than one round: not fused
@@ -1606,6 +1664,21 @@ hipError_t fused_dispatch(const MatvecFuse& f, int vrows, const float* x, int in
   if (U == 0 || (U != 64 && U != 128)) return hipSuccess;  // whole units per lane, one slice
   for (const uint8_t* w : {f.w0, f.w1, f.w2})
     if (w && !fast_aligned<F>(w, x, in_dim, bpr)) return hipSuccess;
+  if (f.norm_w) {
+    // the norm-fused forms: the row counts of the Llama-3-8B-sized layers (QKV
+    // 6144 rows: 2 per wave; SwiGLU 2 x 14336: 10), one unit per lane; other
+    // shapes take a separate norm launch and the plain fused kernel
+    if (U != 64) return hipSuccess;
+    hipError_t e = f.norm_res ? run_fused<F, 1, 2, 4>(f, x, vrows, bpr, s, used)
+                              : run_fused<F, 1, 2, 3>(f, x, vrows, bpr, s, used);
+    if (e != hipSuccess || *used) return e;
+    // more rows: 10 per wave, but only where that is the fewest that fit one
+    // round (12 waves per workgroup, one workgroup per CU)
+    for (int rmax : {4, 6})
+      if ((vrows / 2 + rmax / 2 - 1) / (rmax / 2) <= 12L * device_cu_count()) return hipSuccess;
+    return f.norm_res ? run_fused<F, 1, 10, 4>(f, x, vrows, bpr, s, used)
+                      : run_fused<F, 1, 10, 3>(f, x, vrows, bpr, s, used);
+  }
   if (U == 64) {
     // the fewest rows per wave that still fit one round of workgroups: rows
     // past a wave's share are still loaded (clamped), so spare capacity costs
@@ -1917,7 +1990,9 @@ size_t matvec_workspace_bytes(int dtype, const void* w, const float* x, size_t o
 }
 
 hipError_t launch_matvec_acc(int dtype, const uint8_t* w, const float* x, float* acc, float* y, size_t out_dim,
-                             size_t in_dim, hipStream_t s, void* workspace, size_t workspace_bytes) {
+                             size_t in_dim, hipStream_t s, void* workspace, size_t workspace_bytes,
+                             const float* acc_in) {
+  if (!acc_in) acc_in = acc;
   if (out_dim == 0) return hipSuccess;
   bool used = false;
   hipError_t e = hipSuccess;
@@ -1927,7 +2002,7 @@ hipError_t launch_matvec_acc(int dtype, const uint8_t* w, const float* x, float*
   auto go = [&](auto f_c, int bpr) {
     constexpr int F = decltype(f_c)::value;
     if (bpr == 0 || !fast_aligned<F>(w, x, id, bpr)) return hipSuccess;
-    return b1_dispatch<F>(w, x, y, od, bpr, s, ws, wf, &used, acc);
+    return b1_dispatch<F>(w, x, y, od, bpr, s, ws, wf, &used, acc, acc_in);
   };
   switch (dtype) {
     case kQ4_0: e = go(std::integral_constant<int, kQ4_0>{}, id / 32); break;
@@ -1939,7 +2014,7 @@ hipError_t launch_matvec_acc(int dtype, const uint8_t* w, const float* x, float*
   if (e != hipSuccess || used) return e;
   e = launch_matvec(dtype, w, x, y, out_dim, in_dim, 1, s, workspace, workspace_bytes);
   if (e != hipSuccess) return e;
-  return launch_residual_add(acc, y, od, s);
+  return launch_add(acc, acc_in, y, od, s);
 }
 
 hipError_t launch_matvec(int dtype, const uint8_t* w, const float* x, float* y, size_t out_dim,

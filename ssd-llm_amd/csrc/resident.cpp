@@ -213,8 +213,8 @@ namespace {
 // Scratch layout: one region per stage output, each 256-byte aligned.
 size_t layer_layout(const ssdq_layer_config* c, size_t* off) {
   const size_t q_dim = c->n_head * c->head_dim, kv_dim = c->n_head_kv * c->head_dim;
-  const size_t n[SSDQ_LAYER_N_STAGES] = {c->n_embd, q_dim, kv_dim,  kv_dim,   q_dim,       c->n_embd,
-                                         c->n_embd, c->n_ff, c->n_ff, c->n_ff, c->n_embd, 2 * c->n_embd};
+  const size_t n[SSDQ_LAYER_N_STAGES] = {c->n_embd, q_dim,  kv_dim, kv_dim,    q_dim,         c->n_embd, c->n_embd,
+                                         c->n_ff,   c->n_ff, c->n_ff, c->n_embd, 2 * c->n_embd, c->n_embd};
   size_t at = 0;
   for (int i = 0; i < SSDQ_LAYER_N_STAGES; i++) {
     if (off) off[i] = at;
@@ -350,6 +350,7 @@ int ssdq_decode_layer_dev(const ssdq_weights* w, uint32_t layer, const ssdq_laye
   float* up = (float*)(base + off[SSDQ_LAYER_FFN_UP]);
   float* fo = (float*)(base + off[SSDQ_LAYER_FFN_OUT]);
   float* nw = (float*)(base + off[SSDQ_LAYER_NORM_W]);
+  float* hmid = (float*)(base + off[SSDQ_LAYER_HIDDEN_MID]);
   int worst = SSDQ_OK;
   // keeps the worst status of the steps: a failure ends the layer, the
   // unsupported-type warning (that projection zero-filled) is passed on
@@ -362,16 +363,40 @@ int ssdq_decode_layer_dev(const ssdq_weights* w, uint32_t layer, const ssdq_laye
     return false;
   };
 
-  // 1. attn_input = rms_norm(hidden, attn_norm) (transformer.rs:319-323)
+  // 1-2. attn_input = rms_norm(hidden, attn_norm) (transformer.rs:319-323),
+  // then multi_head_attention_fused_rope's QKV + RoPE (attention.rs:190-198):
+  // one launch when the norm folds into the fused QKV kernel's staging of x
   hipError_t e = hipSuccess;
-  if (t_an) {
-    const float* g = nullptr;
-    if ((rc = norm_weight(t_an, pre + "attn_norm.weight", n_embd, nw, s, &g))) return rc;
-    e = ssdq::launch_rmsnorm(hidden, nullptr, g, cfg->norm_eps, nullptr, xn, (int)n_embd, s);
-  } else {
-    e = hipMemcpyAsync(xn, hidden, n_embd * sizeof(float), hipMemcpyDeviceToDevice, s);
+  const float* g_attn = nullptr;
+  if (t_an && (rc = norm_weight(t_an, pre + "attn_norm.weight", n_embd, nw, s, &g_attn))) return rc;
+  bool qkv_done = false;
+  if (g_attn && attn && t_q->dtype == t_k->dtype && t_k->dtype == t_v->dtype) {
+    ssdq::MatvecFuse f{};
+    f.w0 = (const uint8_t*)t_q->dev;
+    f.w1 = (const uint8_t*)t_k->dev;
+    f.w2 = (const uint8_t*)t_v->dev;
+    f.y0 = q;
+    f.y1 = k;
+    f.y2 = v;
+    f.start1 = (int)q_dim;
+    f.start2 = (int)(q_dim + kv_dim);
+    f.rope_mask = 3u;
+    f.head_dim = (int)cfg->head_dim;
+    f.position = (int)position;
+    ssdq::api_rope_freqs(&f.freq, (int)cfg->head_dim, cfg->rope_theta);
+    f.norm_w = g_attn;
+    f.norm_eps = cfg->norm_eps;
+    f.xn_out = xn;
+    e = ssdq::launch_matvec_fused(t_q->dtype, f, (int)(q_dim + 2 * kv_dim), hidden, n_embd, s, &qkv_done);
+    if (e != hipSuccess) return api_hip_fail(e, "ssdq_decode_layer_dev: norm + QKV");
   }
-  if (e != hipSuccess) return api_hip_fail(e, "ssdq_decode_layer_dev: attention norm");
+  if (!qkv_done) {
+    if (g_attn)
+      e = ssdq::launch_rmsnorm(hidden, nullptr, g_attn, cfg->norm_eps, nullptr, xn, (int)n_embd, s);
+    else
+      e = hipMemcpyAsync(xn, hidden, n_embd * sizeof(float), hipMemcpyDeviceToDevice, s);
+    if (e != hipSuccess) return api_hip_fail(e, "ssdq_decode_layer_dev: attention norm");
+  }
   // without all four attention tensors the reference skips the rest of the
   // layer (transformer.rs:326-331)
   if (!attn) {
@@ -380,9 +405,11 @@ int ssdq_decode_layer_dev(const ssdq_weights* w, uint32_t layer, const ssdq_laye
   }
 
   // 2-5. multi_head_attention_fused_rope (attention.rs:172-240) over the paged
-  // INT8 cache: QKV + RoPE, append, attention, output projection
-  if (take(ssdq_qkv_rope_dev(t_q->dtype, t_q->dev, t_k->dtype, t_k->dev, t_v->dtype, t_v->dev, xn, q, k, v, q_dim,
-                             kv_dim, n_embd, cfg->head_dim, position, cfg->rope_theta, stream)))
+  // INT8 cache: QKV + RoPE (unless done above), append, attention, output
+  // projection
+  if (!qkv_done && take(ssdq_qkv_rope_dev(t_q->dtype, t_q->dev, t_k->dtype, t_k->dev, t_v->dtype, t_v->dev, xn, q,
+                                          k, v, q_dim, kv_dim, n_embd, cfg->head_dim, position, cfg->rope_theta,
+                                          stream)))
     return worst;
   if (take(ssdq_paged_kv_append_dev(k, v, slot_mapping, k_codes, k_scales, v_codes, v_scales, 1, kv_dim, stream)))
     return worst;
@@ -394,44 +421,70 @@ int ssdq_decode_layer_dev(const ssdq_weights* w, uint32_t layer, const ssdq_laye
 
   // 6. hidden += attn_output, ffn_input = rms_norm(hidden, ffn_norm)
   // (fused_post_attn_norm_f32, transformer.rs:346-359); without ffn_norm the
-  // FFN reads the updated hidden state itself (transformer.rs:381-386)
-  const float* ffn_in = fin;
-  if (t_fn) {
-    const float* g = nullptr;
-    if ((rc = norm_weight(t_fn, pre + "ffn_norm.weight", n_embd, nw + n_embd, s, &g))) return rc;
-    e = ssdq::launch_rmsnorm(hidden, ao, g, cfg->norm_eps, hidden, fin, (int)n_embd, s);
-  } else {
-    e = ssdq::launch_residual_add(hidden, ao, (int)n_embd, s);
-    ffn_in = hidden;
-  }
-  if (e != hipSuccess) return api_hip_fail(e, "ssdq_decode_layer_dev: residual norm");
-
+  // FFN reads the updated hidden state itself (transformer.rs:381-386).
   // 7-8. dense SwiGLU FFN (run_ffn_or_moe_gpu, transformer.rs:470-481 ->
   // feed_forward.rs:16-45) and its residual add (transformer.rs:369-373);
-  // absent FFN tensors leave hidden as it is
-  if (ffn) {
-    if (t_g->dtype == t_u->dtype) {
-      if (take(ssdq_swiglu_dev(t_g->dtype, t_g->dev, t_u->dev, ffn_in, h, n_ff, n_embd, stream))) return worst;
+  // absent FFN tensors leave hidden as hidden + attn_output.
+  const float* g_ffn = nullptr;
+  if (t_fn && (rc = norm_weight(t_fn, pre + "ffn_norm.weight", n_embd, nw + n_embd, s, &g_ffn))) return rc;
+  // The norm folds into the fused SwiGLU kernel's staging: every workgroup
+  // reads hidden and attn_output, so the updated hidden state goes to hmid
+  // (not in place) and the down projection writes hidden = hmid + W_down h.
+  bool ffn_done = false;
+  if (g_ffn && ffn && t_g->dtype == t_u->dtype) {
+    ssdq::MatvecFuse f{};
+    f.w0 = (const uint8_t*)t_g->dev;
+    f.w1 = (const uint8_t*)t_u->dev;
+    f.y0 = h;
+    f.start1 = f.start2 = INT_MAX;
+    f.swiglu = 1;
+    f.head_dim = 2;
+    f.norm_w = g_ffn;
+    f.norm_res = ao;
+    f.norm_eps = cfg->norm_eps;
+    f.hidden_out = hmid;
+    f.xn_out = fin;
+    e = ssdq::launch_matvec_fused(t_g->dtype, f, (int)(2 * n_ff), hidden, n_embd, s, &ffn_done);
+    if (e != hipSuccess) return api_hip_fail(e, "ssdq_decode_layer_dev: norm + SwiGLU");
+  }
+  const float* ffn_in = fin;
+  const float* h_res = hidden;  // the hidden state the FFN output is added to
+  if (ffn_done) {
+    h_res = hmid;
+  } else {
+    if (g_ffn) {
+      e = ssdq::launch_rmsnorm(hidden, ao, g_ffn, cfg->norm_eps, hidden, fin, (int)n_embd, s);
     } else {
-      // gate and up of different types: two projections, then the product
-      if (take(ssdq_matvec_dev(t_g->dtype, t_g->dev, ffn_in, gate, n_ff, n_embd, 1, stream))) return worst;
-      if (take(ssdq_matvec_dev(t_u->dtype, t_u->dev, ffn_in, up, n_ff, n_embd, 1, stream))) return worst;
-      if ((e = ssdq::launch_swiglu(gate, up, h, (int)n_ff, s)) != hipSuccess)
-        return api_hip_fail(e, "ssdq_decode_layer_dev: swiglu");
+      e = ssdq::launch_residual_add(hidden, ao, (int)n_embd, s);
+      ffn_in = hidden;
     }
+    if (e != hipSuccess) return api_hip_fail(e, "ssdq_decode_layer_dev: residual norm");
+    if (ffn) {
+      if (t_g->dtype == t_u->dtype) {
+        if (take(ssdq_swiglu_dev(t_g->dtype, t_g->dev, t_u->dev, ffn_in, h, n_ff, n_embd, stream))) return worst;
+      } else {
+        // gate and up of different types: two projections, then the product
+        if (take(ssdq_matvec_dev(t_g->dtype, t_g->dev, ffn_in, gate, n_ff, n_embd, 1, stream))) return worst;
+        if (take(ssdq_matvec_dev(t_u->dtype, t_u->dev, ffn_in, up, n_ff, n_embd, 1, stream))) return worst;
+        if ((e = ssdq::launch_swiglu(gate, up, h, (int)n_ff, s)) != hipSuccess)
+          return api_hip_fail(e, "ssdq_decode_layer_dev: swiglu");
+      }
+    }
+  }
+  if (ffn) {
     const int dd = t_d->dtype;
     if (dd == SSDQ_TYPE_Q4_0 || dd == SSDQ_TYPE_Q8_0 || dd == SSDQ_TYPE_Q4_K || dd == SSDQ_TYPE_Q6_K) {
-      // hidden += W_down h inside the K-sliced matvec's slice reduction (fo
-      // still receives W_down h)
+      // hidden = h_res + W_down h inside the K-sliced matvec's slice reduction
+      // (fo still receives W_down h)
       const size_t wsb = ssdq::matvec_workspace_bytes(dd, t_d->dev, h, n_embd, n_ff, 1);
       void* ws = nullptr;
       if (wsb && (e = ssdq::api_workspace(wsb, s, &ws, 0)) != hipSuccess)
         return api_hip_fail(e, "ssdq_decode_layer_dev: workspace");
-      e = ssdq::launch_matvec_acc(dd, (const uint8_t*)t_d->dev, h, hidden, fo, n_embd, n_ff, s, ws, wsb);
+      e = ssdq::launch_matvec_acc(dd, (const uint8_t*)t_d->dev, h, hidden, fo, n_embd, n_ff, s, ws, wsb, h_res);
       if (e != hipSuccess) return api_hip_fail(e, "ssdq_decode_layer_dev: down projection");
     } else {
       if (take(ssdq_matvec_dev(dd, t_d->dev, h, fo, n_embd, n_ff, 1, stream))) return worst;
-      if ((e = ssdq::launch_residual_add(hidden, fo, (int)n_embd, s)) != hipSuccess)
+      if ((e = ssdq::launch_add(hidden, h_res, fo, (int)n_embd, s)) != hipSuccess)
         return api_hip_fail(e, "ssdq_decode_layer_dev: residual");
     }
   }

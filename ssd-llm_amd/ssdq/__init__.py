@@ -49,7 +49,7 @@ class LayerConfig(ctypes.Structure):
 
 # scratch regions of ssdq_decode_layer_dev (SSDQ_LAYER_*)
 LAYER_STAGES = ("attn_in", "q", "k", "v", "attn", "attn_out", "ffn_in", "ffn_h", "ffn_gate", "ffn_up",
-                "ffn_out", "norm_w")
+                "ffn_out", "norm_w", "hidden_mid")
 
 _u64p = _c.POINTER(_c.c_uint64)
 

@@ -114,7 +114,7 @@ def test_weight_store_and_layer_layout_on_the_host():
     # the scratch layout: one 256-byte aligned region per step, in order
     n, offs = ssdq.decode_layer_scratch(cfg)
     sizes = dict(attn_in=4096, q=4096, k=1024, v=1024, attn=4096, attn_out=4096, ffn_in=4096, ffn_h=14336,
-                 ffn_gate=14336, ffn_up=14336, ffn_out=4096, norm_w=8192)
+                 ffn_gate=14336, ffn_up=14336, ffn_out=4096, norm_w=8192, hidden_mid=4096)
     at = 0
     for name in ssdq.LAYER_STAGES:
         assert offs[name] == at and at % 256 == 0

@@ -273,3 +273,30 @@ def test_batch1_long_rows(dtype, out_dim, in_dim):
     assert_close_attributed(y[sel], ref, exact, "long rows")
     y2, _ = run(dtype, w, x, out_dim, in_dim)
     assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))  # fixed summation order
+
+
+K_SLICED = [  # K-sliced rows: slice partials in the workspace, summed in slice order
+    (Q4_K, 28672, 8192),   # row streams, 2 slices
+    (Q4_K, 4096, 14336),   # row streams, 4 slices, partial last slice
+    (Q6_K, 4096, 14336),   # batch-1 kernel, 7 slices
+    (Q8_0, 4096, 28672),   # batch-1 kernel, 7 slices, interleaved row streams
+    (Q4_0, 2000, 28800),   # 8 slices, partial last slice
+    (Q6_K, 33, 14336),     # fewer rows than row streams
+]
+
+
+@pytest.mark.parametrize("dtype,out_dim,in_dim", K_SLICED)
+def test_k_sliced_single_launch_repeats(dtype, out_dim, in_dim):
+    """Three calls in a row agree bit for bit (the workspace's partials are
+    rewritten by each call) and match the oracle."""
+    w = synth.quant_weights(dtype, out_dim, in_dim, 90 + out_dim)
+    x = synth.normal_f32(in_dim, 91 + in_dim)
+    announce("k-sliced repeats", ssdq.TYPE_NAMES[dtype], out_dim, in_dim)
+    w_dev = to_dev(w)
+    ys = [run(dtype, None, x, out_dim, in_dim, w_dev=w_dev)[0] for _ in range(3)]
+    for yk in ys[1:]:
+        assert np.array_equal(ys[0].view(np.uint32), yk.view(np.uint32))
+    sel = np.arange(out_dim) if out_dim <= 1000 else np.r_[0:300, out_dim // 2:out_dim // 2 + 100, out_dim - 300:out_dim]
+    rb = w.size // out_dim
+    ref, exact = reference(dtype, w.reshape(out_dim, rb)[sel].ravel(), x, sel.size, in_dim)
+    assert_close_attributed(ys[0][sel], ref, exact, "k-sliced repeats")

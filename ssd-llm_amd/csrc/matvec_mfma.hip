@@ -150,8 +150,8 @@ __global__ __launch_bounds__(768, 1) void mv_q8r(const uint8_t* __restrict__ w, 
   // the loads above are issued before anything waits for one
   __builtin_amdgcn_sched_barrier(0);
 
-  // ---- x digit planes of the whole row into LDS (digits 0-2 of A rows 4 b' +
-  // t; the rows of digit 3 and of activation rows past NB are never read)
+  // ---- x digit planes of the whole row into LDS (A rows 4 b' + t: digits 0-2
+  // and a zero digit 3; the rows of activation rows past NB are never read)
 #pragma unroll
   for (int k = 0; k < P::CPT; k++) {
     const int c0 = (int)threadIdx.x + P::THREADS * k;
@@ -187,20 +187,21 @@ __global__ __launch_bounds__(768, 1) void mv_q8r(const uint8_t* __restrict__ w, 
       for (int d = 0; d < 3; d++)
         f[d] = make_uint2(gather_byte(u[0], u[1], u[2], u[3], d) ^ 0x80808080u,
                           gather_byte(u[4], u[5], u[6], u[7], d) ^ 0x80808080u);
+      f[3] = make_uint2(0u, 0u);
       if (q == 0) scl[j * NB + b] = badf != 0.f ? __builtin_nanf("") : ldexpf(1.0f, e - 22);
     }
   }
   __syncthreads();
 
   // A row lane % 16 of MFMA m is digit lane % 4 of activation row 4 m +
-  // lane % 16 / 4; D rows 4 q .. 4 q + 3 are activation row 4 m + q.  Rows
-  // that do not exist are masked to zero (as bits: a select here becomes a
-  // branch around the LDS reads)
+  // lane % 16 / 4; D rows 4 q .. 4 q + 3 are activation row 4 m + q.  Rows of
+  // activation rows past NB (batches that are not a multiple of 4) are masked
+  // to zero, as bits: a select here becomes a branch around the LDS reads
   uint64_t amask[NM];
   uint32_t xmask[NM];
 #pragma unroll
   for (int m4 = 0; m4 < NM; m4++) {
-    amask[m4] = (lane & 3) != 3 && 4 * m4 + ((lane & 15) >> 2) < NB ? ~0ull : 0ull;
+    amask[m4] = 4 * m4 + ((lane & 15) >> 2) < NB ? ~0ull : 0ull;
     xmask[m4] = 4 * m4 + kg < NB ? ~0u : 0u;
   }
   float acc[NM];
@@ -242,7 +243,8 @@ __global__ __launch_bounds__(768, 1) void mv_q8r(const uint8_t* __restrict__ w, 
 #pragma unroll
         for (int m4 = 0; m4 < NM; m4++) {
           const uint2 fa = reinterpret_cast<const uint2*>(frag + (size_t)j * P::FS + m4 * 512)[lane];
-          const int64_t aop = (int64_t)((((uint64_t)fa.y << 32) | fa.x) & amask[m4]);
+          const uint64_t av = ((uint64_t)fa.y << 32) | fa.x;
+          const int64_t aop = (int64_t)(NB % 4 == 0 ? av : av & amask[m4]);
           const float xs = __uint_as_float(__float_as_uint(scl[j * NB + min(4 * m4 + kg, NB - 1)]) & xmask[m4]);
           const i32x4 c = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, i32x4{0, 0, 0, 0}, 0, 0, 0);
           // I0 + 256 I1 exactly in int (|I1| <= 2^16), then one rounding with 65536 I2

@@ -218,6 +218,7 @@ def test_extreme_and_nonfinite_activations(dtype, batch):
 Q8_MFMA = [  # (out_dim, in_dim, batch): Q8_0 batches of 2-8 on the matrix cores
     (11008, 4096, 2), (11008, 4096, 3), (11008, 4096, 5), (11008, 4096, 6), (11008, 4096, 7),
     (4097, 4096, 8), (1000, 2048, 3), (17, 1024, 5), (4096, 1024, 8), (16, 4096, 2), (300, 4096, 12),
+    (20000, 4096, 4), (12289, 2048, 8),  # runs capped at 48 rows: more workgroups than CUs
 ]
 
 

@@ -276,7 +276,11 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
 //    converted once (v_cvt_f32_i32 of a sign-extended byte) and accumulated
 //    for all 4 heads.
 // Partial records (m, l, acc[head_dim]) per split go to the combine kernel.
-constexpr int kAt = 64;  // tokens per tile
+// A tile is KT = 64 tokens, or 32 when the context is short enough that each
+// wave would hold a single 64-token tile (its chain of K / V load, QK,
+// softmax and PV then sets the time, and half a tile halves it).
+constexpr int kAt = 64;     // tokens per tile
+constexpr int kAtMin = 32;  // short contexts
 
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
@@ -298,7 +302,7 @@ __device__ __forceinline__ float row16_sum(float v) {
 
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
-template <int HD, int NWV>
+template <int HD, int NWV, int KT>
 __global__ __launch_bounds__(64 * NWV, HD == 256 ? 1 : 8 / NWV) void paged_attn_mfma_kernel(
     const float* __restrict__ q, const int8_t* __restrict__ kc, const float* __restrict__ ks,
     const int8_t* __restrict__ vc, const float* __restrict__ vs, const int32_t* __restrict__ tables,
@@ -307,9 +311,12 @@ __global__ __launch_bounds__(64 * NWV, HD == 256 ? 1 : 8 / NWV) void paged_attn_
   constexpr int NMI = HD / 64;  // MFMAs per 16-token sub-tile
   constexpr int VD = HD / 16;   // dims per lane in the PV layout
   constexpr int VW = VD / 4;    // V dwords per lane per round
-  __shared__ float p_s[NWV][kAt * 4];     // per wave: p * v_scale [token][head]
-  __shared__ int row_s[NWV][2 * kAt];     // per wave, two tiles: pool row of each token
-  __shared__ float ks_s[NWV][2 * kAt], vs_s[NWV][2 * kAt];
+  constexpr int NSUB = KT / 16;  // QK sub-tiles of 16 tokens
+  constexpr int NRR = KT / 4;    // PV rounds of 4 tokens
+  static_assert(KT == 64 || KT == 32, "tile of 64 or 32 tokens");
+  __shared__ float p_s[NWV][KT * 4];     // per wave: p * v_scale [token][head]
+  __shared__ int row_s[NWV][2 * KT];     // per wave, two tiles: pool row of each token
+  __shared__ float ks_s[NWV][2 * KT], vs_s[NWV][2 * KT];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   // kv_major: the NWV waves take NWV KV heads of one split, so the slices of
@@ -401,24 +408,26 @@ __global__ __launch_bounds__(64 * NWV, HD == 256 ? 1 : 8 / NWV) void paged_attn_
   // Software pipeline over the split's tiles (two register / LDS slots):
   // while tile i is computed, the K and V of tile i+1 and the block-table
   // entries of tile i+2 are in flight.
-  const int n_tiles = s_end > s_begin ? (s_end - s_begin + kAt - 1) / kAt : 0;
+  const int n_tiles = s_end > s_begin ? (s_end - s_begin + KT - 1) / KT : 0;
   auto tok_row = [&](int tab, int t) { return tab * (1 << bs_log2) + (t & bs_mask); };
-  auto tile_tok = [&](int i) { return min(s_begin + i * kAt + lane, s_end - 1); };
+  // token of lane l < KT in tile i (lanes past KT repeat a valid token; only
+  // lanes < KT store rows and scales)
+  auto tile_tok = [&](int i) { return min(s_begin + i * KT + lane, s_end - 1); };
   int tab_n = 0, row_n = 0;
   float ks_n = 0.f, vs_n = 0.f;
-  i32x4 kb[2][4][NMI];
-  uint32_t vraw[2][16][VW];
+  i32x4 kb[2][NSUB][NMI];
+  uint32_t vraw[2][NRR][VW];
   auto issue_kv = [&](auto slot_c) {  // K and V of the tile whose rows sit in rw[slot]
     constexpr int sl = decltype(slot_c)::value;
-    const int* rws = rw + sl * kAt;
+    const int* rws = rw + sl * KT;
 #pragma unroll
-    for (int sub = 0; sub < 4; sub++) {
+    for (int sub = 0; sub < NSUB; sub++) {
       const int8_t* kp = kc + (size_t)rws[16 * sub + r] * kv_dim + (size_t)kvh * HD + 16 * c;
 #pragma unroll
       for (int mi = 0; mi < NMI; mi++) kb[sl][sub][mi] = *reinterpret_cast<const i32x4*>(kp + 64 * mi);
     }
 #pragma unroll
-    for (int rr = 0; rr < 16; rr++) {
+    for (int rr = 0; rr < NRR; rr++) {
       const int8_t* vp = vc + (size_t)rws[4 * rr + tg] * kv_dim + (size_t)kvh * HD + VD * dg;
       if constexpr (VW == 1) {
         vraw[sl][rr][0] = *reinterpret_cast<const uint32_t*>(vp);
@@ -434,7 +443,7 @@ __global__ __launch_bounds__(64 * NWV, HD == 256 ? 1 : 8 / NWV) void paged_attn_
   if (n_tiles > 0) {  // prologue: rows and K / V of tile 0, table entry of tile 1
     const int t = tile_tok(0);
     row_n = tok_row(table[t >> bs_log2], t);
-    rw[lane] = row_n;
+    if (lane < KT) rw[lane] = row_n;
     ks_n = ks[row_n];
     vs_n = vs[row_n];
     const int t1 = tile_tok(1);
@@ -444,15 +453,17 @@ __global__ __launch_bounds__(64 * NWV, HD == 256 ? 1 : 8 / NWV) void paged_attn_
 
   auto tile = [&](auto slot_c, int i) {
     constexpr int sl = decltype(slot_c)::value;
-    const int t0 = s_begin + i * kAt;
-    float* ksl = ksw + sl * kAt;
-    float* vsl = vsw + sl * kAt;
-    ksl[lane] = ks_n;  // scales of tile i (loaded one iteration ago)
-    vsl[lane] = vs_n;
+    const int t0 = s_begin + i * KT;
+    float* ksl = ksw + sl * KT;
+    float* vsl = vsw + sl * KT;
+    if (lane < KT) {  // scales of tile i (loaded one iteration ago)
+      ksl[lane] = ks_n;
+      vsl[lane] = vs_n;
+    }
     {  // rows of tile i+1, their scales, the table entry of tile i+2, then K and V of tile i+1
       const int t = tile_tok(i + 1);
       row_n = tok_row(tab_n, t);
-      rw[(sl ^ 1) * kAt + lane] = row_n;
+      if (lane < KT) rw[(sl ^ 1) * KT + lane] = row_n;
       ks_n = ks[row_n];
       vs_n = vs[row_n];
       const int t2 = tile_tok(i + 2);
@@ -460,9 +471,9 @@ __global__ __launch_bounds__(64 * NWV, HD == 256 ? 1 : 8 / NWV) void paged_attn_
       issue_kv(std::integral_constant<int, sl ^ 1>{});
     }
     // scores of head c, tokens 16*sub + r
-    float sc[4];
+    float sc[NSUB];
 #pragma unroll
-    for (int sub = 0; sub < 4; sub++) {
+    for (int sub = 0; sub < NSUB; sub++) {
       i32x4 cacc = i32x4{0, 0, 0, 0};
 #pragma unroll
       for (int mi = 0; mi < NMI; mi++)
@@ -472,18 +483,24 @@ __global__ __launch_bounds__(64 * NWV, HD == 256 ? 1 : 8 / NWV) void paged_attn_
       sc[sub] = valid ? sv * qscale * ksl[16 * sub + r] * inv_sqrt : -INFINITY;
     }
     // online softmax of head c over the tile
-    const float tmax = row16_max(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
+    float tm = fmaxf(sc[0], sc[1]);
+    if constexpr (NSUB == 4) tm = fmaxf(tm, fmaxf(sc[2], sc[3]));
+    const float tmax = row16_max(tm);
     const float m_new = fmaxf(run_m, tmax);
-    float corr = 1.0f, p[4] = {0.f, 0.f, 0.f, 0.f};
+    float corr = 1.0f, p[NSUB];
+#pragma unroll
+    for (int sub = 0; sub < NSUB; sub++) p[sub] = 0.f;
     if (m_new != -INFINITY) {
       corr = __expf(run_m - m_new);
 #pragma unroll
-      for (int sub = 0; sub < 4; sub++) p[sub] = __expf(sc[sub] - m_new);
+      for (int sub = 0; sub < NSUB; sub++) p[sub] = __expf(sc[sub] - m_new);
     }
-    run_l = run_l * corr + row16_sum((p[0] + p[1]) + (p[2] + p[3]));
+    float ps = p[0] + p[1];
+    if constexpr (NSUB == 4) ps = ps + (p[2] + p[3]);
+    run_l = run_l * corr + row16_sum(ps);
     run_m = m_new;
 #pragma unroll
-    for (int sub = 0; sub < 4; sub++) pw[(16 * sub + r) * 4 + c] = p[sub] * vsl[16 * sub + r];
+    for (int sub = 0; sub < NSUB; sub++) pw[(16 * sub + r) * 4 + c] = p[sub] * vsl[16 * sub + r];
     // rescale the PV accumulators by each head's correction
 #pragma unroll
     for (int h = 0; h < 4; h++) {
@@ -493,7 +510,7 @@ __global__ __launch_bounds__(64 * NWV, HD == 256 ? 1 : 8 / NWV) void paged_attn_
     }
     // PV
 #pragma unroll
-    for (int rr = 0; rr < 16; rr++) {
+    for (int rr = 0; rr < NRR; rr++) {
       const float4 pv = *reinterpret_cast<const float4*>(&pw[(4 * rr + tg) * 4]);
       const float ph[4] = {pv.x, pv.y, pv.z, pv.w};
       float f[VD];
@@ -547,12 +564,14 @@ __global__ __launch_bounds__(64 * NWV, HD == 256 ? 1 : 8 / NWV) void paged_attn_
 // clamped, so every load is unconditional; splits past the end are masked
 // after loading).  The CG running triples are then merged through LDS.  One
 // memory round trip for up to 8 CG splits, where a max / weights / sum pass
-// over the partials would take three.
+// over the partials would take three.  CG fills 1024 threads, so the 129
+// splits of a 4097-token context (32-token tiles) take three round trips per
+// group.
 constexpr int kMaxSplits = 1024;
 
 template <int HD>
 constexpr int combine_groups() {
-  return HD >= 256 ? 2 : 512 / HD;
+  return 1024 / HD;
 }
 
 template <int HD>
@@ -670,17 +689,21 @@ bool paged_mfma_ok(const PagedAttnArgs& a) {
 
 // Splits of the context for the matrix-core kernel: about 8 wavefronts per CU,
 // whole 64-token tiles.
-void paged_mfma_splits(const PagedAttnArgs& a, int* n_splits, int* split_len) {
+// Split length (a multiple of the tile) for about 8 waves per CU; the
+// 32-token tile when even 64-token splits leave fewer waves than that.
+void paged_mfma_splits(const PagedAttnArgs& a, int* n_splits, int* split_len, int* tile) {
   const int group = a.n_head / a.n_head_kv;
   const int units = a.n_seq * a.n_head_kv * ((group + 3) / 4);
   const int target = device_cu_count() * 8;
   const int want = std::max(1, (target + units - 1) / units);
-  int len = (a.max_ctx + want - 1) / want;
-  len = std::max(kAt, (len + kAt - 1) / kAt * kAt);
+  const int raw = (a.max_ctx + want - 1) / want;
+  const int kt = raw <= kAtMin && (a.max_ctx + kAtMin - 1) / kAtMin <= kMaxSplits ? kAtMin : kAt;
+  int len = std::max(kt, (raw + kt - 1) / kt * kt);
   len = std::max(len, (a.max_ctx + kMaxSplits - 1) / kMaxSplits);
-  len = (len + kAt - 1) / kAt * kAt;
+  len = (len + kt - 1) / kt * kt;
   *split_len = len;
   *n_splits = std::max(1, (a.max_ctx + len - 1) / len);
+  *tile = kt;
 }
 
 }  // namespace
@@ -688,8 +711,8 @@ void paged_mfma_splits(const PagedAttnArgs& a, int* n_splits, int* split_len) {
 size_t paged_attn_workspace_bytes(const PagedAttnArgs& a, int* n_splits_out) {
   int n;
   if (paged_mfma_ok(a)) {
-    int len;
-    paged_mfma_splits(a, &n, &len);
+    int len, kt;
+    paged_mfma_splits(a, &n, &len, &kt);
   } else {
     n = pick_splits(a.n_seq * a.n_head_kv, a.max_ctx);
   }
@@ -699,8 +722,8 @@ size_t paged_attn_workspace_bytes(const PagedAttnArgs& a, int* n_splits_out) {
 
 template <int HD>
 hipError_t run_paged_mfma(const PagedAttnArgs& a, float* part, hipStream_t s) {
-  int n_splits, split_len;
-  paged_mfma_splits(a, &n_splits, &split_len);
+  int n_splits, split_len, kt;
+  paged_mfma_splits(a, &n_splits, &split_len, &kt);
   const int group = a.n_head / a.n_head_kv, n_hchunks = (group + 3) / 4;
   // one workgroup per split over 8 (else 4) KV heads when they divide n_head_kv
   auto go = [&](auto nwv_c, bool kv_major) {
@@ -709,10 +732,16 @@ hipError_t run_paged_mfma(const PagedAttnArgs& a, float* part, hipStream_t s) {
         ? dim3((unsigned)n_splits, (unsigned)(a.n_head_kv / NWV * n_hchunks), (unsigned)a.n_seq)
         : dim3((unsigned)((n_splits + NWV - 1) / NWV), (unsigned)(a.n_head_kv * n_hchunks), (unsigned)a.n_seq);
     if (grid.y > 65535 || grid.z > 65535) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((paged_attn_mfma_kernel<HD, NWV>), grid, dim3(64 * NWV), 0, s, a.q, a.k_codes,
-                       a.k_scales, a.v_codes, a.v_scales, a.block_tables, a.ctx_lens,
-                       a.max_blocks_per_seq, log2_exact(a.block_size), a.n_head, a.n_head_kv,
-                       n_hchunks, split_len, n_splits, kv_major, part);
+    if (kt == kAtMin)
+      hipLaunchKernelGGL((paged_attn_mfma_kernel<HD, NWV, kAtMin>), grid, dim3(64 * NWV), 0, s, a.q, a.k_codes,
+                         a.k_scales, a.v_codes, a.v_scales, a.block_tables, a.ctx_lens,
+                         a.max_blocks_per_seq, log2_exact(a.block_size), a.n_head, a.n_head_kv,
+                         n_hchunks, split_len, n_splits, kv_major, part);
+    else
+      hipLaunchKernelGGL((paged_attn_mfma_kernel<HD, NWV, kAt>), grid, dim3(64 * NWV), 0, s, a.q, a.k_codes,
+                         a.k_scales, a.v_codes, a.v_scales, a.block_tables, a.ctx_lens,
+                         a.max_blocks_per_seq, log2_exact(a.block_size), a.n_head, a.n_head_kv,
+                         n_hchunks, split_len, n_splits, kv_major, part);
     return hipGetLastError();
   };
   hipError_t e0;

@@ -121,8 +121,8 @@ __global__ __launch_bounds__(768, 1) void mv_q8r(const uint8_t* __restrict__ w, 
 
   // ---- this wave's weights: step s is unit 4 s + kg of its quarter of row
   // g_row0 + n (rows past the workgroup's run repeat its last row, and idle
-  // waves load that row too: their sums are not stored).  kRd steps are
-  // requested before x is staged and each later one as the step kRd before it
+  // waves load that row too: their sums are not stored).  D steps are
+  // requested before x is staged and each later one as the step D before it
   // is taken up: a workgroup keeps about 50-100 KB in flight, what one CU
   // sustains (with every step requested at once the waves stall at issue for
   // microseconds and the x staging and all of the arithmetic come after the

@@ -814,15 +814,28 @@ __global__ __launch_bounds__(768) void mv_b1(const uint8_t* __restrict__ w,
     n_rows = (int)((gs + 1) * out_dim / n_streams) - r_begin;
   }
   const int ubase = kw * 64 * UPL + lane;
+  // The segments' weight pointers as a base and two offsets: selecting an
+  // offset per row is register arithmetic, where a select of the three
+  // pointers is compiled as an indexed load of the kernel argument.
+  [[maybe_unused]] const uint8_t* fw0 = nullptr;
+  [[maybe_unused]] ptrdiff_t fd1 = 0, fd2 = 0;
+  if constexpr (FUSE >= 2) {
+    fw0 = fu.w0;
+    fd1 = fu.w1 - fu.w0;
+    fd2 = fu.w2 - fu.w0;
+  }
 
   uint32_t buf[RMAX][UPL][NW];
   auto load_row = [&](int rr) {
     const int row = max(0, min(r_begin + rr * r_step, out_dim - 1));
     const uint8_t* rp;
     if constexpr (FUSE >= 2) {
+      // The row is wave-uniform: taken as a scalar, the segment's weight
+      // pointer is scalar arithmetic.  A load of the pointer would need a
+      // wait that drains the rows still in flight.
       int r;
-      const int sg = fuse_seg(fu, row, r);
-      rp = (sg == 0 ? fu.w0 : sg == 1 ? fu.w1 : fu.w2) + (size_t)r * row_bytes;
+      const int sg = fuse_seg(fu, __builtin_amdgcn_readfirstlane(row), r);
+      rp = fw0 + (sg == 0 ? 0 : sg == 1 ? fd1 : fd2) + (size_t)r * row_bytes;
     } else {
       rp = w + (size_t)row * row_bytes;
     }

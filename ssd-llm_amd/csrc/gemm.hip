@@ -123,7 +123,7 @@ __global__ __launch_bounds__(512) void gemm_prep_x(const uint16_t* __restrict__ 
   for (int i = 0; i < 8; i++) {
     const float xs = ldexpf(a[i], sh);  // exact: a power of two, no overflow (|xs| < 2^10)
     const _Float16 hv = (_Float16)xs;
-    h[i] = hv;
+    h[((i & 3) << 1) | (i >> 2)] = hv;  // the element order of codes_times_s: 0, 4, 1, 5, 2, 6, 3, 7
     lost += fabsf(ldexpf(xs - (float)hv, -sh));  // the difference is exact in fp32
     sum += xs;
   }
@@ -160,23 +160,51 @@ __global__ __launch_bounds__(512) void gemm_prep_x(const uint16_t* __restrict__ 
   reinterpret_cast<h8*>(xp)[((size_t)m16 * (K / 32) + (size_t)blk * 8) * 64 + threadIdx.x] = tile[threadIdx.x];
 }
 
-// Two 4-bit codes per byte -> 8 fp16 values s*q in element order (byte i:
-// low nibble = element 2i, high nibble = element 2i+1).  fp16 bits 0x6400 + v
-// are 1024 + v exactly for v < 1024, and s*q <= 945.
-__device__ __forceinline__ h8 codes_times_s(uint32_t qd, uint32_t s2) {
-  const uint32_t ql = qd & 0x0F0F0F0Fu, qh = (qd >> 4) & 0x0F0F0F0Fu;
-  const u16x2 sv = __builtin_bit_cast(u16x2, s2);
-  h8 r;
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    // bytes: low nibble of byte i, 0, high nibble of byte i, 0
-    const uint32_t u = __builtin_amdgcn_perm(qh, ql, (uint32_t)i | 0x0C00u | ((uint32_t)(4 + i) << 16) | 0x0C000000u);
-    const u16x2 vv = __builtin_bit_cast(u16x2, u) * sv + (u16x2){0x6400, 0x6400};
-    const h2 hv = __builtin_bit_cast(h2, vv) - (h2){(_Float16)1024.f, (_Float16)1024.f};
-    r[2 * i] = hv.x;
-    r[2 * i + 1] = hv.y;
-  }
+// The scale constants of codes_times_s for one (column, sub-block) with
+// 6-bit scale s: fp16 pairs (s, s), (-1024 s, -1024 s), (s/16, s/16) and
+// (-64 s, -64 s), all exact.
+struct SubScale {
+  uint32_t s1, c1, s2, c2;
+};
+__device__ __forceinline__ SubScale sub_scale(uint32_t s) {
+  // fp16 bits 0x6400 + s are 1024 + s exactly (s < 1024)
+  const h2 sv = __builtin_bit_cast(h2, (s | (s << 16)) | 0x64006400u) - (h2){(_Float16)1024.f, (_Float16)1024.f};
+  SubScale k;
+  k.s1 = __builtin_bit_cast(uint32_t, sv);
+  k.c1 = __builtin_bit_cast(uint32_t, sv * (h2){(_Float16)-1024.f, (_Float16)-1024.f});
+  k.s2 = __builtin_bit_cast(uint32_t, sv * (h2){(_Float16)0.0625f, (_Float16)0.0625f});
+  k.c2 = __builtin_bit_cast(uint32_t, sv * (h2){(_Float16)-64.f, (_Float16)-64.f});
+  return k;
+}
+
+// One dword of codes (8 elements: byte i holds element 2i in its low nibble
+// and 2i+1 in its high nibble) -> the 8 fp16 values s*q in the order
+// 0, 4, 1, 5, 2, 6, 3, 7 (the prepared X uses the same order; the MFMA sums
+// over k in any order).  Each fp16 pair is one mask-and-bias of the codes:
+// bits 0x6400 + v are 1024 + v exactly for v < 1024, with v = q (low nibbles)
+// or 16 q (high nibbles), and one fma takes it to s*q: s (1024 + q) - 1024 s
+// and (s/16) (1024 + 16 q) - 64 s are exact before the fma's single rounding,
+// and their value s*q <= 945 is an fp16 integer, so the result is exact.
+// (a & m) | b in one instruction: VOP3 takes no literal here and one scalar
+// operand, so the mask comes in a scalar register and the bias in a vector
+// register (written with two literals, the compiler emits an and and an or).
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t b) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(m), "v"(b));
   return r;
+}
+
+__device__ __forceinline__ h8 codes_times_s(uint32_t qd, const SubScale& k, uint32_t bias) {
+  const uint32_t q8 = qd >> 8;
+  const h2 b0 = __builtin_bit_cast(h2, and_or(qd, 0x000F000Fu, bias));  // elements 0, 4
+  const h2 b1 = __builtin_bit_cast(h2, and_or(qd, 0x00F000F0u, bias));  // 1, 5 (16 q)
+  const h2 b2 = __builtin_bit_cast(h2, and_or(q8, 0x000F000Fu, bias));  // 2, 6
+  const h2 b3 = __builtin_bit_cast(h2, and_or(q8, 0x00F000F0u, bias));  // 3, 7 (16 q)
+  const h2 s1 = __builtin_bit_cast(h2, k.s1), c1 = __builtin_bit_cast(h2, k.c1);
+  const h2 s2 = __builtin_bit_cast(h2, k.s2), c2 = __builtin_bit_cast(h2, k.c2);
+  const h2 r0 = __builtin_elementwise_fma(s1, b0, c1), r1 = __builtin_elementwise_fma(s2, b1, c2);
+  const h2 r2 = __builtin_elementwise_fma(s1, b2, c1), r3 = __builtin_elementwise_fma(s2, b3, c2);
+  return h8{r0.x, r0.y, r1.x, r1.y, r2.x, r2.y, r3.x, r3.y};
 }
 
 // 4 bytes (values < 1024) -> fp16 values: bytes 0, 1 -> r[0], bytes 2, 3 -> r[1]
@@ -413,14 +441,16 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void gemm_q4k_mfma(GEMM_MATS
 #pragma unroll
     for (int j = 0; j < NT; j++) tot[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
+  const uint32_t bias = opaque(0x64006400u);  // fp16 pair (1024, 1024), kept in a register
+  const uint32_t mkeep = lane < 32 ? 0xFFFFFFFFu : 0u;  // min-term B lanes that carry the mins
   // One MFMA step t (0-7) of a super-block, X from LDS stage buffer xs
-  auto step = [&](auto t_c, const h8* xs, const uint32_t (&s2)[NT][2], const u32x4a4 (&cd)[NT]) {
+  auto step = [&](auto t_c, const h8* xs, const SubScale (&s2)[NT][2], const u32x4a4 (&cd)[NT]) {
     constexpr int t = decltype(t_c)::value;
     h8 bf[NT];
 #pragma unroll
     for (int j = 0; j < NT; j++) {
       const uint32_t qd = (t & 3) == 0 ? cd[j].x : (t & 3) == 1 ? cd[j].y : (t & 3) == 2 ? cd[j].z : cd[j].w;
-      bf[j] = codes_times_s(qd, s2[j][t >> 2]);
+      bf[j] = codes_times_s(qd, s2[j][t >> 2], bias);
     }
 #pragma unroll
     for (int m4 = 0; m4 < MT; m4 += 4) {
@@ -447,7 +477,8 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void gemm_q4k_mfma(GEMM_MATS
     // this super-block's scales (reference unpacking, compute.rs:724-735):
     // s[0..3] = sc[0..3] & 63, s[4..7] = sc[0..3] >> 6 | (sc[8..11] & 15) << 2,
     // m[0..3] = sc[4..7] & 63, m[4..7] = sc[4..7] >> 6 | (sc[8..11] >> 4) << 2
-    uint32_t s2[NT][2], mlo[NT], mhi[NT], dbits[NT];
+    SubScale s2[NT][2];
+    uint32_t mlo[NT], mhi[NT], dbits[NT];
 #pragma unroll
     for (int j = 0; j < NT; j++) {
       const u32x4a4 hdr = hdr_n[j];
@@ -458,8 +489,8 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void gemm_q4k_mfma(GEMM_MATS
       mlo[j] = h2v & 0x3F3F3F3Fu;
       mhi[j] = ((h2v >> 6) & 0x03030303u) | (((h3 >> 4) & 0x0F0F0F0Fu) << 2);
       const uint32_t sa = (slo >> (8 * c)) & 0xFFu, sb = (shi >> (8 * c)) & 0xFFu;
-      s2[j][0] = sa | (sa << 16);
-      s2[j][1] = sb | (sb << 16);
+      s2[j][0] = sub_scale(sa);
+      s2[j][1] = sub_scale(sb);
       dbits[j] = hdr.x;
     }
     step(std::integral_constant<int, 0>{}, xa, s2, cd0);
@@ -475,15 +506,17 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void gemm_q4k_mfma(GEMM_MATS
     step(std::integral_constant<int, 5>{}, xb, s2, cd1);
     step(std::integral_constant<int, 6>{}, xb, s2, cd1);
     step(std::integral_constant<int, 7>{}, xb, s2, cd1);
-    // min term: A = XS hi (lanes 0-15) / lo (16-31) / zeros (32-63), B = the
-    // 8 mins m in every lane group (finite, so the zero A lanes add 0)
+    // min term: A = XS hi (lanes 0-15) / lo (16-31) / hi, lo again (32-63),
+    // B = the 8 mins m in lanes 0-31 and zeros in lanes 32-63, so only the
+    // hi + lo pair is summed.  A row's XS are finite unless the row is
+    // flagged, and a flagged row's MFMA results are never stored.
     h8 bmin[NT];
     float dd[NT], dm[NT];
 #pragma unroll
     for (int j = 0; j < NT; j++) {
       uint32_t mv[4];
-      bytes_to_f16(mlo[j], mv);
-      bytes_to_f16(mhi[j], mv + 2);
+      bytes_to_f16(mlo[j] & mkeep, mv);
+      bytes_to_f16(mhi[j] & mkeep, mv + 2);
       bmin[j] = __builtin_bit_cast(h8, u32x4{mv[0], mv[1], mv[2], mv[3]});
       // opaque: kept as f32 values, not folded into v_fma_mix_f32 (slower here)
       dd[j] = __uint_as_float(opaque(__float_as_uint(f16_to_f32(dbits[j] & 0xFFFFu))));
@@ -492,8 +525,7 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void gemm_q4k_mfma(GEMM_MATS
     const h8* sums = &xsl[b & 1][0];
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
-      const h8 raw = sums[(mt >> 1) * 64 + (mt & 1) * 32 + (lane & 31)];
-      const h8 amin = lane < 32 ? raw : h8{};
+      const h8 amin = sums[(mt >> 1) * 64 + (mt & 1) * 32 + (lane & 31)];
       const f4 rs = xel[b & 1][mt * 4 + c];  // 2^-sh of rows 4c .. 4c+3
 #pragma unroll
       for (int j = 0; j < NT; j++) {

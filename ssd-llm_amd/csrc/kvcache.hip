@@ -95,8 +95,12 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
 // issued first.  Straight-line code (rows past the end are clamped to the
 // last row, quantized again to the same bits; FULL = len == NV*256 drops the
 // per-lane bounds tests): a loop or a memory access under a branch makes the
-// compiler wait for every outstanding load.
-constexpr int kRowsPerWave = 4;
+// compiler wait for every outstanding load.  Every input and code byte is
+// touched once, by one instruction per 1 KB or 256 B, so loads and stores are
+// nontemporal: at config 5a (2 GiB in, 512 MiB out) 492 -> 430 us, and one row
+// per wave is faster than four (464 against 492 us with ordinary loads).
+constexpr int kRowsPerWave = 1;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 template <int NV, bool FULL>
 __global__ __launch_bounds__(256) void kv_quantize_pipe_kernel(const float* __restrict__ in,
@@ -116,8 +120,12 @@ __global__ __launch_bounds__(256) void kv_quantize_pipe_kernel(const float* __re
 #pragma unroll
     for (int i = 0; i < NV; i++) {
       const int e = (i * 64 + lane) * 4;
-      rv[k][i] = (FULL || e < len) ? *reinterpret_cast<const float4*>(src + e)
-                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+      if (FULL || e < len) {
+        const f32x4 t = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(src + e));
+        rv[k][i] = make_float4(t.x, t.y, t.z, t.w);
+      } else {
+        rv[k][i] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
     }
   }
 #pragma unroll
@@ -137,8 +145,8 @@ __global__ __launch_bounds__(256) void kv_quantize_pipe_kernel(const float* __re
       // amax == 0 gives inv == 0 and so codes 0 (NaN inputs map to 0 too):
       // no branch needed
       if (FULL || e < len)
-        *reinterpret_cast<uint32_t*>(dst + e) =
-            pack4(rv[k][i].x, rv[k][i].y, rv[k][i].z, rv[k][i].w, inv);
+        __builtin_nontemporal_store(pack4(rv[k][i].x, rv[k][i].y, rv[k][i].z, rv[k][i].w, inv),
+                                    reinterpret_cast<uint32_t*>(dst + e));
     }
     if (lane == 0) scales[row] = amax / 127.0f;  // 0 when amax == 0
   }

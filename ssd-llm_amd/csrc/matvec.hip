@@ -1005,6 +1005,122 @@ __global__ __launch_bounds__(768) void mv_b1s(const uint8_t* __restrict__ w, con
   }
 }
 
+// One 16-byte nontemporal load per lane straight into LDS: lane l writes
+// bytes [16 l, 16 l + 16) above the wave-uniform LDS offset lds.  Inline
+// assembly, so the compiler neither counts nor waits for it: the kernel waits
+// for these loads itself.  M0 is restored.
+__device__ __forceinline__ void dma16_nt(const void* g, uint32_t lds) {
+  uint32_t keep;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %2, off nt\n\ts_mov_b32 m0, %0"
+               : "=&s"(keep)
+               : "s"(lds), "v"(g)
+               : "memory");
+}
+
+// Q4_K row streams as mv_b1s, with each row slice (at most 16 blocks, 2304
+// bytes) copied into a per-wave LDS slot by three contiguous 1 KB nontemporal
+// loads, so every 128-byte line of the matrix is requested once, by one
+// instruction (the three overlapping per-unit loads of load_unit hit each line
+// up to three times, which only the vector cache absorbs, and the
+// nontemporal hint bypasses it).  D slots form the rolling window; a row's
+// copy is waited for with an exact count (three copies per later row), so the
+// loop holds no other vector memory instruction: row sums go to LDS and are
+// stored after the loop.  (The compiler's wait for x, which does not count
+// the copies, drains the first rows' copies before x is staged; staging x
+// through the same LDS copies instead measured slower.)  Used for long row
+// streams only: 28672 x 8192 Q4_K (19 rows per wave) 27.4 -> 26.2 us, while
+// 4096 x 14336 (5 rows per wave) was 3% slower than mv_b1s.
+template <int D, bool FULL, int SIT>
+__global__ __launch_bounds__(768) void mv_b1s_lds(const uint8_t* __restrict__ w, const float* __restrict__ x,
+                                                  float* __restrict__ y, int out_dim, int row_bpr, int slice_bpr,
+                                                  int rows_cap) {
+  constexpr int F = kQ4_K;
+  constexpr int US = Dig<F>::US, SLOT = 3072, NC = 3;
+  extern __shared__ uint4 lds4[];
+  uint32_t* lds = reinterpret_cast<uint32_t*>(lds4);
+  const int blk0 = blockIdx.y * slice_bpr;
+  const int bpr = min(slice_bpr, row_bpr - blk0);
+  w += (size_t)blk0 * Geom<F>::bb;
+  x += (size_t)blk0 * Geom<F>::bs;
+  y += (size_t)blockIdx.y * out_dim;
+  const int keff = bpr * Geom<F>::bs;
+  const int U = keff / FastUnit<F>::E;
+  const int nbytes = bpr * Geom<F>::bb;  // <= 2304
+  const int lane = threadIdx.x & 63, nwaves = blockDim.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // scalar: the LDS slots' M0 base
+  const size_t row_bytes = (size_t)row_bpr * Geom<F>::bb;
+  const long n_streams = (long)gridDim.x * nwaves, gs = (long)blockIdx.x * nwaves + wave;
+  const int r_begin = (int)(gs * out_dim / n_streams);
+  const int n_rows = (int)((gs + 1) * out_dim / n_streams) - r_begin;
+  const int r_last = r_begin + max(n_rows, 1) - 1;
+  const int u = FULL ? lane : min(lane, U - 1);
+  uint8_t* wl = reinterpret_cast<uint8_t*>(lds4) + (size_t)U * US * sizeof(uint32_t);
+  float* red = reinterpret_cast<float*>(wl + (size_t)nwaves * D * SLOT) + (size_t)wave * rows_cap;
+  wl += (size_t)wave * D * SLOT;
+  const uint32_t wl_off = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)wl;
+
+  // Copy k of a row slice: lanes whose 16 bytes lie in the slice (a whole
+  // slice of 2304 bytes fills copies 0 and 1 and lanes 0-15 of copy 2), and
+  // lane 0 always (a dummy copy of the row's first bytes into the unused part
+  // of the slot when the slice ends before 1024 k), so that every row issues
+  // NC copies.
+  auto copy_row = [&](int rr, int sl) {
+    const uint8_t* rp = w + (size_t)min(r_begin + rr, r_last) * row_bytes;
+#pragma unroll
+    for (int k = 0; k < NC; k++) {
+      const int o = 1024 * k + 16 * lane;
+      if (o < nbytes || lane == 0) dma16_nt(rp + (o < nbytes ? o : 0), wl_off + sl * SLOT + 1024 * k);
+    }
+  };
+
+  XChunks<SIT> st;
+  stage_load<SIT>(x, keff, st, blockDim.x);
+#pragma unroll
+  for (int i = 0; i < D; i++) copy_row(i, i);
+  stage_store<F, SIT>(st, keff, lds, blockDim.x);
+  lds_barrier();
+  uint32_t pr[US];
+#pragma unroll
+  for (int t = 0; t < US; t += 4) {
+    const uint4 v = lds4[(size_t)u * (US / 4) + t / 4];
+    pr[t] = v.x; pr[t + 1] = v.y; pr[t + 2] = v.z; pr[t + 3] = v.w;
+  }
+  const bool live = FULL || lane < U;
+  const int boff = 144 * (u >> 2), qoff = boff + 16 + 32 * (u & 3);
+  for (int r0 = 0; r0 < n_rows; r0 += D) {
+#pragma unroll
+    for (int i = 0; i < D; i++) {
+      // the copies of row r0 + i have landed: NC copies per later row may be pending
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(((NC * (D - 1)) & 15) | (((NC * (D - 1)) >> 4) << 14) | (7 << 4) | (15 << 8));
+      __builtin_amdgcn_sched_barrier(0);
+      const uint8_t* sl = wl + i * SLOT;
+      uint32_t raw[12];
+      const uint4 h = *reinterpret_cast<const uint4*>(sl + boff);
+      const uint4 q0 = *reinterpret_cast<const uint4*>(sl + qoff);
+      const uint4 q1 = *reinterpret_cast<const uint4*>(sl + qoff + 16);
+      raw[0] = h.x; raw[1] = h.y; raw[2] = h.z; raw[3] = h.w;
+      raw[4] = q0.x; raw[5] = q0.y; raw[6] = q0.z; raw[7] = q0.w;
+      raw[8] = q1.x; raw[9] = q1.y; raw[10] = q1.z; raw[11] = q1.w;
+      float a = 0.f;
+      accumulate_dig<F>(raw, u, [&](int t) { return pr[t]; }, a);
+      // The slot's LDS reads complete before its next copy is requested: the
+      // compiler may issue the copy (inline assembly) right after the read
+      // instructions, and a copy served from the cache can land before reads
+      // still queued in the LDS pipeline.
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+      __builtin_amdgcn_sched_barrier(0);
+      copy_row(r0 + i + D, i);
+      a = wave_sum_l63(live ? a : 0.f);
+      if (lane == 63 && r0 + i < n_rows) red[r0 + i] = a;
+    }
+  }
+  // the window's last copies land before the workgroup's LDS is released
+  __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+  for (int r = lane; r < n_rows; r += 64) y[r_begin + r] = red[r];
+}
+
 // With res non-null, y = res + (the slice sum), the residual add of a decoder
 // layer (y may alias res: each thread reads its element before writing it),
 // and the slice sum itself also goes to sum_out.
@@ -1501,6 +1617,22 @@ hipError_t run_b1s(const uint8_t* w, const float* x, float* y, int out_dim, int 
                        slice_bpr);
     return hipGetLastError();
   };
+  if constexpr (F == kQ4_K) {
+    // weights through LDS (mv_b1s_lds): two 3 KB slots per wave and the row sums
+    const long n_streams = n_wg * 12;
+    const int rows_cap = (int)((out_dim + n_streams - 1) / n_streams) + 1;
+    const size_t lds2 = lds + (size_t)12 * 2 * 3072 + (size_t)12 * rows_cap * sizeof(float);
+    if (lds2 <= (size_t)lds_limit() && sit <= 2 && rows_cap > 12) {
+      auto go2 = [&](auto kern) {
+        hipError_t e = set_lds_attr(kern, lds2);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(kern, dim3((unsigned)n_wg, (unsigned)slices), dim3(768), lds2, s, w, x, y, out_dim,
+                           row_bpr, slice_bpr, rows_cap);
+        return hipGetLastError();
+      };
+      return sit <= 1 ? go2(mv_b1s_lds<2, FULL, 1>) : go2(mv_b1s_lds<2, FULL, 2>);
+    }
+  }
   switch (sit) {
     case 0:
     case 1: return go(mv_b1s<F, 2, FULL, 1>);

@@ -258,6 +258,7 @@ LONG_ROWS = [  # batch-1 rows of 129-256 units (K slices summed in slice order)
     (Q4_0, 300, 64 * 144), (Q4_0, 64, 64 * 256), (Q8_0, 129, 64 * 192), (Q8_0, 4096, 14336),
     # whole rows beyond one round of workgroups: per-wave row streams, one slice
     (Q4_0, 40000, 2048), (Q4_K, 50000, 4096), (Q6_K, 60000, 2048), (Q8_0, 33333, 1024),
+    (Q4_K, 40000, 2048),  # rows of 32 units through the LDS row copies: partial copies, dummy third copy
 ]
 
 

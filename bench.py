@@ -41,6 +41,10 @@ def parse():
     ap.add_argument("--ceiling", action="store_true",
                     help="plain streaming-read bandwidth versus size and the cost of an empty launch "
                          "(libssdq_probe.so), timed like the matvecs; prints one JSON line")
+    ap.add_argument("--mfma-ceiling", action="store_true",
+                    help="fp16 matrix-core rate of a register-operand MFMA loop (random or zero operands, "
+                         "0-4 VALU instructions per MFMA; libssdq_probe.so) and torch's fp16 GEMM at the "
+                         "config-4 shapes; prints one JSON line")
     ap.add_argument("--hipblaslt", action="store_true",
                     help="torch's fp16 GEMM (hipBLASLt) of the config-4 layer shapes on already "
                          "dequantized weights, for comparison with the Q4_K prefill GEMM; prints one JSON line")
@@ -189,6 +193,9 @@ def main():
         return
     if args.hipblaslt:
         print(json.dumps(hipblaslt_layer(torch)))
+        return
+    if args.mfma_ceiling:
+        print(json.dumps(mfma_ceiling(torch)))
         return
     timer = Timer(torch, graph=not args.eager)
     if args.layer:
@@ -426,8 +433,13 @@ def _probe_lib():
     lib.ssdq_probe_read.restype = ctypes.c_int
     lib.ssdq_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
                                     ctypes.c_void_p]
+    lib.ssdq_probe_read_nt.restype = ctypes.c_int
+    lib.ssdq_probe_read_nt.argtypes = lib.ssdq_probe_read.argtypes
     lib.ssdq_probe_empty.restype = ctypes.c_int
     lib.ssdq_probe_empty.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    lib.ssdq_probe_mfma.restype = ctypes.c_int
+    lib.ssdq_probe_mfma.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                    ctypes.c_int, ctypes.c_void_p]
     return lib
 
 
@@ -441,31 +453,90 @@ def read_ceiling(torch):
     timer = Timer(torch)
     sink = torch.zeros(65536, dtype=torch.int32, device="cuda")
     stream = lambda: torch.cuda.current_stream().cuda_stream
-    out = {"read": [], "empty_kernel_us": {}}
+    out = {"read": [], "read_nontemporal": [], "empty_kernel_us": {}}
     for mb in (4, 8, 16, 33.1, 48, 64, 128, 256, 512):
         nbytes = int(mb * 1e6) // 16 * 16 if mb == 33.1 else int(mb * (1 << 20))
         if mb == 33.1:
             nbytes = 33103872  # the headline matvec's algorithmic bytes
         n = copies_for(nbytes)
         bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1) for _ in range(n)]
-        best = None
-        for grid, block in ((256, 768), (512, 512), (1024, 256), (2048, 256), (2048, 512), (4096, 256)):
-            def step(i, grid=grid, block=block):
-                rc = lib.ssdq_probe_read(bufs[i % n].data_ptr(), nbytes, sink.data_ptr(), grid, block, stream())
-                if rc != 0:
-                    raise RuntimeError(f"ssdq_probe_read: hip error {rc}")
-            tr = timer.run(step, 200, 200)
-            us = tr["t_median"] / tr["steps"] * 1e6
-            if best is None or us < best[0]:
-                best = (us, grid, block)
-        out["read"].append({"bytes": nbytes, "us": round(best[0], 3), "GB/s": round(nbytes / best[0] / 1e3, 1),
-                            "pct_hbm_peak": round(100 * nbytes / best[0] / 1e3 / HBM_PEAK_GBS, 2),
-                            "grid": best[1], "block": best[2]})
+        for key, fn in (("read", lib.ssdq_probe_read), ("read_nontemporal", lib.ssdq_probe_read_nt)):
+            best = None
+            for grid, block in ((256, 768), (512, 512), (1024, 256), (2048, 256), (2048, 512), (4096, 256)):
+                def step(i, grid=grid, block=block, fn=fn):
+                    rc = fn(bufs[i % n].data_ptr(), nbytes, sink.data_ptr(), grid, block, stream())
+                    if rc != 0:
+                        raise RuntimeError(f"{key} probe: hip error {rc}")
+                tr = timer.run(step, 200, 200)
+                us = tr["t_median"] / tr["steps"] * 1e6
+                if best is None or us < best[0]:
+                    best = (us, grid, block)
+            out[key].append({"bytes": nbytes, "us": round(best[0], 3), "GB/s": round(nbytes / best[0] / 1e3, 1),
+                             "pct_hbm_peak": round(100 * nbytes / best[0] / 1e3 / HBM_PEAK_GBS, 2),
+                             "grid": best[1], "block": best[2]})
         del bufs
         torch.cuda.empty_cache()
     for grid, block in ((256, 256), (256, 768)):
         tr = timer.run(lambda i: lib.ssdq_probe_empty(grid, block, stream()), 200, 200)
         out["empty_kernel_us"][f"{grid}x{block}"] = round(tr["t_median"] / tr["steps"] * 1e6, 3)
+    return out
+
+
+def mfma_ceiling(torch):
+    """The fp16 matrix-core rate on this part: an MFMA loop with register
+    operands (eight independent v_mfma_f32_16x16x32_f16 chains per wave, 512
+    workgroups) on random or all-zero fp16 operands, with 0, 2 or 4 independent
+    VALU instructions after each MFMA; and torch.matmul in fp16 (hipBLASLt) at
+    the config-4 shapes and at 8192^3, on random and on zero inputs.  HIP
+    events around eager launches, best of 5."""
+    lib = _probe_lib()
+    stream = lambda: torch.cuda.current_stream().cuda_stream
+    src = {"random": (torch.rand(4096 * 8, device="cuda") * 2 - 1).to(torch.float16),
+           "zero": torch.zeros(4096 * 8, dtype=torch.float16, device="cuda")}
+    out = {"mfma_loop": [], "torch_matmul_fp16": []}
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def best_ms(fn, reps=5):
+        fn()
+        torch.cuda.synchronize()
+        best = None
+        for _ in range(reps):
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1)
+            best = ms if best is None else min(best, ms)
+        return best
+
+    grid, iters = 512, 4000
+    for block in (256, 512):
+        sink = torch.empty(grid * block, device="cuda")
+        for nv in (0, 1, 2):
+            for kind in ("random", "zero"):
+                def launch(kind=kind, nv=nv, block=block, sink=sink):
+                    rc = lib.ssdq_probe_mfma(src[kind].data_ptr(), sink.data_ptr(), iters, nv, grid, block, stream())
+                    if rc != 0:
+                        raise RuntimeError(f"ssdq_probe_mfma: hip error {rc}")
+                ms = best_ms(launch)
+                flop = 16384.0 * 8 * iters * grid * (block // 64)
+                tf = flop / ms / 1e9
+                out["mfma_loop"].append({"operands": kind, "valu_per_mfma": 2 * nv, "block": block,
+                                         "waves_per_simd": block // 128, "ms": round(ms, 4),
+                                         "TFLOP/s": round(tf, 1), "pct_bf16_peak": round(100 * tf / BF16_PEAK_TFLOPS, 2)})
+    for M, N, K in ((512, 28672, 4096), (512, 6144, 4096), (512, 4096, 4096), (512, 4096, 14336), (8192, 8192, 8192)):
+        for kind in ("random", "zero"):
+            a = torch.randn(M, K, device="cuda", dtype=torch.float16)
+            b = torch.randn(K, N, device="cuda", dtype=torch.float16)
+            if kind == "zero":
+                a.zero_()
+                b.zero_()
+            ms = best_ms(lambda: torch.matmul(a, b), 5)
+            tf = 2.0 * M * N * K / ms / 1e9
+            out["torch_matmul_fp16"].append({"M": M, "N": N, "K": K, "inputs": kind, "us": round(ms * 1e3, 1),
+                                             "TFLOP/s": round(tf, 1),
+                                             "pct_bf16_peak": round(100 * tf / BF16_PEAK_TFLOPS, 2)})
+            del a, b
     return out
 
 

@@ -1017,25 +1017,33 @@ __device__ __forceinline__ void dma16_nt(const void* g, uint32_t lds) {
                : "memory");
 }
 
-// Q4_K row streams as mv_b1s, with each row slice (at most 16 blocks, 2304
-// bytes) copied into a per-wave LDS slot by three contiguous 1 KB nontemporal
-// loads, so every 128-byte line of the matrix is requested once, by one
-// instruction (the three overlapping per-unit loads of load_unit hit each line
-// up to three times, which only the vector cache absorbs, and the
-// nontemporal hint bypasses it).  D slots form the rolling window; a row's
-// copy is waited for with an exact count (three copies per later row), so the
-// loop holds no other vector memory instruction: row sums go to LDS and are
-// stored after the loop.  (The compiler's wait for x, which does not count
-// the copies, drains the first rows' copies before x is staged; staging x
-// through the same LDS copies instead measured slower.)  Used for long row
-// streams only: 28672 x 8192 Q4_K (19 rows per wave) 27.4 -> 26.2 us, while
-// 4096 x 14336 (5 rows per wave) was 3% slower than mv_b1s.
-template <int D, bool FULL, int SIT>
+// Row streams as mv_b1s, with each row slice (at most 64 units) copied into a
+// per-wave LDS slot by contiguous 1 KB nontemporal loads, so every 128-byte
+// line of the matrix is requested once, by one instruction (the overlapping
+// per-unit loads of load_unit hit a line up to three times, which only the
+// vector cache absorbs, and the nontemporal hint bypasses it); load_unit then
+// reads the unit from the slot at the same byte offsets.  The slice must start
+// 16-byte aligned in memory (the slot keeps its alignment, which the Q6_K
+// realignment reads).  D slots form the rolling window; a row's copies are
+// waited for with an exact count (NC per later row), so the loop holds no
+// other vector memory instruction: row sums go to LDS and are stored after
+// the loop.  (The compiler's wait for x, which does not count the copies,
+// drains the first rows' copies before x is staged; staging x through the
+// same LDS copies instead measured slower.)  Used for long row streams only:
+// 28672 x 8192 Q4_K (19 rows per wave) 27.4 -> 26.2 us, while 4096 x 14336
+// (5 rows per wave) was 3% slower than mv_b1s.
+template <int F>
+struct LdsSlot {
+  static constexpr int unit_bytes = Geom<F>::bb * FastUnit<F>::E / Geom<F>::bs;
+  static constexpr int NC = (64 * unit_bytes + 1023) / 1024;  // 1 KB copies per row slice
+  static constexpr int SLOT = 1024 * NC;
+};
+
+template <int F, int D, bool FULL, int SIT>
 __global__ __launch_bounds__(768) void mv_b1s_lds(const uint8_t* __restrict__ w, const float* __restrict__ x,
                                                   float* __restrict__ y, int out_dim, int row_bpr, int slice_bpr,
                                                   int rows_cap) {
-  constexpr int F = kQ4_K;
-  constexpr int US = Dig<F>::US, SLOT = 3072, NC = 3;
+  constexpr int US = Dig<F>::US, SLOT = LdsSlot<F>::SLOT, NC = LdsSlot<F>::NC;
   extern __shared__ uint4 lds4[];
   uint32_t* lds = reinterpret_cast<uint32_t*>(lds4);
   const int blk0 = blockIdx.y * slice_bpr;
@@ -1045,7 +1053,7 @@ __global__ __launch_bounds__(768) void mv_b1s_lds(const uint8_t* __restrict__ w,
   y += (size_t)blockIdx.y * out_dim;
   const int keff = bpr * Geom<F>::bs;
   const int U = keff / FastUnit<F>::E;
-  const int nbytes = bpr * Geom<F>::bb;  // <= 2304
+  const int nbytes = bpr * Geom<F>::bb;  // <= SLOT
   const int lane = threadIdx.x & 63, nwaves = blockDim.x >> 6;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // scalar: the LDS slots' M0 base
   const size_t row_bytes = (size_t)row_bpr * Geom<F>::bb;
@@ -1059,11 +1067,10 @@ __global__ __launch_bounds__(768) void mv_b1s_lds(const uint8_t* __restrict__ w,
   wl += (size_t)wave * D * SLOT;
   const uint32_t wl_off = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)wl;
 
-  // Copy k of a row slice: lanes whose 16 bytes lie in the slice (a whole
-  // slice of 2304 bytes fills copies 0 and 1 and lanes 0-15 of copy 2), and
-  // lane 0 always (a dummy copy of the row's first bytes into the unused part
-  // of the slot when the slice ends before 1024 k), so that every row issues
-  // NC copies.
+  // Copy k of a row slice: lanes whose 16 bytes lie in the slice, and lane 0
+  // always (a dummy copy of the row's first bytes into the unused part of the
+  // slot when the slice ends before 1024 k), so that every row issues NC
+  // copies.
   auto copy_row = [&](int rr, int sl) {
     const uint8_t* rp = w + (size_t)min(r_begin + rr, r_last) * row_bytes;
 #pragma unroll
@@ -1086,7 +1093,6 @@ __global__ __launch_bounds__(768) void mv_b1s_lds(const uint8_t* __restrict__ w,
     pr[t] = v.x; pr[t + 1] = v.y; pr[t + 2] = v.z; pr[t + 3] = v.w;
   }
   const bool live = FULL || lane < U;
-  const int boff = 144 * (u >> 2), qoff = boff + 16 + 32 * (u & 3);
   for (int r0 = 0; r0 < n_rows; r0 += D) {
 #pragma unroll
     for (int i = 0; i < D; i++) {
@@ -1094,14 +1100,8 @@ __global__ __launch_bounds__(768) void mv_b1s_lds(const uint8_t* __restrict__ w,
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_waitcnt(((NC * (D - 1)) & 15) | (((NC * (D - 1)) >> 4) << 14) | (7 << 4) | (15 << 8));
       __builtin_amdgcn_sched_barrier(0);
-      const uint8_t* sl = wl + i * SLOT;
-      uint32_t raw[12];
-      const uint4 h = *reinterpret_cast<const uint4*>(sl + boff);
-      const uint4 q0 = *reinterpret_cast<const uint4*>(sl + qoff);
-      const uint4 q1 = *reinterpret_cast<const uint4*>(sl + qoff + 16);
-      raw[0] = h.x; raw[1] = h.y; raw[2] = h.z; raw[3] = h.w;
-      raw[4] = q0.x; raw[5] = q0.y; raw[6] = q0.z; raw[7] = q0.w;
-      raw[8] = q1.x; raw[9] = q1.y; raw[10] = q1.z; raw[11] = q1.w;
+      uint32_t raw[FastUnit<F>::NW];
+      load_unit<F>(wl + i * SLOT, u, raw);
       float a = 0.f;
       accumulate_dig<F>(raw, u, [&](int t) { return pr[t]; }, a);
       // The slot's LDS reads complete before its next copy is requested: the
@@ -1600,6 +1600,10 @@ B1Plan<F> b1_plan(int bpr, int out_dim) {
   return p;
 }
 
+// Types whose long row streams take mv_b1s_lds.
+template <int F>
+constexpr bool kLdsRowStreams = F == kQ4_K || F == kQ6_K || F == kQ4_0 || F == kQ8_0;
+
 // mv_b1s launch: one workgroup of 12 waves per CU and K slice (at least one
 // row per wave), two rows in flight per wave.
 template <int F, bool FULL>
@@ -1617,12 +1621,15 @@ hipError_t run_b1s(const uint8_t* w, const float* x, float* y, int out_dim, int 
                        slice_bpr);
     return hipGetLastError();
   };
-  if constexpr (F == kQ4_K) {
-    // weights through LDS (mv_b1s_lds): two 3 KB slots per wave and the row sums
+  if constexpr (kLdsRowStreams<F>) {
+    // weights through LDS (mv_b1s_lds): two slots per wave and the row sums;
+    // slices that start 16-byte aligned in memory
     const long n_streams = n_wg * 12;
     const int rows_cap = (int)((out_dim + n_streams - 1) / n_streams) + 1;
-    const size_t lds2 = lds + (size_t)12 * 2 * 3072 + (size_t)12 * rows_cap * sizeof(float);
-    if (lds2 <= (size_t)lds_limit() && sit <= 2 && rows_cap > 12) {
+    const size_t lds2 = lds + (size_t)12 * 2 * LdsSlot<F>::SLOT + (size_t)12 * rows_cap * sizeof(float);
+    const bool aligned16 = ((uintptr_t)w % 16) == 0 && ((size_t)row_bpr * Geom<F>::bb) % 16 == 0 &&
+                           ((size_t)slice_bpr * Geom<F>::bb) % 16 == 0;
+    if (aligned16 && lds2 <= (size_t)lds_limit() && sit <= 2 && rows_cap > 12) {
       auto go2 = [&](auto kern) {
         hipError_t e = set_lds_attr(kern, lds2);
         if (e != hipSuccess) return e;
@@ -1630,7 +1637,7 @@ hipError_t run_b1s(const uint8_t* w, const float* x, float* y, int out_dim, int 
                            row_bpr, slice_bpr, rows_cap);
         return hipGetLastError();
       };
-      return sit <= 1 ? go2(mv_b1s_lds<2, FULL, 1>) : go2(mv_b1s_lds<2, FULL, 2>);
+      return sit <= 1 ? go2(mv_b1s_lds<F, 2, FULL, 1>) : go2(mv_b1s_lds<F, 2, FULL, 2>);
     }
   }
   switch (sit) {

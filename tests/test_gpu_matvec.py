@@ -259,6 +259,7 @@ LONG_ROWS = [  # batch-1 rows of 129-256 units (K slices summed in slice order)
     # whole rows beyond one round of workgroups: per-wave row streams, one slice
     (Q4_0, 40000, 2048), (Q4_K, 50000, 4096), (Q6_K, 60000, 2048), (Q8_0, 33333, 1024),
     (Q4_K, 40000, 2048),  # rows of 32 units through the LDS row copies: partial copies, dummy third copy
+    (Q8_0, 50000, 2048),  # Q8_0 rows of 32 units through the LDS row copies (five 1 KB copies per row)
 ]
 
 
@@ -284,6 +285,7 @@ K_SLICED = [  # K-sliced rows: slice partials in the workspace, summed in slice 
     (Q8_0, 4096, 28672),   # batch-1 kernel, 7 slices, interleaved row streams
     (Q4_0, 2000, 28800),   # 8 slices, partial last slice
     (Q6_K, 33, 14336),     # fewer rows than row streams
+    (Q6_K, 128256, 4096),  # output-head shape: long row streams through LDS, 2 slices
 ]
 
 

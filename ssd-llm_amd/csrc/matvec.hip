@@ -1032,18 +1032,20 @@ __device__ __forceinline__ void dma16_nt(const void* g, uint32_t lds) {
 // same LDS copies instead measured slower.)  Used for long row streams only:
 // 28672 x 8192 Q4_K (19 rows per wave) 27.4 -> 26.2 us, while 4096 x 14336
 // (5 rows per wave) was 3% slower than mv_b1s.
-template <int F>
+template <int F, int UPL = 1>
 struct LdsSlot {
   static constexpr int unit_bytes = Geom<F>::bb * FastUnit<F>::E / Geom<F>::bs;
-  static constexpr int NC = (64 * unit_bytes + 1023) / 1024;  // 1 KB copies per row slice
+  static constexpr int NC = (UPL * 64 * unit_bytes + 1023) / 1024;  // 1 KB copies per row slice
   static constexpr int SLOT = 1024 * NC;
 };
 
-template <int F, int D, bool FULL, int SIT>
+// UPL units per lane: rows of up to 64 UPL units run whole (UPL = 2: rows of
+// 65-128 units without K slices, whose partials would need a second launch).
+template <int F, int UPL, int D, bool FULL, int SIT>
 __global__ __launch_bounds__(768) void mv_b1s_lds(const uint8_t* __restrict__ w, const float* __restrict__ x,
                                                   float* __restrict__ y, int out_dim, int row_bpr, int slice_bpr,
                                                   int rows_cap) {
-  constexpr int US = Dig<F>::US, SLOT = LdsSlot<F>::SLOT, NC = LdsSlot<F>::NC;
+  constexpr int US = Dig<F>::US, SLOT = LdsSlot<F, UPL>::SLOT, NC = LdsSlot<F, UPL>::NC;
   extern __shared__ uint4 lds4[];
   uint32_t* lds = reinterpret_cast<uint32_t*>(lds4);
   const int blk0 = blockIdx.y * slice_bpr;
@@ -1061,7 +1063,9 @@ __global__ __launch_bounds__(768) void mv_b1s_lds(const uint8_t* __restrict__ w,
   const int r_begin = (int)(gs * out_dim / n_streams);
   const int n_rows = (int)((gs + 1) * out_dim / n_streams) - r_begin;
   const int r_last = r_begin + max(n_rows, 1) - 1;
-  const int u = FULL ? lane : min(lane, U - 1);
+  int u[UPL];
+#pragma unroll
+  for (int i = 0; i < UPL; i++) u[i] = FULL ? lane + 64 * i : min(lane + 64 * i, U - 1);
   uint8_t* wl = reinterpret_cast<uint8_t*>(lds4) + (size_t)U * US * sizeof(uint32_t);
   float* red = reinterpret_cast<float*>(wl + (size_t)nwaves * D * SLOT) + (size_t)wave * rows_cap;
   wl += (size_t)wave * D * SLOT;
@@ -1086,13 +1090,14 @@ __global__ __launch_bounds__(768) void mv_b1s_lds(const uint8_t* __restrict__ w,
   for (int i = 0; i < D; i++) copy_row(i, i);
   stage_store<F, SIT>(st, keff, lds, blockDim.x);
   lds_barrier();
-  uint32_t pr[US];
+  uint32_t pr[UPL][US];
 #pragma unroll
-  for (int t = 0; t < US; t += 4) {
-    const uint4 v = lds4[(size_t)u * (US / 4) + t / 4];
-    pr[t] = v.x; pr[t + 1] = v.y; pr[t + 2] = v.z; pr[t + 3] = v.w;
-  }
-  const bool live = FULL || lane < U;
+  for (int j = 0; j < UPL; j++)
+#pragma unroll
+    for (int t = 0; t < US; t += 4) {
+      const uint4 v = lds4[(size_t)u[j] * (US / 4) + t / 4];
+      pr[j][t] = v.x; pr[j][t + 1] = v.y; pr[j][t + 2] = v.z; pr[j][t + 3] = v.w;
+    }
   for (int r0 = 0; r0 < n_rows; r0 += D) {
 #pragma unroll
     for (int i = 0; i < D; i++) {
@@ -1100,10 +1105,15 @@ __global__ __launch_bounds__(768) void mv_b1s_lds(const uint8_t* __restrict__ w,
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_waitcnt(((NC * (D - 1)) & 15) | (((NC * (D - 1)) >> 4) << 14) | (7 << 4) | (15 << 8));
       __builtin_amdgcn_sched_barrier(0);
-      uint32_t raw[FastUnit<F>::NW];
-      load_unit<F>(wl + i * SLOT, u, raw);
       float a = 0.f;
-      accumulate_dig<F>(raw, u, [&](int t) { return pr[t]; }, a);
+#pragma unroll
+      for (int j = 0; j < UPL; j++) {
+        uint32_t raw[FastUnit<F>::NW];
+        load_unit<F>(wl + i * SLOT, u[j], raw);
+        float aj = 0.f;
+        accumulate_dig<F>(raw, u[j], [&](int t) { return pr[j][t]; }, aj);
+        a += (FULL || lane + 64 * j < U) ? aj : 0.f;
+      }
       // The slot's LDS reads complete before its next copy is requested: the
       // compiler may issue the copy (inline assembly) right after the read
       // instructions, and a copy served from the cache can land before reads
@@ -1112,7 +1122,7 @@ __global__ __launch_bounds__(768) void mv_b1s_lds(const uint8_t* __restrict__ w,
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
       __builtin_amdgcn_sched_barrier(0);
       copy_row(r0 + i + D, i);
-      a = wave_sum_l63(live ? a : 0.f);
+      a = wave_sum_l63(a);
       if (lane == 63 && r0 + i < n_rows) red[r0 + i] = a;
     }
   }
@@ -1626,7 +1636,7 @@ hipError_t run_b1s(const uint8_t* w, const float* x, float* y, int out_dim, int 
     // slices that start 16-byte aligned in memory
     const long n_streams = n_wg * 12;
     const int rows_cap = (int)((out_dim + n_streams - 1) / n_streams) + 1;
-    const size_t lds2 = lds + (size_t)12 * 2 * LdsSlot<F>::SLOT + (size_t)12 * rows_cap * sizeof(float);
+    const size_t lds2 = lds + (size_t)12 * 2 * LdsSlot<F, 1>::SLOT + (size_t)12 * rows_cap * sizeof(float);
     const bool aligned16 = ((uintptr_t)w % 16) == 0 && ((size_t)row_bpr * Geom<F>::bb) % 16 == 0 &&
                            ((size_t)slice_bpr * Geom<F>::bb) % 16 == 0;
     if (aligned16 && lds2 <= (size_t)lds_limit() && sit <= 2 && rows_cap > 12) {
@@ -1637,7 +1647,7 @@ hipError_t run_b1s(const uint8_t* w, const float* x, float* y, int out_dim, int 
                            row_bpr, slice_bpr, rows_cap);
         return hipGetLastError();
       };
-      return sit <= 1 ? go2(mv_b1s_lds<F, 2, FULL, 1>) : go2(mv_b1s_lds<F, 2, FULL, 2>);
+      return sit <= 1 ? go2(mv_b1s_lds<F, 1, 2, FULL, 1>) : go2(mv_b1s_lds<F, 1, 2, FULL, 2>);
     }
   }
   switch (sit) {
@@ -1647,6 +1657,39 @@ hipError_t run_b1s(const uint8_t* w, const float* x, float* y, int out_dim, int 
     case 3:
     case 4: return go(mv_b1s<F, 2, FULL, 4>);
     default: return hipErrorNotSupported;
+  }
+}
+
+// Rows of 65-128 units as whole-row LDS streams (mv_b1s_lds, two units per
+// lane, one workgroup per CU): no K slices, so no partials and no second
+// launch.  hipErrorNotSupported when the shape does not qualify (short
+// streams, unaligned rows, LDS).
+template <int F>
+hipError_t run_b1s_lds_rows(const uint8_t* w, const float* x, float* y, int out_dim, int bpr, hipStream_t s) {
+  if constexpr (!kLdsRowStreams<F>) {
+    return hipErrorNotSupported;
+  } else {
+    const int U = bpr * Geom<F>::bs / FastUnit<F>::E;
+    if (U <= 64 || U > 128) return hipErrorNotSupported;
+    if (((uintptr_t)w % 16) != 0 || ((size_t)bpr * Geom<F>::bb) % 16 != 0) return hipErrorNotSupported;
+    const int sit = (bpr * Geom<F>::bs / 8 + 767) / 768;
+    if (sit > 2) return hipErrorNotSupported;
+    const long n_wg = std::max<long>(1, std::min<long>(device_cu_count(), (out_dim + 11) / 12));
+    const long n_streams = n_wg * 12;
+    const int rows_cap = (int)((out_dim + n_streams - 1) / n_streams) + 1;
+    if (rows_cap <= 12) return hipErrorNotSupported;
+    const size_t lds = (size_t)U * Dig<F>::US * sizeof(uint32_t) + (size_t)12 * 2 * LdsSlot<F, 2>::SLOT +
+                       (size_t)12 * rows_cap * sizeof(float);
+    if (lds > (size_t)lds_limit()) return hipErrorNotSupported;
+    auto go = [&](auto kern) {
+      hipError_t e = set_lds_attr(kern, lds);
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL(kern, dim3((unsigned)n_wg), dim3(768), lds, s, w, x, y, out_dim, bpr, bpr, rows_cap);
+      return hipGetLastError();
+    };
+    const bool full = U == 128;
+    if (sit <= 1) return full ? go(mv_b1s_lds<F, 2, 2, true, 1>) : go(mv_b1s_lds<F, 2, 2, false, 1>);
+    return full ? go(mv_b1s_lds<F, 2, 2, true, 2>) : go(mv_b1s_lds<F, 2, 2, false, 2>);
   }
 }
 
@@ -1665,6 +1708,14 @@ hipError_t b1_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, 
   if (acc && !acc_in) acc_in = acc;
   const int U = bpr * Geom<F>::bs / FastUnit<F>::E;
   if (U == 0) return hipSuccess;
+  {
+    hipError_t e = run_b1s_lds_rows<F>(w, x, y, out_dim, bpr, s);
+    if (e != hipErrorNotSupported) {
+      *used = e == hipSuccess;
+      if (e != hipSuccess) return e;
+      return acc ? launch_add(acc, acc_in, y, out_dim, s) : hipSuccess;
+    }
+  }
   const B1Plan<F> p = b1_plan<F>(bpr, out_dim);
   if (p.slices > 1 && (!ws || ws_floats < (size_t)p.slices * out_dim)) return hipSuccess;
   float* dst = p.slices > 1 ? ws : y;

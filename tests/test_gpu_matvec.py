@@ -260,6 +260,7 @@ LONG_ROWS = [  # batch-1 rows of 129-256 units (K slices summed in slice order)
     (Q4_0, 40000, 2048), (Q4_K, 50000, 4096), (Q6_K, 60000, 2048), (Q8_0, 33333, 1024),
     (Q4_K, 40000, 2048),  # rows of 32 units through the LDS row copies: partial copies, dummy third copy
     (Q8_0, 50000, 2048),  # Q8_0 rows of 32 units through the LDS row copies (five 1 KB copies per row)
+    (Q4_K, 50000, 6144),  # whole rows of 96 units, two units per lane through LDS (partial second unit)
 ]
 
 

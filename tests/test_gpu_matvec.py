@@ -287,6 +287,7 @@ K_SLICED = [  # K-sliced rows: slice partials in the workspace, summed in slice 
     (Q4_0, 2000, 28800),   # 8 slices, partial last slice
     (Q6_K, 33, 14336),     # fewer rows than row streams
     (Q6_K, 128256, 4096),  # output-head shape: long row streams through LDS, 2 slices
+    (Q4_K, 40000, 8704),   # LDS row streams, 3 slices of 12, 12 and 10 blocks (short last slice)
 ]
 
 

@@ -67,27 +67,56 @@ class Timer:
     to GRAPH_CHUNK captured launches, so the host's per-launch cost (ctypes
     marshalling, ~15 us) does not set the step time.  A timed block is exactly
     `steps` launches (whole replays of the chunk graph, then one replay of a
-    graph of the remainder).  Warm-up runs at least `warmup` launches and at
-    least MIN_WARM_S seconds (the first millisecond after a pause runs up to 5%
-    slow), in whole replays.  After the first timed block, further blocks are
-    timed until STAB_S seconds or STAB_BLOCKS blocks have passed: their median
-    is reported beside the first block."""
+    graph of the remainder), bracketed by device synchronizations.  Each block
+    starts behind a short GPU spin (LEAD_S) enqueued before its start event:
+    the host enqueues the block's launches while the spin runs, so the events
+    time the device executing exactly those launches and not the host
+    submitting the first of them.
+
+    Warm-up runs at least `warmup` launches and at least MIN_WARM_S seconds,
+    in whole replays, then further untimed blocks until two consecutive blocks
+    agree within SETTLE_TOL (at most SETTLE_MAX_S seconds: the first
+    milliseconds after a pause run up to 5% slow).  Then at least MIN_BLOCKS
+    and up to MAX_BLOCKS blocks are timed (STAB_S seconds); the reported time
+    is their median, and the first of them is kept beside it."""
 
     GRAPH_CHUNK = 50
     MIN_WARM_S = 0.05
+    SETTLE_TOL = 0.01
+    SETTLE_MAX_S = 1.0
     STAB_S = 0.02
-    STAB_BLOCKS = 10
+    MIN_BLOCKS = 5
+    MAX_BLOCKS = 11
+    LEAD_S = 100e-6
 
     def __init__(self, torch, graph=True):
         self.torch = torch
         self.graph = graph
         self.e0 = torch.cuda.Event(enable_timing=True)
         self.e1 = torch.cuda.Event(enable_timing=True)
+        self._lead_cycles = None
+
+    def _lead(self):
+        """torch.cuda._sleep cycles that spin for about LEAD_S (measured once)."""
+        torch = self.torch
+        if self._lead_cycles is None:
+            n = 100000
+            torch.cuda._sleep(n)  # first launch outside the measurement
+            torch.cuda.synchronize()
+            self.e0.record()
+            torch.cuda._sleep(n)
+            self.e1.record()
+            torch.cuda.synchronize()
+            per = max(self.e0.elapsed_time(self.e1) * 1e-3, 1e-6) / n
+            self._lead_cycles = int(min(max(self.LEAD_S / per, 1000), 5e7))
+        return self._lead_cycles
 
     def _block(self, body):
         torch = self.torch
+        cycles = self._lead()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
+        torch.cuda._sleep(cycles)
         self.e0.record()
         body()
         self.e1.record()
@@ -95,10 +124,11 @@ class Timer:
         return self.e0.elapsed_time(self.e1) * 1e-3, time.perf_counter() - t0
 
     def run(self, fn, steps, warmup, graph=None, stability=True):
-        """Times `steps` launches of fn(i).  Returns a dict: t (event seconds of
-        the first timed block), wall (its host seconds), steps, chunk (launches
-        per graph replay, 0 when eager), warm_launches, blocks (further blocks
-        timed) and t_median (their median event seconds)."""
+        """Times `steps` launches of fn(i).  Returns a dict: t (the median event
+        seconds of the timed blocks), t_median (the same), t_first (the first
+        timed block), wall (its host seconds), steps, chunk (launches per graph
+        replay, 0 when eager), warm_launches, settle_blocks (untimed blocks
+        until two agreed) and blocks (timed blocks)."""
         torch = self.torch
         use_graph = self.graph if graph is None else graph
         if not use_graph:
@@ -144,16 +174,27 @@ class Timer:
                 if warm % (20 * chunk) == 0:
                     torch.cuda.synchronize()
             torch.cuda.synchronize()
-        t, wall = self._block(body)
-        extra = []
+        settle = 0
+        if stability:
+            prev, t1 = self._block(body)[0], time.perf_counter()
+            settle = 1
+            while time.perf_counter() - t1 < self.SETTLE_MAX_S:
+                cur = self._block(body)[0]
+                settle += 1
+                if abs(cur - prev) <= self.SETTLE_TOL * min(cur, prev):
+                    break
+                prev = cur
+        t_first, wall = self._block(body)
+        times = [t_first]
         if stability:
             t1 = time.perf_counter()
-            while len(extra) < self.STAB_BLOCKS and (time.perf_counter() - t1 < self.STAB_S or len(extra) < 3):
-                extra.append(self._block(body)[0])
+            while len(times) < self.MAX_BLOCKS and (time.perf_counter() - t1 < self.STAB_S
+                                                    or len(times) < self.MIN_BLOCKS):
+                times.append(self._block(body)[0])
         del graphs
-        med = sorted(extra)[len(extra) // 2] if extra else t
-        return {"t": t, "wall": wall, "steps": steps, "chunk": chunk, "warm_launches": warm,
-                "blocks": len(extra), "t_median": med}
+        med = sorted(times)[len(times) // 2]
+        return {"t": med, "t_median": med, "t_first": t_first, "wall": wall, "steps": steps, "chunk": chunk,
+                "warm_launches": warm, "settle_blocks": settle, "blocks": len(times)}
 
 
 def matvec_case(torch, ssdq, synth, dtype, out_dim, in_dim, batch, seed_cfg):
@@ -230,8 +271,10 @@ def main():
                    "launch": "eager" if args.eager else
                    f"hip graph replays of {tm['chunk']} launches (remainder in a second graph)",
                    "warmup_launches_run": tm["warm_launches"],
-                   "stability": {"further_blocks_of_steps": tm["blocks"],
-                                 "median_GB/s": round(algo_bytes * steps / tm["t_median"] / 1e9, 1)}},
+                   "timing": {"value_from": "median of the timed blocks of exactly `steps` launches",
+                              "settle_blocks": tm["settle_blocks"], "timed_blocks": tm["blocks"],
+                              "first_block_GB/s": round(algo_bytes * steps / tm["t_first"] / 1e9, 1),
+                              "median_GB/s": round(algo_bytes * steps / tm["t_median"] / 1e9, 1)}},
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "roofline": {
             "bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

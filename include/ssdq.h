@@ -94,18 +94,20 @@ int ssdq_ctx_device(const ssdq_ctx* ctx);
 /* ------------------------------------------------------------- workspace */
 /* The "dev" functions that need scratch memory (K-sliced matvec partials,
  * split-K GEMM partials and its prepared X, attention split partials) take it
- * from a grow-only buffer the library keeps per (device, stream). Growing it
- * never frees the old buffer: work already queued, and any HIP graph captured
- * earlier on that stream, keeps using the old address. Growth is refused while
- * the stream is being captured (SSDQ_ERR_HIP): run the call once on the stream
- * before capture, or reserve. No reference counterpart (the reference
- * allocates Metal buffers per call, gpu.rs:492-535). */
+ * from a grow-only buffer the library keeps per (device, stream). Growth is
+ * geometric (at least double, in 2 MiB steps). A replaced buffer that was
+ * handed out while its stream was being captured into a HIP graph is retired,
+ * not freed, so the graph keeps a valid address; any other replaced buffer is
+ * freed once the stream has drained the work queued with it (one stream
+ * synchronize per growth). Growth is refused while the stream is being
+ * captured (SSDQ_ERR_HIP): run the call once on the stream before capture, or
+ * reserve. No reference counterpart (the reference allocates Metal buffers per
+ * call, gpu.rs:492-535). */
 /* Grows the stream's scratch buffer of the current device to at least
  * `bytes` now, so later calls up to that need do not allocate. */
 int ssdq_reserve_workspace(size_t bytes, ssdq_stream_t stream);
-/* Frees the buffers that growth replaced (after a device synchronize). A
- * graph captured while one of them was current must not be replayed after
- * this call. */
+/* Frees the retired buffers (after a device synchronize). A graph captured
+ * while one of them was current must not be replayed after this call. */
 int ssdq_release_workspaces(void);
 
 /* --------------------------------------------------- dequant (bit-exact) */

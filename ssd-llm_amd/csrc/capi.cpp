@@ -58,6 +58,7 @@ bool fits_int(size_t v) { return v <= (size_t)INT_MAX; }
 struct Workspace {
   void* ptr = nullptr;
   size_t bytes = 0;
+  bool captured = false;  // handed out while its stream was being captured into a graph
 };
 // slot 0: the kernels' own scratch; slot 1: intermediates of the unfused
 // decode-layer paths, which call kernels that use slot 0; slot 2: the
@@ -65,33 +66,58 @@ struct Workspace {
 // slots 0 and 1.
 std::mutex g_ws_mu;
 std::map<std::tuple<int, void*, int>, Workspace> g_ws;
-// Buffers replaced by a larger one.  A HIP graph captured earlier on that
-// stream still holds their addresses, so they are never freed on growth: only
-// ssdq_release_workspaces() frees them (device, pointer).
+// Buffers replaced by a larger one that a HIP graph captured on their stream
+// may still hold: never freed on growth, only by ssdq_release_workspaces()
+// (device, pointer).
 std::vector<std::pair<int, void*>> g_ws_retired;
 
+// Growth is geometric (at least twice the old size, in 2 MiB steps), so a
+// caller whose request creeps up (the decode attention's split count as the
+// context grows) replaces its buffer O(log n) times.  A replaced buffer that
+// was never handed out during a graph capture is freed after the stream
+// drains the work already queued with it; one that was is retired.
 hipError_t workspace_get(size_t bytes, hipStream_t stream, void** out, int slot = 0) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   std::lock_guard<std::mutex> lk(g_ws_mu);
   Workspace& w = g_ws[std::make_tuple(dev, (void*)stream, slot)];
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  const bool capturing =
+      stream && hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
   if (w.bytes < bytes) {
     // No allocation while the stream is being captured into a graph (it would
     // invalidate the capture): run the call once on this stream beforehand,
     // or reserve with ssdq_reserve_workspace().
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (stream && hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
-      return hipErrorStreamCaptureUnsupported;
+    if (capturing) return hipErrorStreamCaptureUnsupported;
+    constexpr size_t kStep = (size_t)2 << 20;
+    size_t want = bytes > 2 * w.bytes ? bytes : 2 * w.bytes;
+    want = (want + kStep - 1) / kStep * kStep;
     void* p = nullptr;
-    e = hipMalloc(&p, bytes);
-    if (e != hipSuccess) return e;
-    // work already queued on the stream keeps using the old buffer, and so
-    // does any graph captured with it: retire it, do not free it
-    if (w.ptr) g_ws_retired.emplace_back(dev, w.ptr);
+    e = hipMalloc(&p, want);
+    if (e != hipSuccess) {
+      want = bytes;  // the geometric size does not fit: the exact one may
+      e = hipMalloc(&p, want);
+      if (e != hipSuccess) return e;
+    }
+    if (w.ptr) {
+      if (w.captured) {
+        g_ws_retired.emplace_back(dev, w.ptr);
+      } else {
+        // work already queued on the stream may still use the old buffer
+        e = hipStreamSynchronize(stream);
+        if (e == hipSuccess) e = hipFree(w.ptr);
+        if (e != hipSuccess) {
+          (void)hipFree(p);
+          return e;
+        }
+      }
+    }
     w.ptr = p;
-    w.bytes = bytes;
+    w.bytes = want;
+    w.captured = false;
   }
+  if (capturing) w.captured = true;
   *out = w.ptr;
   return hipSuccess;
 }

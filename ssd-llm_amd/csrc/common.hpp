@@ -33,6 +33,20 @@ __device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) {
   return (uint32_t)p[0] | ((uint32_t)p[1] << 8);
 }
 
+// s_waitcnt vmcnt(N) as inline assembly with a memory clobber.  The builtin
+// s_waitcnt is a no-memory intrinsic at IR level, so LDS reads placed after it
+// may be moved above it; after loads the compiler does not track (LDS DMA
+// issued from inline assembly) the wait must also order those reads.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// s_waitcnt lgkmcnt(0) with a memory clobber (every LDS read issued so far has
+// returned its data).
+__device__ __forceinline__ void wait_lgkmcnt0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
 // Byte k (0..3) of a dword.
 __device__ __forceinline__ uint32_t byte_of(uint32_t v, int k) { return (v >> (8 * k)) & 0xFFu; }
 

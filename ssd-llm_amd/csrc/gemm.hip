@@ -221,11 +221,12 @@ __device__ __forceinline__ void bytes_to_f16(uint32_t b, uint32_t* r) {
 // [16 l, 16 l + 16) above the wave-uniform LDS offset lds.  Written as inline
 // assembly so that the compiler, which cannot tell which LDS buffer such a load
 // fills, does not wait for it before every LDS read; the kernel waits for its
-// own loads (vmcnt(0)) before the barrier that publishes a stage.  M0 is
-// restored.
+// own loads (vmcnt(0)) before the barrier that publishes a stage.  One wait
+// state (s_nop) separates the M0 write from the LDS-DMA load that reads M0.  M0
+// is restored.
 __device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
   uint32_t keep;
-  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %2, off\n\ts_mov_b32 m0, %0"
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %2, off\n\ts_mov_b32 m0, %0"
                : "=&s"(keep)
                : "s"(lds), "v"(g)
                : "memory");

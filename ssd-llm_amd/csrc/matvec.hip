@@ -1008,10 +1008,13 @@ __global__ __launch_bounds__(768) void mv_b1s(const uint8_t* __restrict__ w, con
 // One 16-byte nontemporal load per lane straight into LDS: lane l writes
 // bytes [16 l, 16 l + 16) above the wave-uniform LDS offset lds.  Inline
 // assembly, so the compiler neither counts nor waits for it: the kernel waits
-// for these loads itself.  M0 is restored.
+// for these loads itself.  One wait state (s_nop) separates the M0 write from
+// the LDS-DMA load that reads M0, as the ISA requires and as the compiler's
+// hazard recognizer, which does not look inside inline assembly, would insert.
+// M0 is restored.
 __device__ __forceinline__ void dma16_nt(const void* g, uint32_t lds) {
   uint32_t keep;
-  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %2, off nt\n\ts_mov_b32 m0, %0"
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %2, off nt\n\ts_mov_b32 m0, %0"
                : "=&s"(keep)
                : "s"(lds), "v"(g)
                : "memory");
@@ -1103,7 +1106,7 @@ __global__ __launch_bounds__(768) void mv_b1s_lds(const uint8_t* __restrict__ w,
     for (int i = 0; i < D; i++) {
       // the copies of row r0 + i have landed: NC copies per later row may be pending
       __builtin_amdgcn_sched_barrier(0);
-      __builtin_amdgcn_s_waitcnt(((NC * (D - 1)) & 15) | (((NC * (D - 1)) >> 4) << 14) | (7 << 4) | (15 << 8));
+      wait_vmcnt<NC * (D - 1)>();
       __builtin_amdgcn_sched_barrier(0);
       float a = 0.f;
 #pragma unroll
@@ -1119,7 +1122,7 @@ __global__ __launch_bounds__(768) void mv_b1s_lds(const uint8_t* __restrict__ w,
       // instructions, and a copy served from the cache can land before reads
       // still queued in the LDS pipeline.
       __builtin_amdgcn_sched_barrier(0);
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+      wait_lgkmcnt0();
       __builtin_amdgcn_sched_barrier(0);
       copy_row(r0 + i + D, i);
       a = wave_sum_l63(a);
@@ -1127,8 +1130,115 @@ __global__ __launch_bounds__(768) void mv_b1s_lds(const uint8_t* __restrict__ w,
     }
   }
   // the window's last copies land before the workgroup's LDS is released
-  __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+  wait_vmcnt<0>();
   for (int r = lane; r < n_rows; r += 64) y[r_begin + r] = red[r];
+}
+
+// Batch-1 matvec of whole rows (at most 64 units) with the rows copied into
+// LDS and x staged by waves of its own.  One workgroup per CU of kB1rXW "x
+// waves" and NRW "row waves".  The workgroup owns a contiguous range of rows;
+// row wave v takes rows v, v + NRW, v + 2 NRW, ... of it, so the workgroup's
+// copies in flight cover consecutive rows.  Each row wave keeps D row slots of
+// NCR KB and copies a row into a slot with NCR contiguous 1 KB nontemporal
+// copies (lanes past the row masked off; lane 0 always issues, so every row
+// issues NCR copies); the row after the last is a clamped repeat, loaded and
+// not stored.
+//
+// Schedule (per-wave wall-clock timelines on MI355X, 14336 x 4096 Q4_K):
+//   1. The x waves request x, then every wave meets at a barrier: every x load
+//      is queued in the CU before any weight copy (x lands at ~0.55 us from the
+//      first wave's start instead of ~1 us).
+//   2. The row waves copy their first D rows.  The x waves wait for x, write
+//      the digit planes and meet the row waves at a second (LDS-only) barrier.
+//      x is fetched by waves that issue no copies, so the compiler's wait for
+//      x, which cannot count the copies (inline assembly), drains nothing of
+//      the weight stream; staging x (~0.8 us) hides under the first rows'
+//      memory latency.
+//   3. Each row is computed once its copies have landed (exact wait counts:
+//      the loop issues no other vector memory instruction), and its slot takes
+//      the copies of row r + D as soon as the slot's LDS reads are done.  Row
+//      sums go to LDS and are stored after the loop.
+// Measured (kernel alone, graph replays): 14336 x 4096 Q4_K 8.45 -> 7.99 us
+// (D 1, 12 row waves), 28672 x 4096 14.3 -> 12.5 us and 4096 x 4096 4.81 ->
+// 4.56 us (D 2, 8 row waves); 1024 rows (4 per CU) stay on mv_b1 (3.6 against
+// 3.9 us).  Slots of one whole row each beat a contiguous 1 KB ring of the
+// wave's run (8.2-8.8 us) and requesting every row of the run at the start
+// (10.4 us: the copies stall at issue and the stream slows).
+constexpr int kB1rXW = 4;
+
+template <int F, int NCR, int D, int NRW>
+__global__ __launch_bounds__(64 * (kB1rXW + NRW)) void mv_b1r(const uint8_t* __restrict__ w,
+                                                              const float* __restrict__ x, float* __restrict__ y,
+                                                              int out_dim, int row_bpr, int q, int rem, int rows_cap) {
+  constexpr int US = Dig<F>::US, NW = FastUnit<F>::NW, SLOT = 1024 * NCR, SIT = 2;
+  static_assert(NCR * (D - 1) < 64, "vmcnt range");
+  extern __shared__ uint4 lds4[];
+  uint32_t* lds = reinterpret_cast<uint32_t*>(lds4);
+  const int keff = row_bpr * Geom<F>::bs;  // at most 4096: 512 chunks of 8, two per x-wave thread
+  const int U = keff / FastUnit<F>::E;
+  const int row_bytes = row_bpr * Geom<F>::bb;  // at most SLOT
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  if (wave < kB1rXW) {
+    XChunks<SIT> st;
+    stage_load<SIT>(x, keff, st, 64 * kB1rXW);
+    __builtin_amdgcn_s_barrier();  // 1.
+    stage_store<F, SIT>(st, keff, lds, 64 * kB1rXW);
+    lds_barrier();  // 2.
+    return;
+  }
+  __builtin_amdgcn_s_barrier();  // 1.
+  const int rw = wave - kB1rXW;
+  const int b = (int)blockIdx.x;
+  const int wg_begin = b * q + min(b, rem), wg_rows = q + (b < rem ? 1 : 0);
+  const int nr = wg_rows > rw ? (wg_rows - 1 - rw) / NRW + 1 : 0;  // <= rows_cap
+  uint8_t* wl = reinterpret_cast<uint8_t*>(lds4) + (size_t)U * US * sizeof(uint32_t) + (size_t)rw * D * SLOT;
+  float* red = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(lds4) + (size_t)U * US * sizeof(uint32_t) +
+                                        (size_t)NRW * D * SLOT) +
+               (size_t)rw * rows_cap;
+  const uint32_t wl_off = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)wl;
+  auto copy_row = [&](int k, int sl) {
+    const int row = min(wg_begin + rw + min(k, max(nr, 1) - 1) * NRW, out_dim - 1);
+    const uint8_t* rp = w + (size_t)row * row_bytes;
+#pragma unroll
+    for (int c = 0; c < NCR; c++) {
+      const int o = 1024 * c + 16 * lane;
+      if (o < row_bytes || lane == 0) dma16_nt(rp + (o < row_bytes ? o : 0), wl_off + sl * SLOT + 1024 * c);
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < D; i++) copy_row(i, i);  // 2.
+  lds_barrier();                                // 2.
+  const int u = min(lane, U - 1);
+  uint32_t pr[US];
+#pragma unroll
+  for (int t = 0; t < US; t += 4) {
+    const uint4 v = lds4[(size_t)u * (US / 4) + t / 4];
+    pr[t] = v.x; pr[t + 1] = v.y; pr[t + 2] = v.z; pr[t + 3] = v.w;
+  }
+  for (int r0 = 0; r0 < nr; r0 += D) {  // 3.
+#pragma unroll
+    for (int i = 0; i < D; i++) {
+      __builtin_amdgcn_sched_barrier(0);
+      wait_vmcnt<NCR * (D - 1)>();  // row r0 + i has landed; the D - 1 later rows may be pending
+      __builtin_amdgcn_sched_barrier(0);
+      uint32_t raw[NW];
+      load_unit<F>(wl + i * SLOT, u, raw);
+      // The slot's LDS reads complete before its next copies are requested (a
+      // copy served from the cache can land before reads still queued in the
+      // LDS pipeline).
+      __builtin_amdgcn_sched_barrier(0);
+      wait_lgkmcnt0();
+      __builtin_amdgcn_sched_barrier(0);
+      copy_row(r0 + i + D, i);
+      float a = 0.f;
+      accumulate_dig<F>(raw, u, [&](int t) { return pr[t]; }, a);
+      a = wave_sum_l63(lane < U ? a : 0.f);
+      if (lane == 63 && r0 + i < nr) red[r0 + i] = a;
+    }
+  }
+  wait_vmcnt<0>();  // the last (clamped) copies land before the workgroup's LDS is released
+  for (int r = lane; r < nr; r += 64) y[wg_begin + rw + r * NRW] = red[r];
 }
 
 // With res non-null, y = res + (the slice sum), the residual add of a decoder
@@ -1693,6 +1803,47 @@ hipError_t run_b1s_lds_rows(const uint8_t* w, const float* x, float* y, int out_
   }
 }
 
+// Types whose whole rows of 4096 elements take mv_b1r (LDS row slots).
+template <int F>
+constexpr bool kRowSlots = F == kQ4_K || F == kQ4_0 || F == kQ8_0;
+
+// mv_b1r launch: whole rows of 3584-4096 elements (3 KB slots for Q4_K and
+// Q4_0, 5 KB for Q8_0), 16-byte aligned, from 8 rows per CU up to one round of
+// mv_b1 workgroups (10 rows per wave).  One row in flight per wave with 12 row
+// waves for 24-80 rows per CU, else two with 8 row waves (measured on 256
+// CUs: 4096, 14336 and 28672 rows).  hipErrorNotSupported when the shape does
+// not qualify.
+template <int F>
+hipError_t run_b1r(const uint8_t* w, const float* x, float* y, int out_dim, int bpr, hipStream_t s) {
+  if constexpr (!kRowSlots<F>) {
+    return hipErrorNotSupported;
+  } else {
+    constexpr int NCR = F == kQ8_0 ? 5 : 3;
+    const int keff = bpr * Geom<F>::bs, U = keff / FastUnit<F>::E;
+    const size_t row_bytes = (size_t)bpr * Geom<F>::bb;
+    if (U > 64 || keff > 4096 || row_bytes <= (size_t)1024 * (NCR - 1) || row_bytes > (size_t)1024 * NCR)
+      return hipErrorNotSupported;
+    if (((uintptr_t)w % 16) != 0 || row_bytes % 16 != 0) return hipErrorNotSupported;
+    const int cu = device_cu_count();
+    if ((long)out_dim < 8L * cu || (long)out_dim > 10L * 12 * cu) return hipErrorNotSupported;
+    const bool one = (long)out_dim >= 24L * cu && (long)out_dim <= 80L * cu;
+    const int nrw = one ? 12 : 8, d = one ? 1 : 2;
+    const int n_wg = cu, q = out_dim / n_wg, rem = out_dim % n_wg;
+    const int rows_cap = (q + (rem ? 1 : 0) + nrw - 1) / nrw;
+    const size_t lds = (size_t)U * Dig<F>::US * sizeof(uint32_t) + (size_t)nrw * d * 1024 * NCR +
+                       (size_t)nrw * rows_cap * sizeof(float);
+    if (lds > (size_t)lds_limit()) return hipErrorNotSupported;
+    auto go = [&](auto kern, int threads) {
+      hipError_t e = set_lds_attr(kern, lds);
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL(kern, dim3((unsigned)n_wg), dim3((unsigned)threads), lds, s, w, x, y, out_dim, bpr, q, rem,
+                         rows_cap);
+      return hipGetLastError();
+    };
+    return one ? go(mv_b1r<F, NCR, 1, 12>, 64 * (kB1rXW + 12)) : go(mv_b1r<F, NCR, 2, 8>, 64 * (kB1rXW + 8));
+  }
+}
+
 template <int F>
 size_t b1_workspace_floats(int out_dim, int bpr) {
   const B1Plan<F> p = b1_plan<F>(bpr, out_dim);
@@ -1710,6 +1861,7 @@ hipError_t b1_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, 
   if (U == 0) return hipSuccess;
   {
     hipError_t e = run_b1s_lds_rows<F>(w, x, y, out_dim, bpr, s);
+    if (e == hipErrorNotSupported) e = run_b1r<F>(w, x, y, out_dim, bpr, s);
     if (e != hipErrorNotSupported) {
       *used = e == hipSuccess;
       if (e != hipSuccess) return e;

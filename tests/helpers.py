@@ -5,7 +5,8 @@ import numpy as np
 
 import ssdq_oracle as o
 
-# (test id, what, substituted outputs, outputs) of every assert_close_attributed
+# (test id, what, substituted outputs, outputs, worst substituted |gpu - exact| / tol)
+# of every assert_close_attributed
 # call in this process; tests/conftest.py prints them in the terminal summary.
 SUBSTITUTIONS = []
 
@@ -39,26 +40,32 @@ def assert_close_attributed(gpu, ref32, exact, what="", max_ill_frac=1e-3):
     own rounding error is ~1e-4 rms (~5e-3 at worst at K = 14336), the size of
     ATOL, and no other summation order can reproduce it.  So every element
     must be within tolerance of the reference's fp32 value, except elements
-    whose difference from it comes from the reference's own rounding: those
-    must be within the same tolerance of the exact sum of the reference's
-    (bit-exact) element values, and they must be rare (max_ill_frac of the
-    outputs).
+    where the reference's own chain is off: its fp32 value is more than half a
+    tolerance from the exact sum of the reference's (bit-exact) element
+    values.  Only there may the device value be judged against the exact sum
+    instead, within the same tolerance; such substitutions must be rare
+    (max_ill_frac of the outputs), and the worst |gpu - exact| / tol(exact)
+    among them is recorded for the terminal summary.
     """
     gpu = np.asarray(gpu, np.float64).ravel()
     ref32 = np.asarray(ref32, np.float64).ravel()
     exact = np.asarray(exact, np.float64).ravel()
     assert np.all(np.isfinite(gpu)), f"{what}: non-finite device output"
     ok_ref = np.abs(gpu - ref32) <= tol(ref32)
+    ref_off = np.abs(ref32 - exact) > 0.5 * tol(exact)
     ok_exact = np.abs(gpu - exact) <= tol(exact)
-    good = ok_ref | ok_exact
+    sub = ~ok_ref & ref_off & ok_exact
+    good = ok_ref | sub
     if not good.all():
         i = int(np.flatnonzero(~good)[0])
         raise AssertionError(
-            f"{what}: {int((~good).sum())} of {gpu.size} outside tolerance; first idx {i}: "
+            f"{what}: {int((~good).sum())} of {gpu.size} outside tolerance of the fp32 reference "
+            f"(substitution allowed only where |ref32 - exact| > 0.5 tol); first idx {i}: "
             f"gpu={gpu[i]!r} ref32={ref32[i]!r} exact={exact[i]!r}")
-    n_sub = int((~ok_ref).sum())
+    n_sub = int(sub.sum())
+    worst = float((np.abs(gpu - exact) / tol(exact))[sub].max()) if n_sub else 0.0
     test = os.environ.get("PYTEST_CURRENT_TEST", "?").split(" ")[0]
-    SUBSTITUTIONS.append((test, what, n_sub, int(gpu.size)))
+    SUBSTITUTIONS.append((test, what, n_sub, int(gpu.size), worst))
     assert n_sub <= max(1, max_ill_frac * gpu.size), f"{what}: {n_sub} ill-conditioned substitutions"
     return n_sub
 

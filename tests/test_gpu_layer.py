@@ -67,7 +67,7 @@ def test_qkv_rope(dts, n_embd, head_dim, position, theta):
             assert_propagated(from_dev(got), rope_double(ex, head_dim, position, theta), bound,
                               f"{name} {ssdq.TYPE_NAMES[dt]}")
         else:
-            assert_close_attributed(from_dev(got), ref, ex, f"{name} {ssdq.TYPE_NAMES[dt]}", max_ill_frac=0.01)
+            assert_close_attributed(from_dev(got), ref, ex, f"{name} {ssdq.TYPE_NAMES[dt]}")
 
 
 SWIGLU = [(Q4_K, 4096), (Q6_K, 4096), (Q4_0, 4096), (Q5_K, 4096), (Q4_K, 5120)]

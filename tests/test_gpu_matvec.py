@@ -306,3 +306,32 @@ def test_k_sliced_single_launch_repeats(dtype, out_dim, in_dim):
     rb = w.size // out_dim
     ref, exact = reference(dtype, w.reshape(out_dim, rb)[sel].ravel(), x, sel.size, in_dim)
     assert_close_attributed(ys[0][sel], ref, exact, "k-sliced repeats")
+
+
+ROW_SLOTS = [  # whole rows of 4096 through the LDS row slots (mv_b1r), at and around
+    # the rows-per-CU thresholds of its two forms (256 CUs: 8, 24 and 80 rows per
+    # CU, one round of the batch-1 kernel at 120): ragged workgroup shares,
+    # clamped repeat rows after a wave's last, waves with one row more than others
+    (Q4_K, 2048), (Q4_K, 2049), (Q4_K, 6143), (Q4_K, 6144), (Q4_K, 14335), (Q4_K, 20480),
+    (Q4_K, 20481), (Q4_K, 30720), (Q4_0, 2051), (Q4_0, 11008), (Q4_0, 30719),
+    (Q8_0, 2048), (Q8_0, 11009), (Q8_0, 28672),
+]
+
+
+@pytest.mark.parametrize("dtype,out_dim", ROW_SLOTS)
+def test_batch1_row_slots(dtype, out_dim):
+    in_dim = 4096
+    w = synth.quant_weights(dtype, out_dim, in_dim, 1200 + out_dim)
+    x = synth.normal_f32(in_dim, 1201 + out_dim)
+    announce("matvec row slots", ssdq.TYPE_NAMES[dtype], out_dim, in_dim)
+    wd = to_dev(w)
+    y, rc = run(dtype, None, x, out_dim, in_dim, w_dev=wd)
+    assert rc == 0
+    # the first, middle and last rows, and every 97th row between
+    sel = np.unique(np.r_[0:600, out_dim // 2 - 300:out_dim // 2 + 300, max(0, out_dim - 600):out_dim,
+                          0:out_dim:97])
+    rb = w.size // out_dim
+    ref, exact = reference(dtype, w.reshape(out_dim, rb)[sel].ravel(), x, sel.size, in_dim)
+    assert_close_attributed(y[sel], ref, exact, "row slots")
+    y2, _ = run(dtype, None, x, out_dim, in_dim, w_dev=wd)
+    assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))  # fixed summation order

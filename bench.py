@@ -68,10 +68,11 @@ class Timer:
     marshalling, ~15 us) does not set the step time.  A timed block is exactly
     `steps` launches (whole replays of the chunk graph, then one replay of a
     graph of the remainder), bracketed by device synchronizations.  Each block
-    starts behind a short GPU spin (LEAD_S) enqueued before its start event:
-    the host enqueues the block's launches while the spin runs, so the events
-    time the device executing exactly those launches and not the host
-    submitting the first of them.
+    is enqueued twice in a row, its start event between the two: the first,
+    untimed copy keeps the device busy (and at its working clock) while the
+    host enqueues the timed one, so the events time the device executing
+    exactly the block's launches, not the host submitting them or the device
+    leaving idle.
 
     Warm-up runs at least `warmup` launches and at least MIN_WARM_S seconds,
     in whole replays, then further untimed blocks until two consecutive blocks
@@ -87,36 +88,18 @@ class Timer:
     STAB_S = 0.02
     MIN_BLOCKS = 5
     MAX_BLOCKS = 11
-    LEAD_S = 100e-6
 
     def __init__(self, torch, graph=True):
         self.torch = torch
         self.graph = graph
         self.e0 = torch.cuda.Event(enable_timing=True)
         self.e1 = torch.cuda.Event(enable_timing=True)
-        self._lead_cycles = None
-
-    def _lead(self):
-        """torch.cuda._sleep cycles that spin for about LEAD_S (measured once)."""
-        torch = self.torch
-        if self._lead_cycles is None:
-            n = 100000
-            torch.cuda._sleep(n)  # first launch outside the measurement
-            torch.cuda.synchronize()
-            self.e0.record()
-            torch.cuda._sleep(n)
-            self.e1.record()
-            torch.cuda.synchronize()
-            per = max(self.e0.elapsed_time(self.e1) * 1e-3, 1e-6) / n
-            self._lead_cycles = int(min(max(self.LEAD_S / per, 1000), 5e7))
-        return self._lead_cycles
 
     def _block(self, body):
         torch = self.torch
-        cycles = self._lead()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        torch.cuda._sleep(cycles)
+        body()  # untimed lead copy
         self.e0.record()
         body()
         self.e1.record()

@@ -275,6 +275,21 @@ int ssdq_paged_attention_int8_dev(const float* q, const int8_t* k_codes, const f
                                   float* out, size_t n_seq, size_t n_head, size_t n_head_kv,
                                   size_t head_dim, size_t block_size, size_t max_blocks_per_seq,
                                   size_t max_ctx, ssdq_stream_t stream);
+/* The same paged INT8 decode attention over a position window per sequence:
+ * sequence s attends over [max(window_starts[s], 0), min(window_ends[s],
+ * ctx_lens[s])), the range flash_attention_windowed takes
+ * (src/inference/flash_attention.rs:146-227, effective_end = min(window_end,
+ * seq_len)) and MetalCompute::flash_attention_f32 passes to its kernel
+ * (compute.rs:217-258), here over the paged INT8 cache; an empty window gives
+ * zeros, as the reference's running_sum == 0 case does. Either array may be
+ * NULL (start 0, no end bound). The window length is at most max_ctx. */
+int ssdq_paged_attention_int8_window_dev(const float* q, const int8_t* k_codes, const float* k_scales,
+                                         const int8_t* v_codes, const float* v_scales,
+                                         const int32_t* block_tables, const int32_t* ctx_lens,
+                                         const int32_t* window_starts, const int32_t* window_ends, float* out,
+                                         size_t n_seq, size_t n_head, size_t n_head_kv, size_t head_dim,
+                                         size_t block_size, size_t max_blocks_per_seq, size_t max_ctx,
+                                         ssdq_stream_t stream);
 /* The same paged INT8 decode attention, allocating nothing: no counterpart in
  * the reference. It is for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid

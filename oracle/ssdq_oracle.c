@@ -992,6 +992,8 @@ typedef struct {
     size_t n_head, group, head_dim, max_blocks;
     size_t u0, u1; /* units = seq*n_head + h */
     float* out;
+    const int32_t* win_lo; /* optional per-sequence window (NULL: 0 / no bound) */
+    const int32_t* win_hi;
 } attn_job;
 
 static void* attn_worker(void* p) {
@@ -1002,7 +1004,14 @@ static void* attn_worker(void* p) {
         kv_src src = j->base;
         src.table = j->block_tables + s * j->max_blocks;
         size_t ctx = j->ctx_lens[s] > 0 ? (size_t)j->ctx_lens[s] : 0;
-        attend_head(j->q + u * j->head_dim, &src, h / j->group, j->head_dim, 0, ctx,
+        /* flash_attention_windowed, flash_attention.rs:176 and 187:
+         * positions window_start .. min(window_end, seq_len), empty when the
+         * start is past the end (attend_head then writes zeros) */
+        size_t p0 = 0, p1 = ctx;
+        if (j->win_lo && j->win_lo[s] > 0) p0 = (size_t)j->win_lo[s];
+        if (j->win_hi) p1 = j->win_hi[s] > 0 ? ((size_t)j->win_hi[s] < ctx ? (size_t)j->win_hi[s] : ctx) : 0;
+        if (p0 > p1) p0 = p1;
+        attend_head(j->q + u * j->head_dim, &src, h / j->group, j->head_dim, p0, p1,
                     j->out + u * j->head_dim, scratch, scratch + j->head_dim,
                     scratch + 2 * j->head_dim);
     }
@@ -1010,12 +1019,13 @@ static void* attn_worker(void* p) {
     return NULL;
 }
 
-void ssdo_paged_attention_int8_mt(const float* q, const int8_t* k_codes, const float* k_scales,
-                                  const int8_t* v_codes, const float* v_scales,
-                                  const int32_t* block_tables, const int32_t* ctx_lens,
-                                  size_t n_seq, size_t n_head, size_t n_head_kv, size_t head_dim,
-                                  size_t block_size, size_t max_blocks_per_seq, float* out,
-                                  int nthreads) {
+void ssdo_paged_attention_int8_window_mt(const float* q, const int8_t* k_codes, const float* k_scales,
+                                         const int8_t* v_codes, const float* v_scales,
+                                         const int32_t* block_tables, const int32_t* ctx_lens,
+                                         const int32_t* window_starts, const int32_t* window_ends,
+                                         size_t n_seq, size_t n_head, size_t n_head_kv, size_t head_dim,
+                                         size_t block_size, size_t max_blocks_per_seq, float* out,
+                                         int nthreads) {
     kv_src base;
     memset(&base, 0, sizeof base);
     base.paged = 1;
@@ -1038,7 +1048,7 @@ void ssdo_paged_attention_int8_mt(const float* q, const int8_t* k_codes, const f
         if (u0 > units) u0 = units;
         if (u1 > units) u1 = units;
         jobs[t] = (attn_job){q, base, block_tables, ctx_lens, n_head, group, head_dim,
-                             max_blocks_per_seq, u0, u1, out};
+                             max_blocks_per_seq, u0, u1, out, window_starts, window_ends};
         if (nthreads == 1)
             attn_worker(&jobs[t]);
         else
@@ -1048,6 +1058,17 @@ void ssdo_paged_attention_int8_mt(const float* q, const int8_t* k_codes, const f
         for (int t = 0; t < nthreads; t++) pthread_join(th[t], NULL);
     free(th);
     free(jobs);
+}
+
+void ssdo_paged_attention_int8_mt(const float* q, const int8_t* k_codes, const float* k_scales,
+                                  const int8_t* v_codes, const float* v_scales,
+                                  const int32_t* block_tables, const int32_t* ctx_lens,
+                                  size_t n_seq, size_t n_head, size_t n_head_kv, size_t head_dim,
+                                  size_t block_size, size_t max_blocks_per_seq, float* out,
+                                  int nthreads) {
+    ssdo_paged_attention_int8_window_mt(q, k_codes, k_scales, v_codes, v_scales, block_tables, ctx_lens,
+                                        NULL, NULL, n_seq, n_head, n_head_kv, head_dim, block_size,
+                                        max_blocks_per_seq, out, nthreads);
 }
 
 void ssdo_paged_attention_int8(const float* q, const int8_t* k_codes, const float* k_scales,

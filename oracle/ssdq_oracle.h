@@ -105,6 +105,17 @@ void ssdo_paged_attention_int8(const float* q, const int8_t* k_codes, const floa
                                size_t n_seq, size_t n_head, size_t n_head_kv, size_t head_dim,
                                size_t block_size, size_t max_blocks_per_seq, float* out);
 /* Same over (n_seq*n_head) units sharded on `nthreads` workers. */
+/* The same over a per-sequence window (flash_attention_windowed,
+ * flash_attention.rs:146-227): positions [window_starts[s],
+ * min(window_ends[s], ctx_lens[s])), zeros when empty; either array may be
+ * NULL (start 0, no end bound). */
+void ssdo_paged_attention_int8_window_mt(const float* q, const int8_t* k_codes, const float* k_scales,
+                                         const int8_t* v_codes, const float* v_scales,
+                                         const int32_t* block_tables, const int32_t* ctx_lens,
+                                         const int32_t* window_starts, const int32_t* window_ends,
+                                         size_t n_seq, size_t n_head, size_t n_head_kv, size_t head_dim,
+                                         size_t block_size, size_t max_blocks_per_seq, float* out,
+                                         int nthreads);
 void ssdo_paged_attention_int8_mt(const float* q, const int8_t* k_codes, const float* k_scales,
                                   const int8_t* v_codes, const float* v_scales,
                                   const int32_t* block_tables, const int32_t* ctx_lens,

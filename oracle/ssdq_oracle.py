@@ -47,6 +47,8 @@ def lib():
             "ssdo_flash_attention_f32": (None, [_vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _vp]),
             "ssdo_paged_attention_int8_mt": (
                 None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _vp, _i]),
+            "ssdo_paged_attention_int8_window_mt": (
+                None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _vp, _i]),
             "ssdo_gemm_q4k_bf16": (None, [_vp, _vp, _sz, _sz, _sz, _vp, _i]),
             "ssdo_gemm_q4k_bf16_exact": (None, [_vp, _vp, _sz, _sz, _sz, _vp, _i]),
         }
@@ -149,6 +151,26 @@ def paged_attention_int8(q, k_codes, k_scales, v_codes, v_scales, block_tables, 
                                        vs.ctypes.data, bt.ctypes.data, cl.ctypes.data, n_seq, n_head,
                                        n_head_kv, head_dim, block_size, max_blocks_per_seq,
                                        out.ctypes.data, threads)
+    return out
+
+
+def paged_attention_int8_window(q, k_codes, k_scales, v_codes, v_scales, block_tables, ctx_lens, window_starts,
+                                window_ends, n_seq, n_head, n_head_kv, head_dim, block_size, max_blocks_per_seq,
+                                threads=1):
+    """paged_attention_int8 over [window_starts[s], min(window_ends[s], ctx_lens[s])) per sequence
+    (flash_attention_windowed, src/inference/flash_attention.rs:146-227); either may be None."""
+    q = _c(q, np.float32)
+    kc, vc = _c(k_codes, np.int8), _c(v_codes, np.int8)
+    ks, vs = _c(k_scales, np.float32), _c(v_scales, np.float32)
+    bt, cl = _c(block_tables, np.int32), _c(ctx_lens, np.int32)
+    lo = None if window_starts is None else _c(window_starts, np.int32)
+    hi = None if window_ends is None else _c(window_ends, np.int32)
+    out = np.empty(n_seq * n_head * head_dim, np.float32)
+    lib().ssdo_paged_attention_int8_window_mt(q.ctypes.data, kc.ctypes.data, ks.ctypes.data, vc.ctypes.data,
+                                              vs.ctypes.data, bt.ctypes.data, cl.ctypes.data,
+                                              None if lo is None else lo.ctypes.data,
+                                              None if hi is None else hi.ctypes.data, n_seq, n_head, n_head_kv,
+                                              head_dim, block_size, max_blocks_per_seq, out.ctypes.data, threads)
     return out
 
 

@@ -22,6 +22,8 @@
 #include <mutex>
 #include <type_traits>
 
+#include <climits>
+
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -55,9 +57,9 @@ struct FlatSrc {
 template <int HD, class Src>
 __global__ __launch_bounds__(kThreads) void attn_split_kernel(
     const float* __restrict__ q, Src src, const int32_t* __restrict__ block_tables,
-    const int32_t* __restrict__ ctx_lens, int max_blocks_per_seq, int n_head, int n_head_kv,
-    int pos_begin_flat, int pos_end_flat, int split_len, int n_splits,
-    float* __restrict__ partial) {
+    const int32_t* __restrict__ ctx_lens, const int32_t* __restrict__ win_lo, const int32_t* __restrict__ win_hi,
+    int max_blocks_per_seq, int n_head, int n_head_kv, int pos_begin_flat, int pos_end_flat, int split_len,
+    int n_splits, float* __restrict__ partial) {
   constexpr int QK_PARTS = kThreads / kTile;     // threads per token in the QK phase
   constexpr int QK_DIMS = HD / QK_PARTS;
   constexpr int PV_THREADS_PER_TOK = HD / 2;     // 2 dims per thread
@@ -73,9 +75,11 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
   int p_begin, p_end;
   if constexpr (std::is_same<Src, PagedSrc>::value) {
     src.table = block_tables + (size_t)seq * max_blocks_per_seq;
-    p_begin = 0;
-    // never address past the block table, whatever ctx_lens holds
+    // the window [lo, hi) of this sequence; never address past the block
+    // table, whatever ctx_lens holds
+    p_begin = win_lo ? max(win_lo[seq], 0) : 0;
     p_end = min(ctx_lens[seq], max_blocks_per_seq * src.block_size);
+    if (win_hi) p_end = min(p_end, win_hi[seq]);
   } else {
     p_begin = pos_begin_flat;
     p_end = pos_end_flat;
@@ -261,15 +265,15 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
 // One wavefront owns one split of one (sequence, KV head, chunk of up to 4
 // query heads); there are no workgroup barriers.  Per 64-token tile:
 //  * QK^T on v_mfma_i32_16x16x64_i8.  The A operand holds q as integer digit
-//    planes: q of head h is scaled by a power of two so |q| < 2^22, rounded,
-//    and written as three balanced base-256 signed digits; A row 4h+j is digit
-//    j of head h (row 4h+3 is zero).  The B operand is the K codes as stored
-//    (int8, head_dim contiguous per token), so each lane loads 16 contiguous
-//    bytes per MFMA.  With the MFMA output layout (lane l holds rows
-//    4*(l/16)..+3 of column l%16) every lane ends up with the three exact
-//    digit sums of one (head, token) pair: score = (I0 + 256 I1 + 65536 I2) *
-//    2^(e-22) * k_scale * 1/sqrt(head_dim).  The only rounding beyond the
-//    reference's is q's 23-bit rounding relative to its head's maximum.
+//    planes: q of head h is scaled by a power of two so |q| < 2^30, rounded,
+//    and written as four balanced base-256 signed digits; A row 4h+j is digit
+//    j of head h.  The B operand is the K codes as stored (int8, head_dim
+//    contiguous per token), so each lane loads 16 contiguous bytes per MFMA.
+//    With the MFMA output layout (lane l holds rows 4*(l/16)..+3 of column
+//    l%16) every lane ends up with the four exact digit sums of one (head,
+//    token) pair: score = (I0 + 256 I1 + 2^16 I2 + 2^24 I3) * 2^(e-30) *
+//    k_scale * 1/sqrt(head_dim).  The only rounding beyond the reference's is
+//    q's 31-bit rounding relative to its head's maximum.
 //  * online softmax per head inside each 16-lane row (DPP reductions).
 //  * PV on the VALU: p * v_scale goes through LDS to a lane layout where each
 //    lane owns head_dim/16 dimensions of one token per round; each V code is
@@ -308,8 +312,9 @@ template <int HD, int NWV, int KT>
 __global__ __launch_bounds__(64 * NWV, HD == 256 ? 1 : 8 / NWV) void paged_attn_mfma_kernel(
     const float* __restrict__ q, const int8_t* __restrict__ kc, const float* __restrict__ ks,
     const int8_t* __restrict__ vc, const float* __restrict__ vs, const int32_t* __restrict__ tables,
-    const int32_t* __restrict__ ctx_lens, int max_blocks, int bs_log2, int n_head, int n_head_kv,
-    int n_hchunks, int split_len, int n_splits, bool kv_major, float* __restrict__ partial) {
+    const int32_t* __restrict__ ctx_lens, const int32_t* __restrict__ win_lo, const int32_t* __restrict__ win_hi,
+    int max_blocks, int bs_log2, int n_head, int n_head_kv, int n_hchunks, int split_len, int n_splits,
+    bool kv_major, float* __restrict__ partial) {
   constexpr int NMI = HD / 64;  // MFMAs per 16-token sub-tile
   constexpr int VD = HD / 16;   // dims per lane in the PV layout
   constexpr int VW = VD / 4;    // V dwords per lane per round
@@ -334,8 +339,11 @@ __global__ __launch_bounds__(64 * NWV, HD == 256 ? 1 : 8 / NWV) void paged_attn_
   const int G = min(4, group - hc * 4);
   const int kv_dim = n_head_kv * HD;
   const int32_t* table = tables + (size_t)seq * max_blocks;
-  const int p_end = min(ctx_lens[seq], max_blocks << bs_log2);
-  const int s_begin = split * split_len;
+  // positions [lo, p_end): the sequence's window (ctx_lens and the block
+  // table bound it); the splits tile it from lo (its length is at most max_ctx)
+  const int lo = win_lo ? max(win_lo[seq], 0) : 0;
+  const int p_end = min(min(ctx_lens[seq], win_hi ? win_hi[seq] : INT_MAX), max_blocks << bs_log2);
+  const int s_begin = lo + split * split_len;
   const int s_end = min(p_end, s_begin + split_len);
   float* pw = p_s[wave];
   int* rw = row_s[wave];
@@ -346,7 +354,7 @@ __global__ __launch_bounds__(64 * NWV, HD == 256 ? 1 : 8 / NWV) void paged_attn_
   // lane group c = lane/16 holds dims 64*mi + 16c .. +16 of MFMA mi
   const int r = lane & 15, c = lane >> 4;
   i32x4 qa[NMI];
-  float qscale;  // 2^(e-22) of head c (the head of this lane's scores)
+  float qscale;  // 2^-sh of head c (the head of this lane's scores)
   {
     const int qh = r >> 2, qj = r & 3;
     const bool hv = qh < G;
@@ -376,8 +384,10 @@ __global__ __launch_bounds__(64 * NWV, HD == 256 ? 1 : 8 / NWV) void paged_attn_
     badi |= __shfl_xor(badi, 32, 64);
     int e = 0;
     if (m > 0.f) (void)frexpf(m, &e);  // m < 2^e
-    const int sh = 22 - e;  // scales the values (2^(22 - e) itself overflows below 2^-105)
-    const float qs_row = badi ? __builtin_nanf("") : ldexpf(1.0f, e - 22);
+    // the values are scaled (2^(30 - e) itself overflows below 2^-97); the
+    // shift stops at 149, so that 2^-sh stays a (subnormal) fp32 value
+    const int sh = min(30 - e, 149);
+    const float qs_row = badi ? __builtin_nanf("") : ldexpf(1.0f, -sh);
 #pragma unroll
     for (int mi = 0; mi < NMI; mi++) {
       uint32_t dw[4];
@@ -386,11 +396,11 @@ __global__ __launch_bounds__(64 * NWV, HD == 256 ? 1 : 8 / NWV) void paged_attn_
         uint32_t acc = 0;
 #pragma unroll
         for (int b = 0; b < 4; b++) {
-          const int qi = (int)rintf(ldexpf(qv[mi][4 * k + b], sh));  // |qi| <= 2^22
-          const uint32_t u = ((uint32_t)(qi + 0x808080)) ^ 0x808080u;  // balanced digits
+          const int qi = (int)rintf(ldexpf(qv[mi][4 * k + b], sh));  // |qi| <= 2^30
+          const uint32_t u = ((uint32_t)qi + 0x80808080u) ^ 0x80808080u;  // balanced digits
           acc |= ((u >> (8 * (qj & 3))) & 0xFFu) << (8 * b);
         }
-        dw[k] = (qj == 3 || !hv) ? 0u : acc;
+        dw[k] = hv ? acc : 0u;
       }
       qa[mi] = i32x4{(int)dw[0], (int)dw[1], (int)dw[2], (int)dw[3]};
     }
@@ -484,7 +494,8 @@ __global__ __launch_bounds__(64 * NWV, HD == 256 ? 1 : 8 / NWV) void paged_attn_
 #pragma unroll
       for (int mi = 0; mi < NMI; mi++)
         cacc = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa[mi], kb[sl][sub][mi], cacc, 0, 0, 0);
-      const float sv = fmaf(65536.0f, (float)cacc[2], (float)(cacc[0] + (cacc[1] << 8)));
+      const float sv =
+          fmaf(16777216.0f, (float)cacc[3], fmaf(65536.0f, (float)cacc[2], (float)(cacc[0] + (cacc[1] << 8))));
       const bool valid = (t0 + 16 * sub + r < s_end) && c < G;
       sc[sub] = valid ? sv * qscale * ksl[16 * sub + r] * inv_sqrt : -INFINITY;
     }
@@ -660,13 +671,13 @@ int pick_splits(int units, int max_len) {
 }
 
 template <int HD, class Src>
-hipError_t run_attn(const float* q, Src src, const int32_t* tables, const int32_t* ctx,
-                    int max_blocks, int n_seq, int n_head, int n_head_kv, int pb, int pe,
+hipError_t run_attn(const float* q, Src src, const int32_t* tables, const int32_t* ctx, const int32_t* win_lo,
+                    const int32_t* win_hi, int max_blocks, int n_seq, int n_head, int n_head_kv, int pb, int pe,
                     int max_len, int n_splits, float* partial, float* out, hipStream_t s) {
   int split_len = (max_len + n_splits - 1) / n_splits;
   split_len = std::max(kTile, (split_len + kTile - 1) / kTile * kTile);
   hipLaunchKernelGGL((attn_split_kernel<HD, Src>), dim3(n_splits, n_head_kv, n_seq),
-                     dim3(kThreads), 0, s, q, src, tables, ctx, max_blocks, n_head, n_head_kv, pb,
+                     dim3(kThreads), 0, s, q, src, tables, ctx, win_lo, win_hi, max_blocks, n_head, n_head_kv, pb,
                      pe, split_len, n_splits, partial);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -740,12 +751,12 @@ hipError_t run_paged_mfma(const PagedAttnArgs& a, float* part, hipStream_t s) {
     if (grid.y > 65535 || grid.z > 65535) return hipErrorInvalidValue;
     if (kt == kAtMin)
       hipLaunchKernelGGL((paged_attn_mfma_kernel<HD, NWV, kAtMin>), grid, dim3(64 * NWV), 0, s, a.q, a.k_codes,
-                         a.k_scales, a.v_codes, a.v_scales, a.block_tables, a.ctx_lens,
+                         a.k_scales, a.v_codes, a.v_scales, a.block_tables, a.ctx_lens, a.win_lo, a.win_hi,
                          a.max_blocks_per_seq, log2_exact(a.block_size), a.n_head, a.n_head_kv,
                          n_hchunks, split_len, n_splits, kv_major, part);
     else
       hipLaunchKernelGGL((paged_attn_mfma_kernel<HD, NWV, kAt>), grid, dim3(64 * NWV), 0, s, a.q, a.k_codes,
-                         a.k_scales, a.v_codes, a.v_scales, a.block_tables, a.ctx_lens,
+                         a.k_scales, a.v_codes, a.v_scales, a.block_tables, a.ctx_lens, a.win_lo, a.win_hi,
                          a.max_blocks_per_seq, log2_exact(a.block_size), a.n_head, a.n_head_kv,
                          n_hchunks, split_len, n_splits, kv_major, part);
     return hipGetLastError();
@@ -779,13 +790,13 @@ hipError_t launch_paged_attn(const PagedAttnArgs& a, void* workspace, hipStream_
                a.n_head_kv * a.head_dim};
   switch (a.head_dim) {
     case 64:
-      return run_attn<64>(a.q, src, a.block_tables, a.ctx_lens, a.max_blocks_per_seq, a.n_seq,
+      return run_attn<64>(a.q, src, a.block_tables, a.ctx_lens, a.win_lo, a.win_hi, a.max_blocks_per_seq, a.n_seq,
                           a.n_head, a.n_head_kv, 0, 0, a.max_ctx, n_splits, part, a.out, s);
     case 128:
-      return run_attn<128>(a.q, src, a.block_tables, a.ctx_lens, a.max_blocks_per_seq, a.n_seq,
+      return run_attn<128>(a.q, src, a.block_tables, a.ctx_lens, a.win_lo, a.win_hi, a.max_blocks_per_seq, a.n_seq,
                            a.n_head, a.n_head_kv, 0, 0, a.max_ctx, n_splits, part, a.out, s);
     case 256:
-      return run_attn<256>(a.q, src, a.block_tables, a.ctx_lens, a.max_blocks_per_seq, a.n_seq,
+      return run_attn<256>(a.q, src, a.block_tables, a.ctx_lens, a.win_lo, a.win_hi, a.max_blocks_per_seq, a.n_seq,
                            a.n_head, a.n_head_kv, 0, 0, a.max_ctx, n_splits, part, a.out, s);
     default:
       return hipErrorInvalidValue;
@@ -856,13 +867,13 @@ hipError_t launch_flash_attn_f32(const float* q, const float* k, const float* v,
   FlatSrc src{k, v, n_head_kv * head_dim};
   switch (head_dim) {
     case 64:
-      return run_attn<64>(q, src, nullptr, nullptr, 0, 1, n_head, n_head_kv, pb, pe, len,
+      return run_attn<64>(q, src, nullptr, nullptr, nullptr, nullptr, 0, 1, n_head, n_head_kv, pb, pe, len,
                           n_splits, ws, out, s);
     case 128:
-      return run_attn<128>(q, src, nullptr, nullptr, 0, 1, n_head, n_head_kv, pb, pe, len,
+      return run_attn<128>(q, src, nullptr, nullptr, nullptr, nullptr, 0, 1, n_head, n_head_kv, pb, pe, len,
                            n_splits, ws, out, s);
     case 256:
-      return run_attn<256>(q, src, nullptr, nullptr, 0, 1, n_head, n_head_kv, pb, pe, len,
+      return run_attn<256>(q, src, nullptr, nullptr, nullptr, nullptr, 0, 1, n_head, n_head_kv, pb, pe, len,
                            n_splits, ws, out, s);
     default:
       return hipErrorInvalidValue;

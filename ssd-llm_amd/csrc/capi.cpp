@@ -712,6 +712,31 @@ int ssdq_paged_attention_int8_dev(const float* q, const int8_t* k_codes, const f
   return ok();
 }
 
+int ssdq_paged_attention_int8_window_dev(const float* q, const int8_t* k_codes, const float* k_scales,
+                                         const int8_t* v_codes, const float* v_scales,
+                                         const int32_t* block_tables, const int32_t* ctx_lens,
+                                         const int32_t* window_starts, const int32_t* window_ends, float* out,
+                                         size_t n_seq, size_t n_head, size_t n_head_kv, size_t head_dim,
+                                         size_t block_size, size_t max_blocks_per_seq, size_t max_ctx,
+                                         ssdq_stream_t stream) {
+  const char* fn = "ssdq_paged_attention_int8_window_dev";
+  if (n_seq == 0 || n_head == 0) return ok();
+  ssdq::PagedAttnArgs a;
+  int rc = paged_attention_args(fn, q, k_codes, k_scales, v_codes, v_scales, block_tables, ctx_lens, out, n_seq,
+                                n_head, n_head_kv, head_dim, block_size, max_blocks_per_seq, max_ctx, &a);
+  if (rc != SSDQ_OK) return rc;
+  a.win_lo = window_starts;
+  a.win_hi = window_ends;
+  hipStream_t s = (hipStream_t)stream;
+  const size_t wsb = ssdq::paged_attn_workspace_bytes(a, nullptr);
+  void* ws = nullptr;
+  hipError_t e = workspace_get(wsb, s, &ws);
+  if (e != hipSuccess) return hip_fail(e, "ssdq_paged_attention_int8_window_dev: workspace");
+  e = ssdq::launch_paged_attn(a, ws, s);
+  if (e != hipSuccess) return hip_fail(e, fn);
+  return ok();
+}
+
 int ssdq_paged_attention_int8_noalloc_dev(const float* q, const int8_t* k_codes, const float* k_scales,
                                           const int8_t* v_codes, const float* v_scales,
                                           const int32_t* block_tables, const int32_t* ctx_lens, float* out,

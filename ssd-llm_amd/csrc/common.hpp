@@ -94,6 +94,35 @@ __device__ __forceinline__ float wave_sum_l63(float v) {
   return v;
 }
 
+// DPP moves of a double (both halves moved with the same control).
+template <int CTRL>
+__device__ __forceinline__ double dpp_mov_d(double v) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)b, CTRL, 0xF, 0xF, true);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(b >> 32), CTRL, 0xF, 0xF, true);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ double dpp_upd_d(double v) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, ROW_MASK, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, ROW_MASK, 0xF, false);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+// wave_sum_l63 in double precision (the matvec kernels' row sums: terms of
+// very different sizes, as massive activation channels make them, cancel
+// without fp32 rounding).
+__device__ __forceinline__ double wave_sum_l63_d(double v) {
+  v += dpp_mov_d<0xB1>(v);
+  v += dpp_mov_d<0x4E>(v);
+  v += dpp_mov_d<0x124>(v);
+  v += dpp_mov_d<0x128>(v);
+  v += dpp_upd_d<0x142, 0xA>(v);
+  v += dpp_upd_d<0x143, 0xC>(v);
+  return v;
+}
+
 // Sum across the 64 lanes of a wavefront (result valid in every lane).
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -132,6 +132,11 @@ struct PagedAttnArgs {
   float* out;
   int n_seq, n_head, n_head_kv, head_dim, block_size, max_blocks_per_seq;
   int max_ctx;  // upper bound on ctx_lens (sizes the split-KV grid)
+  // Optional per-sequence position window (flash_attention_windowed,
+  // src/inference/flash_attention.rs:146-227): sequence s attends over
+  // [max(win_lo[s], 0), min(win_hi[s], ctx_lens[s])); null means 0 / no bound.
+  const int32_t* win_lo = nullptr;
+  const int32_t* win_hi = nullptr;
 };
 // Bytes of device workspace the split-KV attention needs for these shapes.
 size_t paged_attn_workspace_bytes(const PagedAttnArgs& a, int* n_splits_out);

@@ -311,32 +311,55 @@ __device__ __forceinline__ void stage_x(const float* __restrict__ x, int in_dim,
 
 // ---------------------------------------------------------- batch 1 path
 // Integer dot products on "digit planes" of x.  Each 32-element group of x is
-// scaled by a power of two so its largest magnitude sits just under 2^22 and
-// rounded to an integer xi (|xi| <= 2^22: the rounding error is at most 2^-23
-// of the group maximum).  xi is written in three balanced base-256 digits
-// (signed bytes), and the digits of the elements that meet one weight dword are
-// packed into "planes" of four bytes.  A weight dword of 4-bit codes then
-// costs two masks and six v_dot4_i32_i8; the three per-digit integer sums of a
-// group are recombined exactly (I0 + 256 I1 + 65536 I2), converted to float
-// once and scaled by the group's power of two.  Per element this is ~1.5 VALU
-// instructions instead of a float conversion plus an FMA.
+// scaled by a power of two so its largest magnitude sits just under 2^30 and
+// rounded to an integer xi (|xi| <= 2^30: the rounding error is at most 2^-31
+// of the group maximum, so an element 2^k below its group's largest keeps
+// 30 - k bits; with 22 bits, a group holding a channel 10^4 times the rest put
+// some Llama-shaped outputs outside the stated tolerance).  xi is written in
+// kDigits = 4 balanced base-256 digits (signed bytes), and the digits of the
+// elements that meet one weight dword are packed into "planes" of four bytes.
+// A weight dword of 4-bit codes then costs two masks and eight v_dot4_i32_i8;
+// the four per-digit integer sums of a group are recombined (I0 + 256 I1
+// exactly in int, then 2^16 I2 and 2^24 I3 in two fp32 FMAs), and scaled by
+// the group's power of two.  Per element this is ~2 VALU instructions instead
+// of a float conversion plus an FMA.  Each group's term (exact integer sum x
+// scales) and a lane's running sum are taken in double precision, and so is
+// the cross-lane row sum: with terms of very different sizes (massive
+// activation channels) an output that cancels to a small value keeps its
+// accuracy, where fp32 partial sums would each round at the terms' size.
 //
-// Group record in LDS (GW dwords): 24 plane dwords [k][parity][digit] for the
+// Group record in LDS (GW dwords): 32 plane dwords [k][parity][digit] for the
 // four 8-element weight dwords k (parity 0 = elements 8k+0,2,4,6, parity 1 =
-// 8k+1,3,5,7; Q8_0 instead uses elements 8k+0..3 / 8k+4..7), the scale 2^(E-22)
-// and the sum of x over the group (two half sums for Q6_K's 16-element scales).
+// 8k+1,3,5,7; Q8_0 instead uses elements 8k+0..3 / 8k+4..7), then at kDigScale
+// the scale 2^-sh and at kDigSum the sum of the group's integers xi as a double
+// (exact: below 2^36; two half sums for the 16-element scales of Q6_K / Q2_K
+// / Q3_K, the second at kDigSum + 2).  A group's term is then 2^-sh (S F - M
+// X) with F its digit sum and X that sum, both exact: the offset term uses
+// the same rounded x as the codes' term.
+constexpr int kDigits = 4;
+constexpr int kDigScale = 8 * kDigits, kDigSum = kDigScale + 1;
 template <int F> struct Dig;
-template <> struct Dig<kQ4_K> { static constexpr int NG = 2, GW = 26, US = 52; static constexpr bool contig = false; };
-template <> struct Dig<kQ4_0> { static constexpr int NG = 2, GW = 26, US = 52; static constexpr bool contig = false; };
-template <> struct Dig<kQ5_K> { static constexpr int NG = 2, GW = 26, US = 52; static constexpr bool contig = false; };
-template <> struct Dig<kQ8_0> { static constexpr int NG = 2, GW = 26, US = 52; static constexpr bool contig = true; };
-template <> struct Dig<kQ8_K> { static constexpr int NG = 2, GW = 26, US = 52; static constexpr bool contig = true; };
-template <> struct Dig<kQ6_K> { static constexpr int NG = 1, GW = 28, US = 28; static constexpr bool contig = false; };
+template <> struct Dig<kQ4_K> { static constexpr int NG = 2, GW = 36, US = 72; static constexpr bool contig = false; };
+template <> struct Dig<kQ4_0> { static constexpr int NG = 2, GW = 36, US = 72; static constexpr bool contig = false; };
+template <> struct Dig<kQ5_K> { static constexpr int NG = 2, GW = 36, US = 72; static constexpr bool contig = false; };
+template <> struct Dig<kQ8_0> { static constexpr int NG = 2, GW = 36, US = 72; static constexpr bool contig = true; };
+template <> struct Dig<kQ8_K> { static constexpr int NG = 2, GW = 36, US = 72; static constexpr bool contig = true; };
+template <> struct Dig<kQ6_K> { static constexpr int NG = 1, GW = 40, US = 40; static constexpr bool contig = false; };
 // Q2_K: a group record holds two 16-element sub-blocks, each as 4 phase planes
-// (elements p, p+4, p+8, p+12: the bytes a code dword yields for shift 2p) x 3
+// (elements p, p+4, p+8, p+12: the bytes a code dword yields for shift 2p) x 4
 // digits, then the scale and the two sub-block sums as for Q6_K.
-template <> struct Dig<kQ2_K> { static constexpr int NG = 2, GW = 28, US = 56; static constexpr bool contig = false; };
-template <> struct Dig<kQ3_K> { static constexpr int NG = 2, GW = 28, US = 56; static constexpr bool contig = false; };
+template <> struct Dig<kQ2_K> { static constexpr int NG = 2, GW = 40, US = 80; static constexpr bool contig = false; };
+template <> struct Dig<kQ3_K> { static constexpr int NG = 2, GW = 40, US = 80; static constexpr bool contig = false; };
+
+// A double kept in two dwords of a group record.
+__device__ __forceinline__ double pair_value(uint32_t lo, uint32_t hi) {
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ void pair_store(uint32_t* p, double d) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, d);
+  p[0] = (uint32_t)b;
+  p[1] = (uint32_t)(b >> 32);
+}
 
 __device__ __forceinline__ uint32_t plane_bytes(uint32_t a, uint32_t b, uint32_t c, uint32_t e, int d) {
   // byte d of a, b, c, e -> bytes 0, 1, 2, 3
@@ -393,64 +416,69 @@ __device__ __forceinline__ void stage_store(const XChunks<SIT>& st, int keff, ui
     const bool live = c0 < total;
     const int r = rows > 1 ? c0 / nchunk : 0, c = c0 - r * nchunk;
     const float* v = st.v[it];
-    float m = 0.f, s = 0.f;
+    float m = 0.f;
     bool bad = false;
 #pragma unroll
     for (int j = 0; j < 8; j++) {
       m = fmaxf(m, fabsf(v[j]));
-      s += v[j];
       bad |= !(fabsf(v[j]) < INFINITY);  // NaN or infinity
     }
     m = fmaxf(m, dpp_mov<0xB1>(m));
     m = fmaxf(m, dpp_mov<0x4E>(m));
-    const float s_half = s + dpp_mov<0xB1>(s);  // Q6_K: sum over this half of the group
-    s = s_half + dpp_mov<0x4E>(s_half);
     const int k = c & 3;
     int e = 0;
     if (m > 0.f) (void)frexpf(m, &e);  // m < 2^e
-    // the value is scaled, not multiplied by 2^(22 - e): that factor overflows
-    // for groups whose largest magnitude is below 2^-105
-    const int sh = 22 - e;
+    // the value is scaled, not multiplied by 2^(30 - e): that factor overflows
+    // for groups whose largest magnitude is below 2^-97; and the shift stops
+    // at 149, so that the scale 2^-sh stays a (subnormal) fp32 value: groups
+    // below 2^-119 keep fp32's subnormal resolution instead
+    const int sh = min(30 - e, 149);
     uint32_t u[8];
+    double s = 0.0;  // the chunk's integers, summed exactly
 #pragma unroll
     for (int j = 0; j < 8; j++) {
-      const int xi = (int)rintf(ldexpf(v[j], sh));     // |xi| <= 2^22
-      u[j] = ((uint32_t)(xi + 0x808080)) ^ 0x808080u;  // bytes 0-2: balanced digits
+      const int xi = (int)rintf(ldexpf(v[j], sh));  // |xi| <= 2^30
+      s += (double)xi;
+      // xi + 0x80808080 lies in [0, 2^32): its bytes are the balanced digits + 128
+      u[j] = ((uint32_t)xi + 0x80808080u) ^ 0x80808080u;
     }
+    const double s_half = s + dpp_mov_d<0xB1>(s);  // sum over this 16-element half of the group
+    s = s_half + dpp_mov_d<0x4E>(s_half);
     bool gbad = bad;
     gbad |= __shfl_xor(gbad ? 1 : 0, 1, 64) != 0;
     gbad |= __shfl_xor(gbad ? 1 : 0, 2, 64) != 0;
     if (live) {
       const int g = c >> 2;
       uint32_t* rec = lds + (size_t)r * lds_stride + (size_t)(g / D::NG) * D::US + (g % D::NG) * D::GW;
-      uint32_t* pl = rec + 6 * k;
+      uint32_t* pl = rec + 2 * kDigits * k;
       if constexpr (F == kQ2_K || F == kQ3_K) {
         // chunk k is half k & 1 of sub-block k >> 1: bytes 2 (k & 1), +1 of its
         // phase planes (elements p and p + 4 of this chunk)
-        uint16_t* pb = reinterpret_cast<uint16_t*>(rec + 12 * (k >> 1)) + (k & 1);
+        uint16_t* pb = reinterpret_cast<uint16_t*>(rec + 4 * kDigits * (k >> 1)) + (k & 1);
 #pragma unroll
         for (int ph = 0; ph < 4; ph++)
 #pragma unroll
-          for (int d = 0; d < 3; d++)
-            pb[2 * (3 * ph + d)] =
+          for (int d = 0; d < kDigits; d++)
+            pb[2 * (kDigits * ph + d)] =
                 (uint16_t)__builtin_amdgcn_perm(u[4 + ph], u[ph], (uint32_t)d | ((uint32_t)(4 + d) << 8) | 0x0C0C0000u);
       } else
 #pragma unroll
-      for (int d = 0; d < 3; d++) {
+      for (int d = 0; d < kDigits; d++) {
         if (D::contig) {
           pl[d] = plane_bytes(u[0], u[1], u[2], u[3], d);
-          pl[3 + d] = plane_bytes(u[4], u[5], u[6], u[7], d);
+          pl[kDigits + d] = plane_bytes(u[4], u[5], u[6], u[7], d);
         } else {
           pl[d] = plane_bytes(u[0], u[2], u[4], u[6], d);
-          pl[3 + d] = plane_bytes(u[1], u[3], u[5], u[7], d);
+          pl[kDigits + d] = plane_bytes(u[1], u[3], u[5], u[7], d);
         }
       }
+      constexpr bool halves = D::GW == 40;  // two 16-element sums per record
       if (k == 0) {
         // a non-finite input poisons its group's result instead of being rounded
-        rec[24] = __float_as_uint(gbad ? __builtin_nanf("") : ldexpf(1.0f, e - 22));
-        rec[25] = __float_as_uint(D::GW == 28 ? s_half : s);
+        rec[kDigScale] = __float_as_uint(gbad ? __builtin_nanf("") : ldexpf(1.0f, -sh));
+        pair_store(rec + kDigSum, halves ? s_half : s);
       }
-      if (D::GW == 28 && k == 2) rec[26] = __float_as_uint(s_half);
+      if (halves && k == 2) pair_store(rec + kDigSum + 2, s_half);
     }
   }
 }
@@ -459,9 +487,10 @@ __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
   return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
 
-// I0 + 256 I1 + 65536 I2 (|I1| <= 2^16 so the first two combine exactly in int)
-__device__ __forceinline__ float digits_value(int i0, int i1, int i2) {
-  return fmaf(65536.0f, (float)i2, (float)(i0 + (i1 << 8)));
+// I0 + 256 I1 + 2^16 (I2 + 256 I3), exactly (|I1|, |I3| < 2^20, so the pairs
+// combine exactly in int; the whole stays below 2^53)
+__device__ __forceinline__ double digits_value(int i0, int i1, int i2, int i3) {
+  return fma(65536.0, (double)(i2 + (i3 << 8)), (double)(i0 + (i1 << 8)));
 }
 
 // Applies one unit (raw weight dwords) to x given as digit planes pl[] (the
@@ -479,7 +508,7 @@ __device__ __forceinline__ uint32_t q5_high_odd(uint32_t hb) {
 }
 
 template <int F, class PL>
-__device__ __forceinline__ void accumulate_dig(const uint32_t* raw, int u, PL pl, float& acc) {
+__device__ __forceinline__ void accumulate_dig(const uint32_t* raw, int u, PL pl, double& acc) {
   using D = Dig<F>;
   if constexpr (F == kQ4_K || F == kQ4_0 || F == kQ5_K) {
     float sc[2], off[2];
@@ -501,7 +530,7 @@ __device__ __forceinline__ void accumulate_dig(const uint32_t* raw, int u, PL pl
     }
 #pragma unroll
     for (int h = 0; h < 2; h++) {
-      int i0 = 0, i1 = 0, i2 = 0;
+      int i0 = 0, i1 = 0, i2 = 0, i3 = 0;
 #pragma unroll
       for (int k = 0; k < 4; k++) {
         uint32_t wd;
@@ -513,50 +542,54 @@ __device__ __forceinline__ void accumulate_dig(const uint32_t* raw, int u, PL pl
           lo |= q5_high_even(hb);
           hi |= q5_high_odd(hb);
         }
-        const int b = h * D::GW + 6 * k;
+        const int b = h * D::GW + 2 * kDigits * k;
         i0 = dot4(lo, pl(b + 0), i0);
         i1 = dot4(lo, pl(b + 1), i1);
         i2 = dot4(lo, pl(b + 2), i2);
-        i0 = dot4(hi, pl(b + 3), i0);
-        i1 = dot4(hi, pl(b + 4), i1);
-        i2 = dot4(hi, pl(b + 5), i2);
+        i3 = dot4(lo, pl(b + 3), i3);
+        i0 = dot4(hi, pl(b + 4), i0);
+        i1 = dot4(hi, pl(b + 5), i1);
+        i2 = dot4(hi, pl(b + 6), i2);
+        i3 = dot4(hi, pl(b + 7), i3);
       }
-      const float f = digits_value(i0, i1, i2);
-      const float xscale = __uint_as_float(pl(h * D::GW + 24));
-      const float xsum = __uint_as_float(pl(h * D::GW + 25));
-      acc = fmaf(sc[h], f * xscale, fmaf(-off[h], xsum, acc));
+      // the scales d * s, dmin * m are exact products of fp32 values
+      const double xs = pair_value(pl(h * D::GW + kDigSum), pl(h * D::GW + kDigSum + 1));
+      const double t = fma((double)sc[h], digits_value(i0, i1, i2, i3), -(double)off[h] * xs);
+      acc = fma(t, (double)__uint_as_float(pl(h * D::GW + kDigScale)), acc);
     }
   } else if constexpr (F == kQ8_0) {
 #pragma unroll
     for (int h = 0; h < 2; h++) {
       const float d = h == 0 ? f16_to_f32(raw[0] & 0xFFFFu) : f16_to_f32(raw[8] >> 16);
-      int i0 = 0, i1 = 0, i2 = 0;
+      int i0 = 0, i1 = 0, i2 = 0, i3 = 0;
 #pragma unroll
       for (int c = 0; c < 8; c++) {
         const uint32_t wd = h == 0 ? __builtin_amdgcn_alignbit(raw[c + 1], raw[c], 16) : raw[9 + c];
-        const int b = h * D::GW + 6 * (c >> 1) + 3 * (c & 1);
+        const int b = h * D::GW + 2 * kDigits * (c >> 1) + kDigits * (c & 1);
         i0 = dot4(wd, pl(b + 0), i0);
         i1 = dot4(wd, pl(b + 1), i1);
         i2 = dot4(wd, pl(b + 2), i2);
+        i3 = dot4(wd, pl(b + 3), i3);
       }
-      const float xscale = __uint_as_float(pl(h * D::GW + 24));
-      acc = fmaf(d, digits_value(i0, i1, i2) * xscale, acc);
+      const double xscale = (double)__uint_as_float(pl(h * D::GW + kDigScale));
+      acc = fma((double)d, digits_value(i0, i1, i2, i3) * xscale, acc);
     }
   } else if constexpr (F == kQ8_K) {
     const float d = __uint_as_float(raw[0]);
 #pragma unroll
     for (int h = 0; h < 2; h++) {
-      int i0 = 0, i1 = 0, i2 = 0;
+      int i0 = 0, i1 = 0, i2 = 0, i3 = 0;
 #pragma unroll
       for (int c = 0; c < 8; c++) {
         const uint32_t wd = raw[1 + 8 * h + c];
-        const int b = h * D::GW + 6 * (c >> 1) + 3 * (c & 1);
+        const int b = h * D::GW + 2 * kDigits * (c >> 1) + kDigits * (c & 1);
         i0 = dot4(wd, pl(b + 0), i0);
         i1 = dot4(wd, pl(b + 1), i1);
         i2 = dot4(wd, pl(b + 2), i2);
+        i3 = dot4(wd, pl(b + 3), i3);
       }
-      const float xscale = __uint_as_float(pl(h * D::GW + 24));
-      acc = fmaf(d, digits_value(i0, i1, i2) * xscale, acc);
+      const double xscale = (double)__uint_as_float(pl(h * D::GW + kDigScale));
+      acc = fma((double)d, digits_value(i0, i1, i2, i3) * xscale, acc);
     }
   } else if constexpr (F == kQ2_K) {
     // 16 sub-blocks of 16 elements; scale / min = low / high nibble of the
@@ -564,23 +597,24 @@ __device__ __forceinline__ void accumulate_dig(const uint32_t* raw, int u, PL pl
     const float d = f16_to_f32(raw[0] & 0xFFFFu), dmin = f16_to_f32(raw[0] >> 16);
 #pragma unroll
     for (int h = 0; h < 2; h++) {
-      const float xscale = __uint_as_float(pl(h * D::GW + 24));
+      const double xscale = (double)__uint_as_float(pl(h * D::GW + kDigScale));
 #pragma unroll
       for (int sb = 0; sb < 2; sb++) {
         const uint32_t wd = raw[2 + 2 * h + sb];
         const uint32_t scb = (raw[1] >> (8 * (2 * h + sb))) & 0xFFu;
-        int i0 = 0, i1 = 0, i2 = 0;
+        int i0 = 0, i1 = 0, i2 = 0, i3 = 0;
 #pragma unroll
         for (int ph = 0; ph < 4; ph++) {
           const uint32_t q = (wd >> (2 * ph)) & 0x03030303u;
-          const int b = h * D::GW + 12 * sb + 3 * ph;
+          const int b = h * D::GW + 4 * kDigits * sb + kDigits * ph;
           i0 = dot4(q, pl(b + 0), i0);
           i1 = dot4(q, pl(b + 1), i1);
           i2 = dot4(q, pl(b + 2), i2);
+          i3 = dot4(q, pl(b + 3), i3);
         }
-        const float S = d * (float)(scb & 15u), Mn = dmin * (float)(scb >> 4);
-        const float xsum = __uint_as_float(pl(h * D::GW + 25 + sb));
-        acc = fmaf(S, digits_value(i0, i1, i2) * xscale, fmaf(-Mn, xsum, acc));
+        const float S = d * (float)(scb & 15u), Mn = dmin * (float)(scb >> 4);  // exact products
+        const double xs = pair_value(pl(h * D::GW + kDigSum + 2 * sb), pl(h * D::GW + kDigSum + 2 * sb + 1));
+        acc = fma(fma((double)S, digits_value(i0, i1, i2, i3), -(double)Mn * xs), xscale, acc);
       }
     }
   } else if constexpr (F == kQ3_K) {
@@ -597,7 +631,7 @@ __device__ __forceinline__ void accumulate_dig(const uint32_t* raw, int u, PL pl
     const uint32_t hi2byte = (raw[8] >> (16 + 8 * (j & 1))) & 0xFFu;  // scales[8 + j]
 #pragma unroll
     for (int h = 0; h < 2; h++) {
-      const float xscale = __uint_as_float(pl(h * D::GW + 24));
+      const double xscale = (double)__uint_as_float(pl(h * D::GW + kDigScale));
 #pragma unroll
       for (int sb = 0; sb < 2; sb++) {
         const int s4 = 2 * h + sb;  // sub-block 4j + s4
@@ -607,21 +641,22 @@ __device__ __forceinline__ void accumulate_dig(const uint32_t* raw, int u, PL pl
         // byte i is the high bit of element 4 i + p
         const uint32_t nib = (hw >> 4) & 0x0F0Fu;
         const uint32_t hr = __builtin_amdgcn_perm(nib, hw, 0x05010400u);
-        int i0 = 0, i1 = 0, i2 = 0;
+        int i0 = 0, i1 = 0, i2 = 0, i3 = 0;
 #pragma unroll
         for (int ph = 0; ph < 4; ph++) {
           const uint32_t q = ((qd[s4] >> (2 * ph)) & 0x03030303u) | (((hr >> ph) & 0x01010101u) << 2);
-          const int b = h * D::GW + 12 * sb + 3 * ph;
+          const int b = h * D::GW + 4 * kDigits * sb + kDigits * ph;
           i0 = dot4(q, pl(b + 0), i0);
           i1 = dot4(q, pl(b + 1), i1);
           i2 = dot4(q, pl(b + 2), i2);
+          i3 = dot4(q, pl(b + 3), i3);
         }
         const uint32_t lo4 = (raw[8] >> (8 * h + 4 * sb)) & 15u;  // scales[2j + h] nibble sb
         const uint32_t hi2 = (hi2byte >> (2 * s4)) & 3u;
         const int sv = (int)((lo4 | (hi2 << 4)) ^ 32u) - 32;  // sign-extended 6 bits
-        const float S = d * (float)sv;
-        const float xsum = __uint_as_float(pl(h * D::GW + 25 + sb));
-        acc = fmaf(S, digits_value(i0, i1, i2) * xscale, fmaf(-4.0f * S, xsum, acc));
+        const float S = d * (float)sv;  // exact product
+        const double xs = pair_value(pl(h * D::GW + kDigSum + 2 * sb), pl(h * D::GW + kDigSum + 2 * sb + 1));
+        acc = fma((double)S * fma(-4.0, xs, digits_value(i0, i1, i2, i3)), xscale, acc);
       }
     }
   } else {  // kQ6_K quarter: 6-bit codes + 32 as bytes, two 16-element scale groups
@@ -632,10 +667,10 @@ __device__ __forceinline__ void accumulate_dig(const uint32_t* raw, int u, PL pl
 #pragma unroll
     for (int j = 0; j < 2; j++) qh[j] = __builtin_amdgcn_alignbit(raw[6 + j], raw[5 + j], sh);
     const float d = f16_to_f32(raw[8] >> 16);
-    const float xscale = __uint_as_float(pl(24));
+    const double xscale = (double)__uint_as_float(pl(kDigScale));
 #pragma unroll
     for (int h = 0; h < 2; h++) {
-      int i0 = 0, i1 = 0, i2 = 0;
+      int i0 = 0, i1 = 0, i2 = 0, i3 = 0;
 #pragma unroll
       for (int kk = 0; kk < 2; kk++) {
         const int k = 2 * h + kk;
@@ -645,17 +680,19 @@ __device__ __forceinline__ void accumulate_dig(const uint32_t* raw, int u, PL pl
         const uint32_t ho = ((p << 2) & 0x00300030u) | ((p >> 2) & 0x30003000u);
         const uint32_t ee = (ql[k] & 0x0F0F0F0Fu) | he;
         const uint32_t eo = ((ql[k] >> 4) & 0x0F0F0F0Fu) | ho;
-        const int b = 6 * k;
+        const int b = 2 * kDigits * k;
         i0 = dot4(ee, pl(b + 0), i0);
         i1 = dot4(ee, pl(b + 1), i1);
         i2 = dot4(ee, pl(b + 2), i2);
-        i0 = dot4(eo, pl(b + 3), i0);
-        i1 = dot4(eo, pl(b + 4), i1);
-        i2 = dot4(eo, pl(b + 5), i2);
+        i3 = dot4(ee, pl(b + 3), i3);
+        i0 = dot4(eo, pl(b + 4), i0);
+        i1 = dot4(eo, pl(b + 5), i1);
+        i2 = dot4(eo, pl(b + 6), i2);
+        i3 = dot4(eo, pl(b + 7), i3);
       }
-      const float sg = d * (float)(int8_t)((raw[8] >> (8 * h)) & 0xFFu);
-      const float xsum = __uint_as_float(pl(25 + h));
-      acc = fmaf(sg, digits_value(i0, i1, i2) * xscale, fmaf(-32.0f * sg, xsum, acc));
+      const float sg = d * (float)(int8_t)((raw[8] >> (8 * h)) & 0xFFu);  // exact product
+      const double xs = pair_value(pl(kDigSum + 2 * h), pl(kDigSum + 2 * h + 1));
+      acc = fma((double)sg * fma(-32.0, xs, digits_value(i0, i1, i2, i3)), xscale, acc);
     }
   }
 }
@@ -787,10 +824,13 @@ __global__ __launch_bounds__(768) void mv_b1(const uint8_t* __restrict__ w,
   const int bpr = min(slice_bpr, row_bpr - blk0);  // blocks of this slice
   w += (size_t)blk0 * Geom<F>::bb;
   x += (size_t)blk0 * Geom<F>::bs;
-  y += (size_t)blockIdx.y * out_dim;
+  // slice z of a K-sliced row writes its partial sums as doubles to
+  // ((double*)y)[z * out_dim + row] (the slice reduction adds them in order)
+  const bool sliced = gridDim.y > 1;
+  double* yp = reinterpret_cast<double*>(y) + (size_t)blockIdx.y * out_dim;
   const int keff = bpr * Geom<F>::bs;
   const int U = keff / FU::E;
-  float* red = reinterpret_cast<float*>(lds + (size_t)U * US);  // [stream][RMAX][ks]
+  double* red = reinterpret_cast<double*>(lds + (size_t)U * US);  // [stream][RMAX][ks]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nw = blockDim.x >> 6, kw = wave % ks, stream = wave / ks, rs = nw / ks;
   const size_t row_bytes = (size_t)row_bpr * Geom<F>::bb;
@@ -877,11 +917,11 @@ __global__ __launch_bounds__(768) void mv_b1(const uint8_t* __restrict__ w,
     }
   }
 
-  float acc[RMAX];
+  double acc[RMAX];
 #pragma unroll
   for (int rr = 0; rr < RMAX; rr++) {  // 3.
     if (rr >= 1 && rr + kB1Depth<RMAX> - 1 < RMAX) load_row(rr + kB1Depth<RMAX> - 1);
-    float a = 0.f;
+    double a = 0.0;
     if (ks > 1 || rr < n_rows) {  // uniform per wave: padding rows are not computed
 #pragma unroll
       for (int i = 0; i < UPL; i++) {
@@ -892,13 +932,13 @@ __global__ __launch_bounds__(768) void mv_b1(const uint8_t* __restrict__ w,
     acc[rr] = a;
   }
 #pragma unroll
-  for (int rr = 0; rr < RMAX; rr++) acc[rr] = wave_sum_l63(acc[rr]);
+  for (int rr = 0; rr < RMAX; rr++) acc[rr] = wave_sum_l63_d(acc[rr]);
   if constexpr (FUSE >= 2) {
     if (lane == 63) {
 #pragma unroll
       for (int rr = 0; rr < RMAX; rr += 2) {
         if (rr < n_rows) {
-          const float a0 = acc[rr], a1 = acc[rr + 1];
+          const float a0 = (float)acc[rr], a1 = (float)acc[rr + 1];
           int r;
           const int sg = fuse_seg(fu, r_begin + rr, r);
           if (fu.swiglu) {
@@ -926,7 +966,10 @@ __global__ __launch_bounds__(768) void mv_b1(const uint8_t* __restrict__ w,
     if (ks == 1) {
 #pragma unroll
       for (int rr = 0; rr < RMAX; rr++)
-        if (rr < n_rows) y[r_begin + rr * r_step] = acc[rr];
+        if (rr < n_rows) {
+          if (sliced) yp[r_begin + rr * r_step] = acc[rr];
+          else y[r_begin + rr * r_step] = (float)acc[rr];
+        }
     } else {
 #pragma unroll
       for (int rr = 0; rr < RMAX; rr++) red[(stream * RMAX + rr) * ks + kw] = acc[rr];
@@ -935,9 +978,10 @@ __global__ __launch_bounds__(768) void mv_b1(const uint8_t* __restrict__ w,
   if (ks > 1) {
     __syncthreads();
     if (kw == 0 && lane < n_rows) {  // the first wave of each row stream
-      float s = 0.f;
+      double s = 0.0;
       for (int k = 0; k < ks; k++) s += red[(stream * RMAX + lane) * ks + k];
-      y[r_begin + lane * r_step] = s;
+      if (sliced) yp[r_begin + lane * r_step] = s;
+      else y[r_begin + lane * r_step] = (float)s;
     }
   }
 }
@@ -961,7 +1005,8 @@ __global__ __launch_bounds__(768) void mv_b1s(const uint8_t* __restrict__ w, con
   const int bpr = min(slice_bpr, row_bpr - blk0);
   w += (size_t)blk0 * Geom<F>::bb;
   x += (size_t)blk0 * Geom<F>::bs;
-  y += (size_t)blockIdx.y * out_dim;
+  const bool sliced = gridDim.y > 1;  // partial sums as doubles (see mv_b1)
+  double* yp = reinterpret_cast<double*>(y) + (size_t)blockIdx.y * out_dim;
   const int keff = bpr * Geom<F>::bs;
   const int U = keff / FU::E;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -996,11 +1041,14 @@ __global__ __launch_bounds__(768) void mv_b1s(const uint8_t* __restrict__ w, con
   for (int r0 = 0; r0 < n_rows; r0 += D) {
 #pragma unroll
     for (int i = 0; i < D; i++) {
-      float a = 0.f;
+      double a = 0.0;
       accumulate_dig<F>(buf[i], u, [&](int t) { return pr[t]; }, a);
       load_row(r0 + i + D, buf[i]);
-      a = wave_sum_l63(live ? a : 0.f);
-      if (lane == 63 && r0 + i < n_rows) y[r_begin + r0 + i] = a;
+      a = wave_sum_l63_d(live ? a : 0.0);
+      if (lane == 63 && r0 + i < n_rows) {
+        if (sliced) yp[r_begin + r0 + i] = a;
+        else y[r_begin + r0 + i] = (float)a;
+      }
     }
   }
 }
@@ -1055,7 +1103,8 @@ __global__ __launch_bounds__(768) void mv_b1s_lds(const uint8_t* __restrict__ w,
   const int bpr = min(slice_bpr, row_bpr - blk0);
   w += (size_t)blk0 * Geom<F>::bb;
   x += (size_t)blk0 * Geom<F>::bs;
-  y += (size_t)blockIdx.y * out_dim;
+  const bool sliced = gridDim.y > 1;  // partial sums as doubles (see mv_b1)
+  double* yp = reinterpret_cast<double*>(y) + (size_t)blockIdx.y * out_dim;
   const int keff = bpr * Geom<F>::bs;
   const int U = keff / FastUnit<F>::E;
   const int nbytes = bpr * Geom<F>::bb;  // <= SLOT
@@ -1070,7 +1119,7 @@ __global__ __launch_bounds__(768) void mv_b1s_lds(const uint8_t* __restrict__ w,
 #pragma unroll
   for (int i = 0; i < UPL; i++) u[i] = FULL ? lane + 64 * i : min(lane + 64 * i, U - 1);
   uint8_t* wl = reinterpret_cast<uint8_t*>(lds4) + (size_t)U * US * sizeof(uint32_t);
-  float* red = reinterpret_cast<float*>(wl + (size_t)nwaves * D * SLOT) + (size_t)wave * rows_cap;
+  double* red = reinterpret_cast<double*>(wl + (size_t)nwaves * D * SLOT) + (size_t)wave * rows_cap;
   wl += (size_t)wave * D * SLOT;
   const uint32_t wl_off = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)wl;
 
@@ -1108,14 +1157,14 @@ __global__ __launch_bounds__(768) void mv_b1s_lds(const uint8_t* __restrict__ w,
       __builtin_amdgcn_sched_barrier(0);
       wait_vmcnt<NC * (D - 1)>();
       __builtin_amdgcn_sched_barrier(0);
-      float a = 0.f;
+      double a = 0.0;
 #pragma unroll
       for (int j = 0; j < UPL; j++) {
         uint32_t raw[FastUnit<F>::NW];
         load_unit<F>(wl + i * SLOT, u[j], raw);
-        float aj = 0.f;
+        double aj = 0.0;
         accumulate_dig<F>(raw, u[j], [&](int t) { return pr[j][t]; }, aj);
-        a += (FULL || lane + 64 * j < U) ? aj : 0.f;
+        a += (FULL || lane + 64 * j < U) ? aj : 0.0;
       }
       // The slot's LDS reads complete before its next copy is requested: the
       // compiler may issue the copy (inline assembly) right after the read
@@ -1125,13 +1174,16 @@ __global__ __launch_bounds__(768) void mv_b1s_lds(const uint8_t* __restrict__ w,
       wait_lgkmcnt0();
       __builtin_amdgcn_sched_barrier(0);
       copy_row(r0 + i + D, i);
-      a = wave_sum_l63(a);
+      a = wave_sum_l63_d(a);
       if (lane == 63 && r0 + i < n_rows) red[r0 + i] = a;
     }
   }
   // the window's last copies land before the workgroup's LDS is released
   wait_vmcnt<0>();
-  for (int r = lane; r < n_rows; r += 64) y[r_begin + r] = red[r];
+  for (int r = lane; r < n_rows; r += 64) {
+    if (sliced) yp[r_begin + r] = red[r];
+    else y[r_begin + r] = (float)red[r];
+  }
 }
 
 // Batch-1 matvec of whole rows (at most 64 units) with the rows copied into
@@ -1193,9 +1245,9 @@ __global__ __launch_bounds__(64 * (kB1rXW + NRW)) void mv_b1r(const uint8_t* __r
   const int wg_begin = b * q + min(b, rem), wg_rows = q + (b < rem ? 1 : 0);
   const int nr = wg_rows > rw ? (wg_rows - 1 - rw) / NRW + 1 : 0;  // <= rows_cap
   uint8_t* wl = reinterpret_cast<uint8_t*>(lds4) + (size_t)U * US * sizeof(uint32_t) + (size_t)rw * D * SLOT;
-  float* red = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(lds4) + (size_t)U * US * sizeof(uint32_t) +
-                                        (size_t)NRW * D * SLOT) +
-               (size_t)rw * rows_cap;
+  double* red = reinterpret_cast<double*>(reinterpret_cast<uint8_t*>(lds4) + (size_t)U * US * sizeof(uint32_t) +
+                                          (size_t)NRW * D * SLOT) +
+                (size_t)rw * rows_cap;
   const uint32_t wl_off = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)wl;
   auto copy_row = [&](int k, int sl) {
     const int row = min(wg_begin + rw + min(k, max(nr, 1) - 1) * NRW, out_dim - 1);
@@ -1231,39 +1283,41 @@ __global__ __launch_bounds__(64 * (kB1rXW + NRW)) void mv_b1r(const uint8_t* __r
       wait_lgkmcnt0();
       __builtin_amdgcn_sched_barrier(0);
       copy_row(r0 + i + D, i);
-      float a = 0.f;
+      double a = 0.0;
       accumulate_dig<F>(raw, u, [&](int t) { return pr[t]; }, a);
-      a = wave_sum_l63(lane < U ? a : 0.f);
+      a = wave_sum_l63_d(lane < U ? a : 0.0);
       if (lane == 63 && r0 + i < nr) red[r0 + i] = a;
     }
   }
   wait_vmcnt<0>();  // the last (clamped) copies land before the workgroup's LDS is released
-  for (int r = lane; r < nr; r += 64) y[wg_begin + rw + r * NRW] = red[r];
+  for (int r = lane; r < nr; r += 64) y[wg_begin + rw + r * NRW] = (float)red[r];
 }
 
-// With res non-null, y = res + (the slice sum), the residual add of a decoder
-// layer (y may alias res: each thread reads its element before writing it),
-// and the slice sum itself also goes to sum_out.
-__global__ __launch_bounds__(256) void slice_reduce_kernel(const float* __restrict__ part, float* y, int n,
+// Sums the K-slice partials (doubles, [slices][n]) in slice order and rounds
+// once.  With res non-null, y = res + (the slice sum), the residual add of a
+// decoder layer (y may alias res: each thread reads its element before
+// writing it), and the slice sum itself also goes to sum_out.
+__global__ __launch_bounds__(256) void slice_reduce_kernel(const double* __restrict__ part, float* y, int n,
                                                            int slices, const float* res, float* sum_out) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   // Eight slice loads are in flight together (addresses clamped, so the
   // loads are unconditional); the sum still runs in slice order.
-  float s = 0.f;
+  double s = 0.0;
   for (int z0 = 0; z0 < slices; z0 += 8) {
-    float v[8];
+    double v[8];
 #pragma unroll
     for (int k = 0; k < 8; k++) v[k] = part[(size_t)min(z0 + k, slices - 1) * n + i];
 #pragma unroll
     for (int k = 0; k < 8; k++)
       if (z0 + k < slices) s = z0 + k == 0 ? v[k] : s + v[k];
   }
+  const float sf = (float)s;
   if (res) {
-    y[i] = res[i] + s;
-    sum_out[i] = s;
+    y[i] = res[i] + sf;
+    sum_out[i] = sf;
   } else {
-    y[i] = s;
+    y[i] = sf;
   }
 }
 
@@ -1288,7 +1342,8 @@ __global__ __launch_bounds__(512) void mv_bn(const uint8_t* __restrict__ w,
   const int bpr = min(slice_bpr, row_bpr - blk0);
   w += (size_t)blk0 * Geom<F>::bb;
   x += (size_t)blk0 * Geom<F>::bs;
-  y += (size_t)blockIdx.y * NB * out_dim;
+  const bool sliced = gridDim.y > 1;  // partial sums as doubles (see mv_b1)
+  double* yp = reinterpret_cast<double*>(y) + (size_t)blockIdx.y * NB * out_dim;
   const int keff = bpr * Geom<F>::bs;
   const int U = keff / FU::E;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
@@ -1328,7 +1383,7 @@ __global__ __launch_bounds__(512) void mv_bn(const uint8_t* __restrict__ w,
 
   // Groups of RG rows: the next group's rows are requested before this one is
   // computed; each activation row's planes are read from LDS once per group.
-  float acc[RMAX][NB];
+  double acc[RMAX][NB];
 #pragma unroll
   for (int g0 = 0; g0 < RMAX; g0 += RG) {
     if (g0 + RG < RMAX) {
@@ -1345,7 +1400,7 @@ __global__ __launch_bounds__(512) void mv_bn(const uint8_t* __restrict__ w,
       }
 #pragma unroll
       for (int r = 0; r < RG; r++) {
-        float a = 0.f;
+        double a = 0.0;
         if (g0 + r < n_rows && ok)  // uniform per wave except the last units of a partial row
           accumulate_dig<F>(buf[g0 + r], u, [&](int t) { return pr[t]; }, a);
         acc[g0 + r][b] = a;
@@ -1355,13 +1410,16 @@ __global__ __launch_bounds__(512) void mv_bn(const uint8_t* __restrict__ w,
 #pragma unroll
   for (int rr = 0; rr < RMAX; rr++)
 #pragma unroll
-    for (int b = 0; b < NB; b++) acc[rr][b] = wave_sum_l63(acc[rr][b]);
+    for (int b = 0; b < NB; b++) acc[rr][b] = wave_sum_l63_d(acc[rr][b]);
   if (lane == 63) {
 #pragma unroll
     for (int rr = 0; rr < RMAX; rr++)
       if (rr < n_rows) {
 #pragma unroll
-        for (int b = 0; b < NB; b++) y[(size_t)b * out_dim + r_begin + rr * r_step] = acc[rr][b];
+        for (int b = 0; b < NB; b++) {
+          if (sliced) yp[(size_t)b * out_dim + r_begin + rr * r_step] = acc[rr][b];
+          else y[(size_t)b * out_dim + r_begin + rr * r_step] = (float)acc[rr][b];
+        }
       }
   }
 }
@@ -1615,7 +1673,7 @@ hipError_t run_b1(const uint8_t* w, const float* x, float* y, int out_dim, int r
                   int slice_bpr, int slices, int ks, hipStream_t s) {
   const int U = slice_bpr * Geom<F>::bs / FastUnit<F>::E;
   // x planes, then the per-wave row sums of every row stream (at most 12 waves)
-  const size_t lds = ((size_t)U * Dig<F>::US + (size_t)RMAX * 12) * sizeof(uint32_t);
+  const size_t lds = ((size_t)U * Dig<F>::US + (size_t)2 * RMAX * 12) * sizeof(uint32_t);  // planes, double sums
   if (lds > (size_t)lds_limit()) return hipErrorInvalidValue;
   // One workgroup per CU holding as many waves as fit (ks waves per row
   // stream); the occupancy is the same for every staging depth.
@@ -1682,6 +1740,14 @@ bool fast_aligned(const uint8_t* w, const float* x, int in_dim, int bpr) {
   else return (a & 3u) == 0 && (bpr % 2) == 0;  // Q4_0 / Q8_0 pairs, Q6_K dword rows
 }
 
+// Two units per lane keep two units' digit planes in registers: only Q6_K's
+// 36-dword records (72 VGPRs) fit beside the row buffers without spilling;
+// the 68- and 72-dword records of the other types (136-144 VGPRs) spill, and
+// scratch accesses would also break the exact wait counts of the kernels that
+// stream rows through LDS.
+template <int F>
+constexpr bool kTwoUnits = Dig<F>::US <= 36;
+
 // Row geometry of the batch-1 kernel: rows of up to 128 units run whole (one
 // wave per row stream); longer rows are cut into slices of at most 64 units.
 template <int F>
@@ -1696,11 +1762,9 @@ B1Plan<F> b1_plan(int bpr, int out_dim) {
   B1Plan<F> p;
   // Rows of 65-128 units run whole with two units per lane (3 rows per wave)
   // while that fits one round of workgroups and the kernel fits its registers
-  // (units of at most 10 raw dwords: Q4_0, Q6_K, Q2_K; the others spill at 768
-  // threads); otherwise as two K slices of one unit per lane, which fit more
-  // rows per wave (14336 x 4096 Q6_K: 18.4 -> 15.2 us)
-  constexpr bool two_units_fit = FastUnit<F>::NW <= 10;
-  if (U <= 64 || (U <= 128 && two_units_fit && out_dim <= 3 * 12 * device_cu_count())) {
+  // (kTwoUnits: Q6_K); otherwise as two K slices of one unit per lane, which
+  // fit more rows per wave (14336 x 4096 Q6_K: 18.4 -> 15.2 us)
+  if (U <= 64 || (U <= 128 && kTwoUnits<F> && out_dim <= 3 * 12 * device_cu_count())) {
     p.upl = U <= 64 ? 1 : 2;
     p.slice_bpr = bpr;
     p.full = (U == p.upl * 64);
@@ -1746,7 +1810,7 @@ hipError_t run_b1s(const uint8_t* w, const float* x, float* y, int out_dim, int 
     // slices that start 16-byte aligned in memory
     const long n_streams = n_wg * 12;
     const int rows_cap = (int)((out_dim + n_streams - 1) / n_streams) + 1;
-    const size_t lds2 = lds + (size_t)12 * 2 * LdsSlot<F, 1>::SLOT + (size_t)12 * rows_cap * sizeof(float);
+    const size_t lds2 = lds + (size_t)12 * 2 * LdsSlot<F, 1>::SLOT + (size_t)12 * rows_cap * sizeof(double);
     const bool aligned16 = ((uintptr_t)w % 16) == 0 && ((size_t)row_bpr * Geom<F>::bb) % 16 == 0 &&
                            ((size_t)slice_bpr * Geom<F>::bb) % 16 == 0;
     if (aligned16 && lds2 <= (size_t)lds_limit() && sit <= 2 && rows_cap > 12) {
@@ -1776,7 +1840,7 @@ hipError_t run_b1s(const uint8_t* w, const float* x, float* y, int out_dim, int 
 // streams, unaligned rows, LDS).
 template <int F>
 hipError_t run_b1s_lds_rows(const uint8_t* w, const float* x, float* y, int out_dim, int bpr, hipStream_t s) {
-  if constexpr (!kLdsRowStreams<F>) {
+  if constexpr (!kLdsRowStreams<F> || !kTwoUnits<F>) {
     return hipErrorNotSupported;
   } else {
     const int U = bpr * Geom<F>::bs / FastUnit<F>::E;
@@ -1789,7 +1853,7 @@ hipError_t run_b1s_lds_rows(const uint8_t* w, const float* x, float* y, int out_
     const int rows_cap = (int)((out_dim + n_streams - 1) / n_streams) + 1;
     if (rows_cap <= 12) return hipErrorNotSupported;
     const size_t lds = (size_t)U * Dig<F>::US * sizeof(uint32_t) + (size_t)12 * 2 * LdsSlot<F, 2>::SLOT +
-                       (size_t)12 * rows_cap * sizeof(float);
+                       (size_t)12 * rows_cap * sizeof(double);
     if (lds > (size_t)lds_limit()) return hipErrorNotSupported;
     auto go = [&](auto kern) {
       hipError_t e = set_lds_attr(kern, lds);
@@ -1831,7 +1895,7 @@ hipError_t run_b1r(const uint8_t* w, const float* x, float* y, int out_dim, int 
     const int n_wg = cu, q = out_dim / n_wg, rem = out_dim % n_wg;
     const int rows_cap = (q + (rem ? 1 : 0) + nrw - 1) / nrw;
     const size_t lds = (size_t)U * Dig<F>::US * sizeof(uint32_t) + (size_t)nrw * d * 1024 * NCR +
-                       (size_t)nrw * rows_cap * sizeof(float);
+                       (size_t)nrw * rows_cap * sizeof(double);
     if (lds > (size_t)lds_limit()) return hipErrorNotSupported;
     auto go = [&](auto kern, int threads) {
       hipError_t e = set_lds_attr(kern, lds);
@@ -1847,7 +1911,7 @@ hipError_t run_b1r(const uint8_t* w, const float* x, float* y, int out_dim, int 
 template <int F>
 size_t b1_workspace_floats(int out_dim, int bpr) {
   const B1Plan<F> p = b1_plan<F>(bpr, out_dim);
-  return p.slices > 1 ? (size_t)p.slices * out_dim : 0;
+  return p.slices > 1 ? (size_t)2 * p.slices * out_dim : 0;  // double partials
 }
 
 // acc non-null: acc = acc_in + W x (acc_in null: acc itself) instead of y =
@@ -1869,7 +1933,8 @@ hipError_t b1_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, 
     }
   }
   const B1Plan<F> p = b1_plan<F>(bpr, out_dim);
-  if (p.slices > 1 && (!ws || ws_floats < (size_t)p.slices * out_dim)) return hipSuccess;
+  // K-slice partials are doubles: an 8-byte aligned workspace of two floats each
+  if (p.slices > 1 && (!ws || ((uintptr_t)ws & 7) || ws_floats < (size_t)2 * p.slices * out_dim)) return hipSuccess;
   float* dst = p.slices > 1 ? ws : y;
   *used = true;
   hipError_t e;
@@ -1904,7 +1969,7 @@ hipError_t b1_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, 
       if (e != hipSuccess) return e;
       if (p.slices == 1) return acc ? launch_add(acc, acc_in, y, out_dim, s) : hipSuccess;
       hipLaunchKernelGGL(slice_reduce_kernel, dim3((unsigned)((out_dim + 255) / 256)), dim3(256), 0, s,
-                         ws, acc ? acc : y, out_dim, p.slices, acc_in, y);
+                         reinterpret_cast<const double*>(ws), acc ? acc : y, out_dim, p.slices, acc_in, y);
       return hipGetLastError();
     }
   }
@@ -1931,9 +1996,11 @@ hipError_t b1_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, 
   else if (p.upl == 1)
     e = p.full ? run_b1<F, 1, 5, true>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s)
                : run_b1<F, 1, 5, false>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s);
-  else
+  else if constexpr (kTwoUnits<F>)
     e = p.full ? run_b1<F, 2, 3, true>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s)
                : run_b1<F, 2, 3, false>(w, x, dst, out_dim, bpr, p.slice_bpr, p.slices, 1, s);
+  else
+    e = hipErrorNotSupported;  // b1_plan gives these types one unit per lane
   if (e == hipErrorNotSupported) {  // not launched: the caller takes the batched path
     *used = false;
     return hipSuccess;
@@ -1941,7 +2008,7 @@ hipError_t b1_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, 
   if (e != hipSuccess) return e;
   if (p.slices == 1) return acc ? launch_add(acc, acc_in, y, out_dim, s) : hipSuccess;
   hipLaunchKernelGGL(slice_reduce_kernel, dim3((unsigned)((out_dim + 255) / 256)), dim3(256), 0, s,
-                     ws, acc ? acc : y, out_dim, p.slices, acc_in, y);
+                     reinterpret_cast<const double*>(ws), acc ? acc : y, out_dim, p.slices, acc_in, y);
   return hipGetLastError();
 }
 
@@ -2048,9 +2115,9 @@ hipError_t fused_dispatch(const MatvecFuse& f, int vrows, const float* x, int in
     if (e != hipSuccess || *used) return e;
     return run_fused<F, 1, 12, 2>(f, x, vrows, bpr, s, used);
   }
-  // two units per lane: Q4_K / Q8_0 (12 / 17 raw dwords per unit) would spill
-  // in the fused form, so those rows take the separate launches
-  if constexpr (F == kQ6_K || F == kQ4_0) return run_fused<F, 2, 4, 2>(f, x, vrows, bpr, s, used);
+  // two units per lane (kTwoUnits: Q6_K); the other types' rows take the
+  // separate launches
+  if constexpr (kTwoUnits<F>) return run_fused<F, 2, 4, 2>(f, x, vrows, bpr, s, used);
   return hipSuccess;
 }
 
@@ -2076,11 +2143,13 @@ B1Plan<F> bn_plan(int bpr) {
 template <int F>
 size_t bn_workspace_floats(int out_dim, int bpr, int nb) {
   const B1Plan<F> p = bn_plan<F>(bpr);
-  return p.slices > 1 ? (size_t)p.slices * nb * out_dim : 0;
+  return p.slices > 1 ? (size_t)2 * p.slices * nb * out_dim : 0;  // double partials
 }
 
-// Rows per wave of mv_bn and rows per group (planes read once per group)
-template <int NB> constexpr int kBnRows = 6;
+// Rows per wave of mv_bn and rows per group (planes read once per group); 4-8
+// activation rows keep 3 rows per wave, so that the double row sums fit the
+// registers beside the row buffers
+template <int NB> constexpr int kBnRows = NB >= 4 ? 3 : 6;
 template <int NB> constexpr int kBnGroup = NB >= 4 ? 3 : 2;
 
 template <int F, int NB, int RMAX, int RG, bool FULL>
@@ -2143,7 +2212,8 @@ hipError_t bn_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, 
                        hipStream_t s, float* ws, size_t ws_floats, bool* used) {
   const B1Plan<F> p = bn_plan<F>(bpr);
   *used = false;
-  if (p.slices > 1 && (!ws || ws_floats < (size_t)p.slices * NB * out_dim)) return hipSuccess;
+  if (p.slices > 1 && (!ws || ((uintptr_t)ws & 7) || ws_floats < (size_t)2 * p.slices * NB * out_dim))
+    return hipSuccess;
   float* dst = p.slices > 1 ? ws : y;
   constexpr int R = kBnRows<NB>, G = kBnGroup<NB>;
   hipError_t e = p.full ? run_bn<F, NB, R, G, true>(w, x, dst, out_dim, in_dim, bpr, p.slice_bpr, p.slices, s)
@@ -2153,38 +2223,19 @@ hipError_t bn_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, 
   *used = true;
   if (p.slices == 1) return hipSuccess;
   const int n = NB * out_dim;
-  hipLaunchKernelGGL(slice_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, ws, y, n,
-                     p.slices, nullptr, nullptr);
+  hipLaunchKernelGGL(slice_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                     reinterpret_cast<const double*>(ws), y, n, p.slices, nullptr, nullptr);
   return hipGetLastError();
 }
 
-// The digit-plane kernels alone (mv_b1 at batch 1, mv_bn for chunks of 8 / 4 /
-// 2 rows and mv_b1 for a last single row), for the types whose float path is
-// mv_ext: *used = false when they do not apply (the first chunk decides).
+// The batch-1 digit-plane kernel alone, for the types whose float path is
+// mv_ext (their batches stay on mv_ext): *used = false when it does not apply.
 template <int F>
 hipError_t digit_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, int in_dim, int bpr,
                           int batch, hipStream_t s, float* ws, size_t ws_floats, bool* used) {
   *used = false;
-  if (bpr == 0 || !fast_aligned<F>(w, x, in_dim, bpr)) return hipSuccess;
-  if (batch == 1) return b1_dispatch<F>(w, x, y, out_dim, bpr, s, ws, ws_floats, used);
-  int b0 = 0;
-  while (b0 < batch) {
-    const int left = batch - b0;
-    const float* xb = x + (size_t)b0 * in_dim;
-    float* yb = y + (size_t)b0 * out_dim;
-    bool u = false;
-    hipError_t e;
-    int take;
-    if (left >= 8) { take = 8; e = bn_dispatch<F, 8>(w, xb, yb, out_dim, in_dim, bpr, s, ws, ws_floats, &u); }
-    else if (left >= 4) { take = 4; e = bn_dispatch<F, 4>(w, xb, yb, out_dim, in_dim, bpr, s, ws, ws_floats, &u); }
-    else if (left >= 2) { take = 2; e = bn_dispatch<F, 2>(w, xb, yb, out_dim, in_dim, bpr, s, ws, ws_floats, &u); }
-    else { take = 1; e = b1_dispatch<F>(w, xb, yb, out_dim, bpr, s, ws, ws_floats, &u); }
-    if (e != hipSuccess) return e;
-    if (!u) return b0 == 0 ? hipSuccess : hipErrorInvalidValue;
-    b0 += take;
-  }
-  *used = true;
-  return hipSuccess;
+  if (batch != 1 || bpr == 0 || !fast_aligned<F>(w, x, in_dim, bpr)) return hipSuccess;
+  return b1_dispatch<F>(w, x, y, out_dim, bpr, s, ws, ws_floats, used);
 }
 
 template <int F>

@@ -6,16 +6,17 @@
 //
 // x is carried as in the other digit-plane kernels: each 32-element block of
 // an activation row is scaled by a power of two so its largest magnitude sits
-// just under 2^22, rounded to integers xi, and written as three balanced
+// just under 2^30, rounded to integers xi, and written as four balanced
 // base-256 digits (signed bytes).  One Q8_0 block is one K = 32 step of
 // v_mfma_i32_16x16x32_i8:
-//   A (16 x 32 i8): row 4 b' + t is digit t of activation row 4 m + b' (t = 3
-//                   is zero), m = 0 for rows 0-3, 1 for rows 4-7;
+//   A (16 x 32 i8): row 4 b' + t is digit t of activation row 4 m + b',
+//                   m = 0 for rows 0-3, 1 for rows 4-7;
 //   B (32 x 16 i8): column c is the 32 codes of weight row c of the group;
-//   D (16 x 16 i32): lane l holds the exact integer sums of digits 0, 1, 2 of
+//   D (16 x 16 i32): lane l holds the exact integer sums of digits 0-3 of
 //                   activation row 4 m + l / 16 against weight row l % 16,
-// so every lane recombines its own digits (I0 + 256 I1 + 65536 I2), scales by
-// the block's d and the x block's power of two, and accumulates in fp32.
+// so every lane recombines its own digits (I0 + 256 I1 + 2^16 I2 + 2^24 I3),
+// scales by the block's d and the x block's power of two, and accumulates in
+// fp32.
 //
 // Layout: a workgroup of 12 waves owns a run of at most 48 rows (three
 // groups of 16; runs are spread evenly over the CUs, 43 rows each for 11008
@@ -69,7 +70,7 @@ struct Q8R {
   static constexpr int FS = NM * 512 + 16;
   static constexpr size_t frag_bytes = (size_t)NBLK * FS;
   static constexpr size_t scl_bytes = (size_t)NBLK * NB * 4;
-  static constexpr size_t red_bytes = (size_t)kRgpw * kRq * NM * 64 * 4;
+  static constexpr size_t red_bytes = (size_t)kRgpw * kRq * NM * 64 * 8;  // double partial sums
   static constexpr size_t lds = frag_bytes + scl_bytes + red_bytes;
 };
 
@@ -98,7 +99,7 @@ __global__ __launch_bounds__(768, 1) void mv_q8r(const uint8_t* __restrict__ w, 
   extern __shared__ __align__(16) uint8_t smem[];
   uint8_t* frag = smem;                                                         // [block][m][lane] (uint2)
   float* scl = reinterpret_cast<float*>(smem + P::frag_bytes);                  // [block][activation row]
-  float* red = reinterpret_cast<float*>(smem + P::frag_bytes + P::scl_bytes);   // [group][quarter][m][lane]
+  double* red = reinterpret_cast<double*>(smem + P::frag_bytes + P::scl_bytes);  // [group][quarter][m][lane]
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int gl = wave / kRq, kq = wave % kRq;
@@ -150,8 +151,8 @@ __global__ __launch_bounds__(768, 1) void mv_q8r(const uint8_t* __restrict__ w, 
   // the loads above are issued before anything waits for one
   __builtin_amdgcn_sched_barrier(0);
 
-  // ---- x digit planes of the whole row into LDS (A rows 4 b' + t: digits 0-2
-  // and a zero digit 3; the rows of activation rows past NB are never read)
+  // ---- x digit planes of the whole row into LDS (A rows 4 b' + t: digits
+  // 0-3; the rows of activation rows past NB are never read)
 #pragma unroll
   for (int k = 0; k < P::CPT; k++) {
     const int c0 = (int)threadIdx.x + P::THREADS * k;
@@ -174,21 +175,20 @@ __global__ __launch_bounds__(768, 1) void mv_q8r(const uint8_t* __restrict__ w, 
     badf = fmaxf(badf, dpp_mov<0x4E>(badf));
     int e = 0;
     if (m > 0.f) (void)frexpf(m, &e);  // m < 2^e
-    const int sh = 22 - e;
-    // xi = rint(v 2^sh), |xi| <= 2^22, as the low bits of 1.5 2^23 + v 2^sh
-    // (one rounding, to nearest even; the sum stays in [2^23, 2^24]); u = xi +
-    // 0x808080, whose bytes 0-2 xor 0x80 are the balanced digits
+    const int sh = min(30 - e, 149);  // 2^-sh stays a (subnormal) fp32 value
+    // xi = rint(v 2^sh), |xi| <= 2^30 (one rounding, to nearest even); u = xi +
+    // 0x80808080 lies in [0, 2^32), and its bytes xor 0x80 are the balanced
+    // digits
     uint32_t u[8];
 #pragma unroll
-    for (int i = 0; i < 8; i++) u[i] = __float_as_uint(ldexpf(v[i], sh) + 12582912.0f) - (0x4B400000u - 0x808080u);
+    for (int i = 0; i < 8; i++) u[i] = (uint32_t)(int)rintf(ldexpf(v[i], sh)) + 0x80808080u;
     if (c0 < chunks) {
       uint2* f = reinterpret_cast<uint2*>(frag + (size_t)j * P::FS + (b >> 2) * 512) + 16 * q + 4 * (b & 3);
 #pragma unroll
-      for (int d = 0; d < 3; d++)
+      for (int d = 0; d < 4; d++)
         f[d] = make_uint2(gather_byte(u[0], u[1], u[2], u[3], d) ^ 0x80808080u,
                           gather_byte(u[4], u[5], u[6], u[7], d) ^ 0x80808080u);
-      f[3] = make_uint2(0u, 0u);
-      if (q == 0) scl[j * NB + b] = badf != 0.f ? __builtin_nanf("") : ldexpf(1.0f, e - 22);
+      if (q == 0) scl[j * NB + b] = badf != 0.f ? __builtin_nanf("") : ldexpf(1.0f, -sh);
     }
   }
   __syncthreads();
@@ -204,9 +204,11 @@ __global__ __launch_bounds__(768, 1) void mv_q8r(const uint8_t* __restrict__ w, 
     amask[m4] = 4 * m4 + ((lane & 15) >> 2) < NB ? ~0ull : 0ull;
     xmask[m4] = 4 * m4 + kg < NB ? ~0u : 0u;
   }
-  float acc[NM];
+  // per-lane sums in double: terms of very different sizes (massive
+  // activation channels) cancel without fp32 rounding
+  double acc[NM];
 #pragma unroll
-  for (int m4 = 0; m4 < NM; m4++) acc[m4] = 0.f;
+  for (int m4 = 0; m4 < NM; m4++) acc[m4] = 0.0;
   if (busy) {
 #pragma unroll
     for (int s = 0; s < P::STEPS; s++) {
@@ -247,9 +249,10 @@ __global__ __launch_bounds__(768, 1) void mv_q8r(const uint8_t* __restrict__ w, 
           const int64_t aop = (int64_t)(NB % 4 == 0 ? av : av & amask[m4]);
           const float xs = __uint_as_float(__float_as_uint(scl[j * NB + min(4 * m4 + kg, NB - 1)]) & xmask[m4]);
           const i32x4 c = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, i32x4{0, 0, 0, 0}, 0, 0, 0);
-          // I0 + 256 I1 exactly in int (|I1| <= 2^16), then one rounding with 65536 I2
-          const float f = fmaf(65536.0f, (float)c.z, (float)(c.x + (c.y << 8)));
-          acc[m4] = fmaf(d, f * xs, acc[m4]);
+          // I0 + 256 I1 and I2 + 256 I3 exactly in int (|I1|, |I3| < 2^20), then
+          // the exact digit sum (below 2^53) and the exact scales in double
+          const double f = fma(65536.0, (double)(c.z + (c.w << 8)), (double)(c.x + (c.y << 8)));
+          acc[m4] = fma((double)d, f * (double)xs, acc[m4]);
         }
         if (bk & 1) __builtin_amdgcn_sched_barrier(0);  // two blocks at a time: bounded registers
       }
@@ -261,11 +264,11 @@ __global__ __launch_bounds__(768, 1) void mv_q8r(const uint8_t* __restrict__ w, 
   __syncthreads();
   for (int t = threadIdx.x; t < kRgpw * NM * 64; t += P::THREADS) {
     const int g2 = t / (NM * 64), m4 = (t >> 6) % NM, l = t & 63;
-    float sum = 0.f;
+    double sum = 0.0;
 #pragma unroll
     for (int q = 0; q < kRq; q++) sum += red[((g2 * kRq + q) * NM + m4) * 64 + l];
     const int b = 4 * m4 + (l >> 4), row = wg_row0 + g2 * kGRows + (l & 15);
-    if (b < NB && row < wg_end) y[(size_t)b * out_dim + row] = sum;
+    if (b < NB && row < wg_end) y[(size_t)b * out_dim + row] = (float)sum;
   }
 }
 

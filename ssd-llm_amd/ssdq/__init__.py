@@ -84,6 +84,8 @@ SIGNATURES = {
     "ssdq_paged_kv_append_dev": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _vp]),
     "ssdq_paged_attention_int8_dev": (
         _i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _vp]),
+    "ssdq_paged_attention_int8_window_dev": (
+        _i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _vp]),
     "ssdq_paged_attention_int8_noalloc_dev": (
         _i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _vp]),
     "ssdq_flash_attention_f32_dev": (_i, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _vp]),
@@ -271,6 +273,19 @@ def paged_attention_int8(q, k_codes, k_scales, v_codes, v_scales, block_tables, 
                      _ptr(q), _ptr(k_codes), _ptr(k_scales), _ptr(v_codes), _ptr(v_scales),
                      _ptr(block_tables), _ptr(ctx_lens), _ptr(out), n_seq, n_head, n_head_kv,
                      head_dim, block_size, max_blocks_per_seq, max_ctx, _stream(stream)))
+
+
+def paged_attention_int8_window(q, k_codes, k_scales, v_codes, v_scales, block_tables, ctx_lens,
+                                window_starts, window_ends, out, n_seq, n_head, n_head_kv, head_dim, block_size,
+                                max_blocks_per_seq, max_ctx, stream=None):
+    """paged_attention_int8 over [window_starts[s], min(window_ends[s], ctx_lens[s])) per
+    sequence (either tensor may be None)."""
+    return check("ssdq_paged_attention_int8_window_dev",
+                 lib().ssdq_paged_attention_int8_window_dev(
+                     _ptr(q), _ptr(k_codes), _ptr(k_scales), _ptr(v_codes), _ptr(v_scales),
+                     _ptr(block_tables), _ptr(ctx_lens), _ptr(window_starts), _ptr(window_ends), _ptr(out),
+                     n_seq, n_head, n_head_kv, head_dim, block_size, max_blocks_per_seq, max_ctx,
+                     _stream(stream)))
 
 
 def paged_attention_int8_noalloc(q, k_codes, k_scales, v_codes, v_scales, block_tables, ctx_lens, out,

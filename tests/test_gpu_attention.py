@@ -118,3 +118,46 @@ def test_flash_attention_host_twin():
         got = ctx.flash_attention_f32(q, k, v, n_head, n_kv, hd, seq, 0, seq)
     ref = o.flash_attention_f32(q, k, v, n_head, n_kv, hd, seq, 0, seq)
     assert_close(got, ref, "host twin")
+
+
+WINDOWS = [
+    # n_seq, n_head, n_kv, hd, bs, ctx_lens, window starts, window ends
+    # (the last sequence of the first case: start past its context -> zeros;
+    # the second: an end past the context, an empty window, a window inside
+    # one block, a start that is not block aligned)
+    (4, 32, 8, 128, 16, [4096, 700, 33, 100], [1000, 0, 17, 200], [3000, 700, 10 ** 6, 300]),
+    (4, 32, 8, 128, 16, [1000, 515, 64, 2048], [3, 300, 20, 1777], [5000, 300, 30, 2048]),
+    (2, 8, 2, 256, 32, [900, 65], [64, 1], [800, 64]),              # head_dim 256, block 32
+    (2, 16, 1, 64, 16, [999, 40], [500, 0], [999, 40]),             # MQA, head_dim 64
+    (2, 4, 2, 128, 1, [50, 30], [10, 29], [49, 30]),                # block size 1
+    (1, 32, 8, 128, 16, [32768], [32768 - 4096], [32768]),          # a 4k sliding window at 32k
+]
+
+
+@pytest.mark.parametrize("n_seq,n_head,n_kv,hd,bs,ctx,lo,hi", WINDOWS)
+def test_paged_attention_window(n_seq, n_head, n_kv, hd, bs, ctx, lo, hi):
+    """flash_attention_windowed (flash_attention.rs:146-227) over the paged INT8
+    cache: positions [lo, min(hi, ctx)) per sequence, zeros when empty."""
+    mb = max(1, -(-max(ctx) // bs))
+    announce("paged attention window", n_seq, n_head, n_kv, hd, bs, ctx, lo, hi)
+    q, kc, ks, vc, vs, tables, cl = paged_case(n_seq, n_head, n_kv, hd, bs, ctx, mb, sum(ctx) + 7 * hd)
+    lo, hi = np.asarray(lo, np.int32), np.asarray(hi, np.int32)
+    out = empty_dev(n_seq * n_head * hd, torch.float32)
+    out.fill_(np.nan)
+    rc = ssdq.paged_attention_int8_window(to_dev(q), to_dev(kc), to_dev(ks), to_dev(vc), to_dev(vs), to_dev(tables),
+                                          to_dev(cl), to_dev(lo), to_dev(hi), out, n_seq, n_head, n_kv, hd, bs, mb,
+                                          int(max(ctx)))
+    assert rc == 0
+    got = from_dev(out)
+    ref = o.paged_attention_int8_window(q, kc, ks, vc, vs, tables, cl, lo, hi, n_seq, n_head, n_kv, hd, bs, mb,
+                                        threads=8)
+    assert_close(got, ref, "paged attention window")
+    empty = np.minimum(hi, cl) <= lo
+    assert np.all(got.reshape(n_seq, -1)[empty] == 0)
+    # windows covering [0, ctx) reproduce the plain entry point bit for bit
+    full, rc = run_paged(q, kc, ks, vc, vs, tables, cl, n_seq, n_head, n_kv, hd, bs, mb)
+    assert rc == 0
+    out.fill_(np.nan)
+    rc = ssdq.paged_attention_int8_window(to_dev(q), to_dev(kc), to_dev(ks), to_dev(vc), to_dev(vs), to_dev(tables),
+                                          to_dev(cl), None, None, out, n_seq, n_head, n_kv, hd, bs, mb, int(max(ctx)))
+    assert rc == 0 and np.array_equal(from_dev(out).view(np.uint32), full.view(np.uint32))

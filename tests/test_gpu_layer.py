@@ -87,8 +87,10 @@ def test_swiglu(dtype, n_embd):
     u = o.matvec_exact(dtype, wu, x, n_ff, n_embd)
     ex, extra = swiglu_propagated(g, u)
     assert_propagated(from_dev(h), ex, extra, "swiglu")
-    # most outputs also sit within the plain tolerance of the fp32 reference
-    assert np.mean(np.abs(from_dev(h) - ref) <= tol(ref)) > 0.99
+    # and every output within the plain tolerance of the fp32 reference, except
+    # where the reference's own chain is more than half a tolerance from the
+    # exact composition
+    assert_close_attributed(from_dev(h), ref, ex, "swiglu")
 
 
 HEAD = [
@@ -116,9 +118,9 @@ def test_rmsnorm_output_head(dtype, vocab, n_embd):
     got = from_dev(y)
     # Outputs outside the tolerance of both the fp32 reference and the exact sum
     # are near-cancellations (|y| << sum |w x|).  The batch-1 kernel carries x
-    # with 23 significant bits per 32-element group (x * norm_w rounded once in
+    # with 31 significant bits per 32-element group (x * norm_w rounded once in
     # fp32, then to the group's digit grid), so such an output may differ from
-    # the exact sum by up to sum_e |w_e| (2^-23 max_group |x'| + 2^-24 |x'_e|).
+    # the exact sum by up to sum_e |w_e| (2^-31 max_group |x'| + 2^-24 |x'_e|).
     bad = np.flatnonzero((np.abs(got - ref) > tol(ref)) & (np.abs(got - ex) > tol(ex)))
     assert bad.size <= max(1, vocab // 10000), f"{bad.size} outputs outside tolerance"
     rb = len(w) // vocab
@@ -126,7 +128,7 @@ def test_rmsnorm_output_head(dtype, vocab, n_embd):
     gmax = np.repeat(xg.reshape(-1, 32).max(axis=1), 32)
     for i in bad:
         e, rc = o.matvec_elements(dtype, w[i * rb:(i + 1) * rb], 1, n_embd)
-        allow = tol(ex[i]) + float((np.abs(e[0].astype(np.float64)) * (gmax * 2.0 ** -23 + xg * 2.0 ** -24)).sum())
+        allow = tol(ex[i]) + float((np.abs(e[0].astype(np.float64)) * (gmax * 2.0 ** -31 + xg * 2.0 ** -24)).sum())
         assert abs(got[i] - ex[i]) <= allow, (i, got[i], ex[i], allow)
     print(f"{bad.size} near-cancelled outputs checked against the x-representation bound")
 

@@ -172,43 +172,49 @@ def test_extreme_and_nonfinite_activations(dtype, batch):
     # every output); row 2 with a whole 32-element block scaled by 1e30 and a
     # 1e3 outlier in another block; row 3 scaled to ~1e-30; row 4 scaled to
     # ~1e-35 (32-element groups whose largest value is below 2^-105, where
-    # 2^(22 - e) as a factor would overflow).  Batch 1 takes the rows one call
-    # at a time, batch 4 runs rows 0-3 as one batch and row 4 alone.  (x is
-    # carried relative to the largest value of its 32-element block, so values
-    # more than ~7 orders below it are not: the outlier stays within that
-    # range.)
+    # 2^(30 - e) as a factor would overflow); row 5 scaled to ~1e-37 (below
+    # 2^-119, where the scale of the digit grid stops at 2^-149).  Batch 1
+    # takes the rows one call at a time, batch 4 runs rows 0-3 as one batch and
+    # rows 4 and 5 alone.  (x is
+    # carried relative to the largest value of its 32-element block, with 30
+    # bits: values more than ~9 orders below it are not.)
     out_dim, in_dim = 300, 4096
     w = synth.quant_weights(dtype, out_dim, in_dim, 71)
-    x = synth.normal_f32((5, in_dim), 72)
+    x = synth.normal_f32((6, in_dim), 72)
     x[1, 1000] = np.nan
     x[2, 64:96] *= np.float32(1e30)
     x[2, 200] = np.float32(1e3)
     x[3] *= np.float32(1e-30)
     x[4] *= np.float32(1e-35)
+    x[5] *= np.float32(1e-37)
     assert np.abs(x[4]).max() < 2.0 ** -105
+    assert np.abs(x[5]).max() < 2.0 ** -119  # the digit grid's scale stops at 2^-149
     announce("matvec extreme activations", ssdq.TYPE_NAMES[dtype], batch)
     if batch == 4:
         y, rc = run(dtype, w, x[:4], out_dim, in_dim, 4)
         assert rc == 0
-        y4, rc = run(dtype, w, x[4], out_dim, in_dim, 1)
-        assert rc == 0
-        y = np.concatenate([y.reshape(4, out_dim), y4.reshape(1, out_dim)])
+        rows = [y.reshape(4, out_dim)]
+        for b in (4, 5):
+            yb, rc = run(dtype, w, x[b], out_dim, in_dim, 1)
+            assert rc == 0
+            rows.append(yb.reshape(1, out_dim))
+        y = np.concatenate(rows)
     else:
         rows = []
-        for b in range(5):
+        for b in range(6):
             yb, rc = run(dtype, w, x[b], out_dim, in_dim, 1)
             assert rc == 0
             rows.append(yb)
         y = np.stack(rows)
-    ref, exact = reference(dtype, w, x, out_dim, in_dim, 5)
-    ref, exact = ref.reshape(5, out_dim), exact.reshape(5, out_dim)
+    ref, exact = reference(dtype, w, x, out_dim, in_dim, 6)
+    ref, exact = ref.reshape(6, out_dim), exact.reshape(6, out_dim)
     assert np.all(np.isnan(ref[1])) and np.all(np.isnan(y[1]))
     for b in (0, 2):
         assert_close_attributed(y[b], ref[b], exact[b], f"row {b}")
-    # rows 3, 4: relative agreement (the absolute 1e-4 term says nothing at
+    # rows 3-5: relative agreement (the absolute 1e-4 term says nothing at
     # these magnitudes); the exact sums are double precision, so they hold the
     # 1e-35-scaled outputs (~1e-33, fp32 subnormal) without underflow
-    for b in (3, 4):
+    for b in (3, 4, 5):
         assert np.all(np.isfinite(y[b])), f"row {b}: non-finite output"
         scale = np.abs(exact[b]).max()
         assert scale > 0

@@ -388,6 +388,41 @@ def test_flash_attention_window_and_empty():
     assert np.all(empty == 0)
 
 
+def test_paged_attention_window_matches_double_two_pass():
+    # flash_attention_windowed (flash_attention.rs:146-227): positions
+    # window_start .. min(window_end, seq_len) per sequence, zeros when empty;
+    # pinned against two-pass double-precision attention over exactly those
+    # rows, and a full window against the unwindowed oracle bit for bit
+    g = np.random.default_rng(24)
+    n_seq, n_head, n_kv, hd, bs, mb = 5, 8, 2, 64, 16, 8
+    ctx = [100, 37, 128, 60, 90]
+    lo = np.array([13, 0, 127, 70, 5], np.int32)   # seq 3: start past ctx -> empty
+    hi = np.array([99, 20, 500, 80, 5], np.int32)  # seq 2: end past ctx; seq 4: empty
+    q, kc, ks, vc, vs, tables, cl = _paged_case(g, n_seq, n_head, n_kv, hd, bs, ctx, mb)
+    out = o.paged_attention_int8_window(q, kc, ks, vc, vs, tables, cl, lo, hi, n_seq, n_head, n_kv, hd, bs, mb)
+    out = out.reshape(n_seq, n_head, hd)
+    group = n_head // n_kv
+    for s in range(n_seq):
+        p = np.arange(lo[s], min(hi[s], ctx[s]))
+        if p.size == 0:
+            assert np.all(out[s] == 0), s
+            continue
+        rows = tables[s, p // bs] * bs + p % bs
+        for h in range(n_head):
+            kh = h // group
+            K = kc[rows, kh * hd:(kh + 1) * hd].astype(np.float32) * ks[rows, None]
+            V = vc[rows, kh * hd:(kh + 1) * hd].astype(np.float32) * vs[rows, None]
+            ref = _attn_double(q[s, h], K.astype(np.float32), V.astype(np.float32))
+            np.testing.assert_allclose(out[s, h], ref, rtol=1e-5, atol=1e-6)
+    full = o.paged_attention_int8_window(q, kc, ks, vc, vs, tables, cl, np.zeros(n_seq, np.int32),
+                                         cl.copy(), n_seq, n_head, n_kv, hd, bs, mb)
+    plain = o.paged_attention_int8(q, kc, ks, vc, vs, tables, cl, n_seq, n_head, n_kv, hd, bs, mb)
+    assert np.array_equal(full.view(np.uint32), plain.view(np.uint32))
+    nowin = o.paged_attention_int8_window(q, kc, ks, vc, vs, tables, cl, None, None, n_seq, n_head, n_kv, hd, bs,
+                                          mb)
+    assert np.array_equal(nowin.view(np.uint32), plain.view(np.uint32))
+
+
 def test_online_softmax_large_scores_finite():
     # flash_attention.rs:461-488: large inputs stay finite
     hd = 64

@@ -263,7 +263,7 @@ def main():
             "bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(value / HBM_PEAK_GBS, 4),
             "traffic": traffic_from_profiles("q4k_matvec_14336x4096"),
-            "kernel": "mv_b1<Q4_K>", "algo_bytes_per_launch": algo_bytes,
+            "kernel": "mv_b1r<Q4_K>", "algo_bytes_per_launch": algo_bytes,
         },
         "host_wall_s": round(wall, 4),
     }

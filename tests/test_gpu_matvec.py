@@ -292,7 +292,8 @@ K_SLICED = [  # K-sliced rows: slice partials in the workspace, summed in slice 
     (Q8_0, 4096, 28672),   # batch-1 kernel, 7 slices, interleaved row streams
     (Q4_0, 2000, 28800),   # 8 slices, partial last slice
     (Q6_K, 33, 14336),     # fewer rows than row streams
-    (Q6_K, 128256, 4096),  # output-head shape: long row streams through LDS, 2 slices
+    (Q6_K, 128256, 4096),  # output-head shape: whole-row LDS streams (128 units per row), no slices
+    (Q6_K, 20000, 8192),   # LDS row streams, 4 slices of 8 blocks (Q6_K head of an 8192-wide model)
     (Q4_K, 40000, 8704),   # LDS row streams, 3 slices of 12, 12 and 10 blocks (short last slice)
 ]
 

@@ -23,9 +23,10 @@ pytestmark = pytest.mark.gpu
 TYPES = list(ssdq.MATVEC_EXTRA_TYPES)
 # Signed 6-bit scales (IQ4_XS, Q3_K) make synthetic rows cancel heavily, so at
 # K = 14336 the reference's serial fp32 sum itself strays past the tolerance on
-# a few outputs; those are held to the same tolerance against the exact sum,
-# and at most 1% of the outputs may need it.
-ILL = 0.01
+# a few outputs; those are held to the same tolerance against the exact sum.
+# The most seen is 3 of the 2000 outputs of IQ4_XS 1000 x 14336 batch 2, so
+# this file allows 0.2% instead of the default 0.1%.
+ILL = 2e-3
 
 
 def run(dtype, w_dev, x, out_dim, in_dim, batch=1, generic=False):

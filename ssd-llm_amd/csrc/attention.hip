@@ -308,13 +308,14 @@ typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 
-template <int HD, int NWV, int KT>
+template <int HD, int NWV, int KT, bool NEW>
 __global__ __launch_bounds__(64 * NWV, HD == 256 ? 1 : 8 / NWV) void paged_attn_mfma_kernel(
     const float* __restrict__ q, const int8_t* __restrict__ kc, const float* __restrict__ ks,
     const int8_t* __restrict__ vc, const float* __restrict__ vs, const int32_t* __restrict__ tables,
     const int32_t* __restrict__ ctx_lens, const int32_t* __restrict__ win_lo, const int32_t* __restrict__ win_hi,
     int max_blocks, int bs_log2, int n_head, int n_head_kv, int n_hchunks, int split_len, int n_splits,
-    bool kv_major, float* __restrict__ partial) {
+    bool kv_major, float* __restrict__ partial, const float* __restrict__ new_k, const float* __restrict__ new_v,
+    const int32_t* __restrict__ new_slot, int8_t* kc_w, float* ks_w, int8_t* vc_w, float* vs_w) {
   constexpr int NMI = HD / 64;  // MFMAs per 16-token sub-tile
   constexpr int VD = HD / 16;   // dims per lane in the PV layout
   constexpr int VW = VD / 4;    // V dwords per lane per round
@@ -349,6 +350,39 @@ __global__ __launch_bounds__(64 * NWV, HD == 256 ? 1 : 8 / NWV) void paged_attn_
   int* rw = row_s[wave];
   float* ksw = ks_s[wave];
   float* vsw = vs_s[wave];
+
+  // ---- the sequence's new token (NEW: a decode step's INT8 append folded
+  // into this launch).  It sits at position ctx_len - 1, the last of the last
+  // split, so of that split's last tile.  Each wave of that split quantizes
+  // its KV head's slice of the token's K and V rows against the rows' scales
+  // (the absmax over all KV heads, kv_dim <= 1024; the arithmetic of
+  // kv_quantize_pipe_kernel): lanes 0 .. HD/4 - 1 four K elements each,
+  // lanes 32 .. 32 + HD/4 - 1 four V elements.  The codes reach the operand
+  // layouts below through the wave's LDS: the lanes that hold the token in
+  // the last tile take them, and its scales, instead of what the pool held.
+  // The same dwords are written to pool row new_slot[seq] at the end of the
+  // kernel (a store earlier would make the wave's later loads wait for it:
+  // vector memory counts both in order).  Waves that read that row before
+  // (clamped repeats of the last token) only read it into lanes that are
+  // masked out and take the new scales.  The rows are requested here, with q,
+  // so that both arrive in one round trip.
+  constexpr int kNewC = 4;  // float4 chunks per lane of a whole new row
+  const int pos_new = NEW ? ctx_lens[seq] - 1 : -1;
+  const bool has_new = NEW && pos_new >= s_begin && pos_new < s_end;
+  const bool nv_lane = lane >= 32;           // this lane's four new elements: V (else K)
+  const int nj = min(lane & 31, HD / 4 - 1);  // ... dims 4 nj .. 4 nj + 3 of head kvh
+  float4 kA[kNewC], vA[kNewC], nown;
+  if (has_new) {
+    const float* kr = new_k + (size_t)seq * kv_dim;
+    const float* vr = new_v + (size_t)seq * kv_dim;
+#pragma unroll
+    for (int i = 0; i < kNewC; i++) {  // chunks past kv_dim repeat the last one (masked below)
+      const int e = min(4 * lane + 256 * i, kv_dim - 4);
+      kA[i] = *reinterpret_cast<const float4*>(kr + e);
+      vA[i] = *reinterpret_cast<const float4*>(vr + e);
+    }
+    nown = *reinterpret_cast<const float4*>((nv_lane ? vr : kr) + (size_t)kvh * HD + 4 * nj);
+  }
 
   // ---- q digit planes (A operand): row r = lane%16 is digit r%4 of head r/4,
   // lane group c = lane/16 holds dims 64*mi + 16c .. +16 of MFMA mi
@@ -405,6 +439,37 @@ __global__ __launch_bounds__(64 * NWV, HD == 256 ? 1 : 8 / NWV) void paged_attn_
       qa[mi] = i32x4{(int)dw[0], (int)dw[1], (int)dw[2], (int)dw[3]};
     }
     qscale = __shfl(qs_row, 4 * c, 64);  // lane 4c holds digit 0 of head c
+  }
+  i32x4 knew[NMI];
+  uint32_t vnew[VW];
+  float ksc_new = 0.f, vsc_new = 0.f;
+  uint32_t ncode = 0;
+  if (has_new) {
+    float ka = 0.f, va = 0.f;
+#pragma unroll
+    for (int i = 0; i < kNewC; i++) {
+      if (4 * lane + 256 * i < kv_dim) {
+        ka = fmaxf(ka, fmaxf(fmaxf(fabsf(kA[i].x), fabsf(kA[i].y)), fmaxf(fabsf(kA[i].z), fabsf(kA[i].w))));
+        va = fmaxf(va, fmaxf(fmaxf(fabsf(vA[i].x), fabsf(vA[i].y)), fmaxf(fabsf(vA[i].z), fabsf(vA[i].w))));
+      }
+    }
+    ka = wave_max_dpp(ka);
+    va = wave_max_dpp(va);
+    const float kinv = ka != 0.0f ? 127.0f / ka : 0.0f, vinv = va != 0.0f ? 127.0f / va : 0.0f;
+    ksc_new = ka / 127.0f;  // 0 for an all-zero row
+    vsc_new = va / 127.0f;
+    ncode = kv_pack4(nown.x, nown.y, nown.z, nown.w, nv_lane ? vinv : kinv);
+    // K code dwords 0 .. HD/4 - 1, V code dwords 32 .. 32 + HD/4 - 1 (the
+    // wave's p_s is free until its first tile)
+    uint32_t* xw = reinterpret_cast<uint32_t*>(p_s[wave]);
+    xw[lane] = ncode;
+#pragma unroll
+    for (int mi = 0; mi < NMI; mi++) {  // K: dims 64 mi + 16 c .. + 16
+      const uint4 t = *reinterpret_cast<const uint4*>(xw + 16 * mi + 4 * (lane >> 4));
+      knew[mi] = i32x4{(int)t.x, (int)t.y, (int)t.z, (int)t.w};
+    }
+#pragma unroll
+    for (int w4 = 0; w4 < VW; w4++) vnew[w4] = xw[32 + VW * (lane & 15) + w4];  // V: dims VD dg .. + VD
   }
   const float inv_sqrt = 1.0f / sqrtf((float)HD);
   const int bs_mask = (1 << bs_log2) - 1;
@@ -473,8 +538,24 @@ __global__ __launch_bounds__(64 * NWV, HD == 256 ? 1 : 8 / NWV) void paged_attn_
     float* ksl = ksw + sl * KT;
     float* vsl = vsw + sl * KT;
     if (lane < KT) {  // scales of tile i (loaded one iteration ago)
-      ksl[lane] = ks_n;
-      vsl[lane] = vs_n;
+      const bool nt = has_new && tile_tok(i) == pos_new;
+      ksl[lane] = nt ? ksc_new : ks_n;
+      vsl[lane] = nt ? vsc_new : vs_n;
+    }
+    if (has_new && i == n_tiles - 1) {
+      // the new token's codes into this tile's operands (the tile's loads
+      // land first; the next tile's loads, issued below, are clamped repeats)
+      const int jr = pos_new - t0;
+#pragma unroll
+      for (int sub = 0; sub < NSUB; sub++)
+#pragma unroll
+        for (int mi = 0; mi < NMI; mi++)
+          if (16 * sub + r == jr) kb[sl][sub][mi] = knew[mi];
+#pragma unroll
+      for (int rr = 0; rr < NRR; rr++)
+#pragma unroll
+        for (int w4 = 0; w4 < VW; w4++)
+          if (4 * rr + tg == jr) vraw[sl][rr][w4] = vnew[w4];
     }
     {  // rows of tile i+1, their scales, the table entry of tile i+2, then K and V of tile i+1
       const int t = tile_tok(i + 1);
@@ -571,6 +652,18 @@ __global__ __launch_bounds__(64 * NWV, HD == 256 ? 1 : 8 / NWV) void paged_attn_
     float* rec = partial + (((size_t)seq * n_head + h0 + c) * n_splits + split) * (HD + 2);
     rec[0] = run_m;
     rec[1] = run_l;
+  }
+  if (has_new && hc == 0) {  // the new token's row slices and scales into the pool
+    const int32_t slot = new_slot[seq];
+    if (slot >= 0) {
+      if ((lane & 31) < HD / 4)
+        *reinterpret_cast<uint32_t*>((nv_lane ? vc_w : kc_w) + (size_t)slot * kv_dim + (size_t)kvh * HD + 4 * nj) =
+            ncode;
+      if (kvh == 0 && lane == 0) {
+        ks_w[slot] = ksc_new;
+        vs_w[slot] = vsc_new;
+      }
+    }
   }
 }
 
@@ -743,23 +836,23 @@ hipError_t run_paged_mfma(const PagedAttnArgs& a, float* part, hipStream_t s) {
   paged_mfma_splits(a, &n_splits, &split_len, &kt);
   const int group = a.n_head / a.n_head_kv, n_hchunks = (group + 3) / 4;
   // one workgroup per split over 8 (else 4) KV heads when they divide n_head_kv
-  auto go = [&](auto nwv_c, bool kv_major) {
+  auto launch = [&](auto nwv_c, auto new_c, bool kv_major) {
     constexpr int NWV = decltype(nwv_c)::value;
+    constexpr bool NEW = decltype(new_c)::value;
     const dim3 grid = kv_major
         ? dim3((unsigned)n_splits, (unsigned)(a.n_head_kv / NWV * n_hchunks), (unsigned)a.n_seq)
         : dim3((unsigned)((n_splits + NWV - 1) / NWV), (unsigned)(a.n_head_kv * n_hchunks), (unsigned)a.n_seq);
     if (grid.y > 65535 || grid.z > 65535) return hipErrorInvalidValue;
-    if (kt == kAtMin)
-      hipLaunchKernelGGL((paged_attn_mfma_kernel<HD, NWV, kAtMin>), grid, dim3(64 * NWV), 0, s, a.q, a.k_codes,
-                         a.k_scales, a.v_codes, a.v_scales, a.block_tables, a.ctx_lens, a.win_lo, a.win_hi,
-                         a.max_blocks_per_seq, log2_exact(a.block_size), a.n_head, a.n_head_kv,
-                         n_hchunks, split_len, n_splits, kv_major, part);
-    else
-      hipLaunchKernelGGL((paged_attn_mfma_kernel<HD, NWV, kAt>), grid, dim3(64 * NWV), 0, s, a.q, a.k_codes,
-                         a.k_scales, a.v_codes, a.v_scales, a.block_tables, a.ctx_lens, a.win_lo, a.win_hi,
-                         a.max_blocks_per_seq, log2_exact(a.block_size), a.n_head, a.n_head_kv,
-                         n_hchunks, split_len, n_splits, kv_major, part);
+    auto kern = kt == kAtMin ? paged_attn_mfma_kernel<HD, NWV, kAtMin, NEW> : paged_attn_mfma_kernel<HD, NWV, kAt, NEW>;
+    hipLaunchKernelGGL(kern, grid, dim3(64 * NWV), 0, s, a.q, a.k_codes, a.k_scales, a.v_codes, a.v_scales,
+                       a.block_tables, a.ctx_lens, a.win_lo, a.win_hi, a.max_blocks_per_seq, log2_exact(a.block_size),
+                       a.n_head, a.n_head_kv, n_hchunks, split_len, n_splits, kv_major, part, a.new_k, a.new_v,
+                       a.new_slot, const_cast<int8_t*>(a.k_codes), const_cast<float*>(a.k_scales),
+                       const_cast<int8_t*>(a.v_codes), const_cast<float*>(a.v_scales));
     return hipGetLastError();
+  };
+  auto go = [&](auto nwv_c, bool kv_major) {
+    return a.new_k ? launch(nwv_c, std::true_type{}, kv_major) : launch(nwv_c, std::false_type{}, kv_major);
   };
   hipError_t e0;
   if constexpr (HD < 256) {  // head_dim 256 fits one wave per SIMD only: 4 waves
@@ -774,7 +867,31 @@ hipError_t run_paged_mfma(const PagedAttnArgs& a, float* part, hipStream_t s) {
   return hipGetLastError();
 }
 
+hipError_t launch_paged_attn_append(const PagedAttnArgs& a, void* workspace, hipStream_t s) {
+  const int kv_dim = a.n_head_kv * a.head_dim;
+  const bool fused = paged_mfma_ok(a) && !a.win_lo && !a.win_hi && kv_dim % 64 == 0 && kv_dim <= 1024 &&
+                     a.head_dim <= 128 && ((uintptr_t)a.new_k & 15) == 0 && ((uintptr_t)a.new_v & 15) == 0;
+  if (!fused) {
+    hipError_t e = launch_paged_kv_append(a.new_k, a.new_v, a.new_slot, const_cast<int8_t*>(a.k_codes),
+                                          const_cast<float*>(a.k_scales), const_cast<int8_t*>(a.v_codes),
+                                          const_cast<float*>(a.v_scales), (size_t)a.n_seq, (size_t)kv_dim, s);
+    if (e != hipSuccess) return e;
+    PagedAttnArgs b = a;
+    b.new_k = b.new_v = nullptr;
+    b.new_slot = nullptr;
+    return launch_paged_attn(b, workspace, s);
+  }
+  float* part = static_cast<float*>(workspace);
+  switch (a.head_dim) {
+    case 64: return run_paged_mfma<64>(a, part, s);
+    case 128: return run_paged_mfma<128>(a, part, s);
+    case 256: return run_paged_mfma<256>(a, part, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 hipError_t launch_paged_attn(const PagedAttnArgs& a, void* workspace, hipStream_t s) {
+  if (a.new_k) return hipErrorInvalidValue;  // launch_paged_attn_append
   float* part = static_cast<float*>(workspace);
   if (paged_mfma_ok(a)) {
     switch (a.head_dim) {

@@ -922,3 +922,32 @@ int ssdq_dequantize_vectors_int8(ssdq_ctx* c, const int8_t* codes, const float* 
 }
 
 }  // extern "C"
+
+// The decode step's INT8 append and paged attention as one launch (plus the
+// combine) where the matrix-core kernel applies (launch_paged_attn_append):
+// the token at position ctx_lens[s] - 1 is the new one, quantized from new_k /
+// new_v rows and written to pool row new_slot[s].  Same arguments and checks
+// as ssdq_paged_kv_append_dev followed by ssdq_paged_attention_int8_dev.
+int ssdq::api_paged_attention_append(const float* q, int8_t* k_codes, float* k_scales, int8_t* v_codes, float* v_scales,
+                               const int32_t* block_tables, const int32_t* ctx_lens, const float* new_k,
+                               const float* new_v, const int32_t* new_slot, float* out, size_t n_seq, size_t n_head,
+                               size_t n_head_kv, size_t head_dim, size_t block_size, size_t max_blocks_per_seq,
+                               size_t max_ctx, hipStream_t s) {
+  const char* fn = "paged INT8 append + attention";
+  if (n_seq == 0 || n_head == 0) return ok();
+  if (!new_k || !new_v || !new_slot) return fail(SSDQ_ERR_INVALID_ARG, "%s: NULL pointer", fn);
+  ssdq::PagedAttnArgs a;
+  int rc = paged_attention_args(fn, q, k_codes, k_scales, v_codes, v_scales, block_tables, ctx_lens, out, n_seq,
+                                n_head, n_head_kv, head_dim, block_size, max_blocks_per_seq, max_ctx, &a);
+  if (rc != SSDQ_OK) return rc;
+  a.new_k = new_k;
+  a.new_v = new_v;
+  a.new_slot = new_slot;
+  const size_t wsb = ssdq::paged_attn_workspace_bytes(a, nullptr);
+  void* ws = nullptr;
+  hipError_t e = workspace_get(wsb, s, &ws);
+  if (e != hipSuccess) return hip_fail(e, "paged INT8 append + attention: workspace");
+  e = ssdq::launch_paged_attn_append(a, ws, s);
+  if (e != hipSuccess) return hip_fail(e, fn);
+  return ok();
+}

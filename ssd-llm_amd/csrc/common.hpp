@@ -136,6 +136,40 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Maximum over the wavefront with DPP only, returned in every lane.
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, dpp_mov<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_mov<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_mov<0x124>(v));  // row_ror:4
+  v = fmaxf(v, dpp_mov<0x128>(v));  // row_ror:8: every lane holds its row's maximum
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                   __builtin_bit_cast(int, v), __builtin_bit_cast(int, v), 0x142, 0xA, 0xF, false)));
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                   __builtin_bit_cast(int, v), __builtin_bit_cast(int, v), 0x143, 0xC, 0xF, false)));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+// INT8 code of one KV element (quantize_vectors_int8, src/ssd/block_swap.rs:36-60
+// = QuantizedVec::quantize, src/inference/quantized_kv_cache.rs:23-41):
+// clamp(round_half_away(v * inv), -127, 127), NaN -> 0 (Rust `as i8`), as a
+// byte.  inv = 127 / absmax of the row (0 for an all-zero row, which gives
+// codes 0); the row's scale is absmax / 127.
+__device__ __forceinline__ uint32_t kv_code_of(float v, float inv) {
+#pragma clang fp contract(off)
+  const float t = roundf(v * inv);  // round half away from zero
+  int c;
+  if (t != t) {
+    c = 0;
+  } else {
+    c = (int)fminf(fmaxf(t, -127.0f), 127.0f);
+  }
+  return (uint32_t)(c & 0xFF);
+}
+
+__device__ __forceinline__ uint32_t kv_pack4(float a, float b, float c, float d, float inv) {
+  return kv_code_of(a, inv) | (kv_code_of(b, inv) << 8) | (kv_code_of(c, inv) << 16) | (kv_code_of(d, inv) << 24);
+}
+
 // 6-bit scale s and min m of Q4_K sub-block sb from the 12 packed bytes, in the
 // reference's bit order (src/metal/compute.rs:724-731): for sb >= 4 the two bits
 // taken from sc[sb-4] / sc[sb] are the LOW bits.  sc1/sc2/sc3 are bytes 0-3,

@@ -22,20 +22,10 @@
 namespace ssdq {
 namespace {
 
-__device__ __forceinline__ uint32_t code_of(float v, float inv) {
-#pragma clang fp contract(off)
-  const float t = roundf(v * inv);  // round half away from zero
-  int c;
-  if (t != t) {
-    c = 0;  // Rust `as i8` maps NaN to 0
-  } else {
-    c = (int)fminf(fmaxf(t, -127.0f), 127.0f);
-  }
-  return (uint32_t)(c & 0xFF);
-}
+__device__ __forceinline__ uint32_t code_of(float v, float inv) { return kv_code_of(v, inv); }
 
 __device__ __forceinline__ uint32_t pack4(float a, float b, float c, float d, float inv) {
-  return code_of(a, inv) | (code_of(b, inv) << 8) | (code_of(c, inv) << 16) | (code_of(d, inv) << 24);
+  return kv_pack4(a, b, c, d, inv);
 }
 
 // Quantizes the row `in` (len floats, 16-byte aligned when len % 4 == 0) into
@@ -75,19 +65,6 @@ __device__ __forceinline__ void quantize_row(const float* __restrict__ in, int l
   const float inv = amax != 0.0f ? 127.0f / amax : 0.0f;
   for (int e = lane; e < len; e += 64) codes[e] = amax == 0.0f ? (int8_t)0 : (int8_t)code_of(in[e], inv);
   if (lane == 0) *scale = amax == 0.0f ? 0.0f : amax / 127.0f;
-}
-
-// Maximum over the wavefront with DPP only, returned in every lane.
-__device__ __forceinline__ float wave_max_dpp(float v) {
-  v = fmaxf(v, dpp_mov<0xB1>(v));   // quad_perm [1,0,3,2]
-  v = fmaxf(v, dpp_mov<0x4E>(v));   // quad_perm [2,3,0,1]
-  v = fmaxf(v, dpp_mov<0x124>(v));  // row_ror:4
-  v = fmaxf(v, dpp_mov<0x128>(v));  // row_ror:8: every lane holds its row's maximum
-  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-                   __builtin_bit_cast(int, v), __builtin_bit_cast(int, v), 0x142, 0xA, 0xF, false)));
-  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-                   __builtin_bit_cast(int, v), __builtin_bit_cast(int, v), 0x143, 0xC, 0xF, false)));
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
 // Rows of len <= NV*256 floats (len % 4 == 0, 16-byte aligned rows): each

@@ -137,10 +137,24 @@ struct PagedAttnArgs {
   // [max(win_lo[s], 0), min(win_hi[s], ctx_lens[s])); null means 0 / no bound.
   const int32_t* win_lo = nullptr;
   const int32_t* win_hi = nullptr;
+  // Optional new token of each sequence (a decode step's INT8 append folded
+  // into the attention launch; no window): the K / V rows new_k[s], new_v[s]
+  // (kv_dim floats each) are quantized in the kernel, bit-identical to
+  // ssdq_kv_quantize_rows_dev, written to pool row new_slot[s] (< 0: not
+  // written), and the token at position ctx_lens[s] - 1 is taken from those
+  // codes instead of being read from the pool.
+  const float* new_k = nullptr;
+  const float* new_v = nullptr;
+  const int32_t* new_slot = nullptr;
 };
 // Bytes of device workspace the split-KV attention needs for these shapes.
 size_t paged_attn_workspace_bytes(const PagedAttnArgs& a, int* n_splits_out);
 hipError_t launch_paged_attn(const PagedAttnArgs& a, void* workspace, hipStream_t stream);
+// The same with a.new_k / a.new_v / a.new_slot set: one launch (plus the
+// combine) where the matrix-core kernel applies (no window, head_dim <= 128,
+// kv_dim a multiple of 64 up to 1024, 16-byte aligned new rows); otherwise the
+// INT8 append kernel, then the attention.
+hipError_t launch_paged_attn_append(const PagedAttnArgs& a, void* workspace, hipStream_t stream);
 // Paged attention with its split partials in the library's static device
 // scratch (kNoAllocScratchBytes per device): allocates nothing.  *need gets the
 // scratch the call requires; hipErrorInvalidValue when that exceeds the maximum.
@@ -177,6 +191,11 @@ int api_fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)
 int api_hip_fail(hipError_t e, const char* what);
 int api_ok();
 hipError_t api_workspace(size_t bytes, hipStream_t stream, void** out, int slot);
+int api_paged_attention_append(const float* q, int8_t* k_codes, float* k_scales, int8_t* v_codes, float* v_scales,
+                               const int32_t* block_tables, const int32_t* ctx_lens, const float* new_k,
+                               const float* new_v, const int32_t* new_slot, float* out, size_t n_seq, size_t n_head,
+                               size_t n_head_kv, size_t head_dim, size_t block_size, size_t max_blocks_per_seq,
+                               size_t max_ctx, hipStream_t stream);
 // theta^(-2i/head_dim) with the C library's powf, as the reference computes them
 void api_rope_freqs(RopeFreq* r, int head_dim, float theta);
 

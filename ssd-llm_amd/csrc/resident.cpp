@@ -411,11 +411,10 @@ int ssdq_decode_layer_dev(const ssdq_weights* w, uint32_t layer, const ssdq_laye
                                           k, v, q_dim, kv_dim, n_embd, cfg->head_dim, position, cfg->rope_theta,
                                           stream)))
     return worst;
-  if (take(ssdq_paged_kv_append_dev(k, v, slot_mapping, k_codes, k_scales, v_codes, v_scales, 1, kv_dim, stream)))
-    return worst;
-  if (take(ssdq_paged_attention_int8_dev(q, k_codes, k_scales, v_codes, v_scales, block_table, ctx_len, att, 1,
-                                         cfg->n_head, cfg->n_head_kv, cfg->head_dim, block_size, max_blocks_per_seq,
-                                         max_ctx, stream)))
+  // append + attention: one launch (and the combine) on the matrix cores
+  if (take(ssdq::api_paged_attention_append(q, k_codes, k_scales, v_codes, v_scales, block_table, ctx_len, k, v,
+                                      slot_mapping, att, 1, cfg->n_head, cfg->n_head_kv, cfg->head_dim, block_size,
+                                      max_blocks_per_seq, max_ctx, s)))
     return worst;
   if (take(ssdq_matvec_dev(t_o->dtype, t_o->dev, att, ao, n_embd, q_dim, 1, stream))) return worst;
 

@@ -1755,12 +1755,12 @@ bool fast_aligned(const uint8_t* w, const float* x, int in_dim, int bpr) {
 }
 
 // Two units per lane keep two units' digit planes in registers: only Q6_K's
-// 36-dword records (72 VGPRs) fit beside the row buffers without spilling;
-// the 68- and 72-dword records of the other types (136-144 VGPRs) spill, and
-// scratch accesses would also break the exact wait counts of the kernels that
-// stream rows through LDS.
+// 40-dword records (80 VGPRs; 126-150 VGPRs per kernel) fit beside the row
+// buffers without spilling; the 72- and 80-dword records of the other types
+// (144-160 VGPRs) spill, and scratch accesses would also break the exact wait
+// counts of the kernels that stream rows through LDS.
 template <int F>
-constexpr bool kTwoUnits = Dig<F>::US <= 36;
+constexpr bool kTwoUnits = Dig<F>::US <= 40;
 
 // Row geometry of the batch-1 kernel: rows of up to 128 units run whole (one
 // wave per row stream); longer rows are cut into slices of at most 64 units.

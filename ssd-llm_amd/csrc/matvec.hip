@@ -1227,14 +1227,24 @@ constexpr int kB1rXW = 4;
 template <int F, int NCR, int D, int NRW>
 __global__ __launch_bounds__(64 * (kB1rXW + NRW)) void mv_b1r(const uint8_t* __restrict__ w,
                                                               const float* __restrict__ x, float* __restrict__ y,
-                                                              int out_dim, int row_bpr, int q, int rem, int rows_cap) {
+                                                              int out_dim, int row_bpr, int slice_bpr, int q, int rem,
+                                                              int rows_cap) {
   constexpr int US = Dig<F>::US, NW = FastUnit<F>::NW, SLOT = 1024 * NCR, SIT = 2;
   static_assert(NCR * (D - 1) < 64, "vmcnt range");
   extern __shared__ uint4 lds4[];
   uint32_t* lds = reinterpret_cast<uint32_t*>(lds4);
-  const int keff = row_bpr * Geom<F>::bs;  // at most 4096: 512 chunks of 8, two per x-wave thread
+  // K slice blockIdx.y of the rows (slice_bpr blocks; the whole row when
+  // gridDim.y == 1): a sliced row writes its partial sums as doubles to
+  // ((double*)y)[z * out_dim + row] (slice_reduce_kernel adds them in order)
+  const int blk0 = blockIdx.y * slice_bpr;
+  const int bpr = min(slice_bpr, row_bpr - blk0);
+  w += (size_t)blk0 * Geom<F>::bb;
+  x += (size_t)blk0 * Geom<F>::bs;
+  const bool sliced = gridDim.y > 1;
+  const int keff = bpr * Geom<F>::bs;  // at most 4096: 512 chunks of 8, two per x-wave thread
   const int U = keff / FastUnit<F>::E;
-  const int row_bytes = row_bpr * Geom<F>::bb;  // at most SLOT
+  const int nbytes = bpr * Geom<F>::bb;  // at most SLOT
+  const size_t row_bytes = (size_t)row_bpr * Geom<F>::bb;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   if (wave < kB1rXW) {
@@ -1261,7 +1271,7 @@ __global__ __launch_bounds__(64 * (kB1rXW + NRW)) void mv_b1r(const uint8_t* __r
 #pragma unroll
     for (int c = 0; c < NCR; c++) {
       const int o = 1024 * c + 16 * lane;
-      if (o < row_bytes || lane == 0) dma16_nt(rp + (o < row_bytes ? o : 0), wl_off + sl * SLOT + 1024 * c);
+      if (o < nbytes || lane == 0) dma16_nt(rp + (o < nbytes ? o : 0), wl_off + sl * SLOT + 1024 * c);
     }
   };
 #pragma unroll
@@ -1304,7 +1314,11 @@ __global__ __launch_bounds__(64 * (kB1rXW + NRW)) void mv_b1r(const uint8_t* __r
     }
   }
   wait_vmcnt<0>();  // the last copies land before the workgroup's LDS is released
-  for (int r = lane; r < nr; r += 64) y[wg_begin + rw + r * NRW] = (float)red[r];
+  double* yp = reinterpret_cast<double*>(y) + (size_t)blockIdx.y * out_dim;
+  for (int r = lane; r < nr; r += 64) {
+    if (sliced) yp[wg_begin + rw + r * NRW] = red[r];
+    else y[wg_begin + rw + r * NRW] = (float)red[r];
+  }
 }
 
 // Sums the K-slice partials (doubles, [slices][n]) in slice order and rounds
@@ -1907,6 +1921,7 @@ hipError_t run_b1r(const uint8_t* w, const float* x, float* y, int out_dim, int 
     const bool one = (long)out_dim >= 24L * cu && (long)out_dim <= 80L * cu;
     const int nrw = one ? 12 : 8, d = one ? 1 : 2;
     const int n_wg = cu, q = out_dim / n_wg, rem = out_dim % n_wg;
+    const int slice_bpr = bpr;
     const int rows_cap = (q + (rem ? 1 : 0) + nrw - 1) / nrw;
     const size_t lds = (size_t)U * Dig<F>::US * sizeof(uint32_t) + (size_t)nrw * d * 1024 * NCR +
                        (size_t)nrw * rows_cap * sizeof(double);
@@ -1914,8 +1929,48 @@ hipError_t run_b1r(const uint8_t* w, const float* x, float* y, int out_dim, int 
     auto go = [&](auto kern, int threads) {
       hipError_t e = set_lds_attr(kern, lds);
       if (e != hipSuccess) return e;
-      hipLaunchKernelGGL(kern, dim3((unsigned)n_wg), dim3((unsigned)threads), lds, s, w, x, y, out_dim, bpr, q, rem,
-                         rows_cap);
+      hipLaunchKernelGGL(kern, dim3((unsigned)n_wg), dim3((unsigned)threads), lds, s, w, x, y, out_dim, bpr, slice_bpr,
+                         q, rem, rows_cap);
+      return hipGetLastError();
+    };
+    return one ? go(mv_b1r<F, NCR, 1, 12>, 64 * (kB1rXW + 12)) : go(mv_b1r<F, NCR, 2, 8>, 64 * (kB1rXW + 8));
+  }
+}
+
+// Types whose K-sliced rows (slices of at most 2 KB) take mv_b1r.
+template <int F>
+constexpr bool kSliceSlots = F == kQ6_K || F == kQ4_K;
+
+// mv_b1r over K slices of slice_bpr blocks (partials as doubles in part,
+// [slice][row], for slice_reduce_kernel): one workgroup per CU and slice, each
+// owning a run of rows of its slice, 2 KB slots (slices start 16-byte aligned
+// in memory).  Rows per workgroup decide the wave layout as in run_b1r.
+// hipErrorNotSupported when the shape does not qualify.
+template <int F>
+hipError_t run_b1r_sliced(const uint8_t* w, const float* x, double* part, int out_dim, int row_bpr, int slice_bpr,
+                          int slices, hipStream_t s) {
+  if constexpr (!kSliceSlots<F>) {
+    return hipErrorNotSupported;
+  } else {
+    constexpr int NCR = 2;
+    const int keff = slice_bpr * Geom<F>::bs, U = keff / FastUnit<F>::E;
+    const size_t slice_bytes = (size_t)slice_bpr * Geom<F>::bb, row_bytes = (size_t)row_bpr * Geom<F>::bb;
+    if (slices < 2 || U > 64 || keff > 4096 || slice_bytes > (size_t)1024 * NCR) return hipErrorNotSupported;
+    if (((uintptr_t)w % 16) != 0 || row_bytes % 16 != 0 || slice_bytes % 16 != 0) return hipErrorNotSupported;
+    const int cu = device_cu_count();
+    const int n_wg = std::max(1, cu / slices), q = out_dim / n_wg, rem = out_dim % n_wg;
+    if (q < 8) return hipErrorNotSupported;
+    const bool one = q >= 24 && q <= 80;
+    const int nrw = one ? 12 : 8, d = one ? 1 : 2;
+    const int rows_cap = (q + (rem ? 1 : 0) + nrw - 1) / nrw;
+    const size_t lds = (size_t)U * Dig<F>::US * sizeof(uint32_t) + (size_t)nrw * d * 1024 * NCR +
+                       (size_t)nrw * rows_cap * sizeof(double);
+    if (lds > (size_t)lds_limit()) return hipErrorNotSupported;
+    auto go = [&](auto kern, int threads) {
+      hipError_t e = set_lds_attr(kern, lds);
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL(kern, dim3((unsigned)n_wg, (unsigned)slices), dim3((unsigned)threads), lds, s, w, x,
+                         reinterpret_cast<float*>(part), out_dim, row_bpr, slice_bpr, q, rem, rows_cap);
       return hipGetLastError();
     };
     return one ? go(mv_b1r<F, NCR, 1, 12>, 64 * (kB1rXW + 12)) : go(mv_b1r<F, NCR, 2, 8>, 64 * (kB1rXW + 8));
@@ -1952,6 +2007,15 @@ hipError_t b1_dispatch(const uint8_t* w, const float* x, float* y, int out_dim, 
   float* dst = p.slices > 1 ? ws : y;
   *used = true;
   hipError_t e;
+  if (p.slices > 1 && p.upl == 1) {  // K slices through LDS row slots
+    e = run_b1r_sliced<F>(w, x, reinterpret_cast<double*>(ws), out_dim, bpr, p.slice_bpr, p.slices, s);
+    if (e != hipErrorNotSupported) {
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL(slice_reduce_kernel, dim3((unsigned)((out_dim + 255) / 256)), dim3(256), 0, s,
+                         reinterpret_cast<const double*>(ws), acc ? acc : y, out_dim, p.slices, acc_in, y);
+      return hipGetLastError();
+    }
+  }
   // (Four waves sharing each row of 129-256 units, summed in LDS, avoid the
   // slices' partials and second launch, but every workgroup then stages the
   // whole x: 4096 x 14336 Q4_K took 15.6 us against 14.0 us sliced.)

@@ -443,7 +443,6 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void gemm_q4k_mfma(GEMM_MATS
     for (int j = 0; j < NT; j++) tot[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
   const uint32_t bias = opaque(0x64006400u);  // fp16 pair (1024, 1024), kept in a register
-  const uint32_t mkeep = lane < 32 ? 0xFFFFFFFFu : 0u;  // min-term B lanes that carry the mins
   // One MFMA step t (0-7) of a super-block, X from LDS stage buffer xs
   auto step = [&](auto t_c, const h8* xs, const SubScale (&s2)[NT][2], const u32x4a4 (&cd)[NT]) {
     constexpr int t = decltype(t_c)::value;
@@ -507,21 +506,54 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void gemm_q4k_mfma(GEMM_MATS
     step(std::integral_constant<int, 5>{}, xb, s2, cd1);
     step(std::integral_constant<int, 6>{}, xb, s2, cd1);
     step(std::integral_constant<int, 7>{}, xb, s2, cd1);
-    // min term: A = XS hi (lanes 0-15) / lo (16-31) / hi, lo again (32-63),
-    // B = the 8 mins m in lanes 0-31 and zeros in lanes 32-63, so only the
-    // hi + lo pair is summed.  A row's XS are finite unless the row is
-    // flagged, and a flagged row's MFMA results are never stored.
+    // Min term on the matrix cores, added to d*P by the MFMA itself:
+    //   v = d*P + sum over the 8 sub-blocks of XS * (-dmin*m),
+    // with A = XS hi (lanes 0-15) / lo (16-31) / hi, lo again (32-63) and B =
+    // the hi part of D = -dmin*m in lanes 0-31, its lo part in lanes 32-63, so
+    // the four products hi*hi, lo*hi, hi*lo, lo*lo fill the 32 k lanes.  D is
+    // exactly hi + lo in fp16: the product of an fp16 dmin and a 6-bit m has at
+    // most 17 significant bits, none below 2^-24, so the fma's remainder lo is
+    // exact, while |D| < 65504, that is |dmin| < 1024.  A column with a larger
+    // finite dmin (never seen in real weights) has D and d*P scaled by 2^-10
+    // (dmin >= 1024 keeps every bit of D at or above 2^-10, and |D| 2^-10 <
+    // 4096), and its running totals are scaled by 2^-10 before the update and
+    // by 2^10 after it: exact powers of two, so the update rounds as it would
+    // unscaled.  A row's XS are finite unless the row is flagged, and a
+    // flagged row's MFMA results are never stored.
     h8 bmin[NT];
-    float dd[NT], dm[NT];
+    float ds[NT];
+    bool wj[NT], wide = false;
 #pragma unroll
     for (int j = 0; j < NT; j++) {
       uint32_t mv[4];
-      bytes_to_f16(mlo[j] & mkeep, mv);
-      bytes_to_f16(mhi[j] & mkeep, mv + 2);
-      bmin[j] = __builtin_bit_cast(h8, u32x4{mv[0], mv[1], mv[2], mv[3]});
+      bytes_to_f16(mlo[j], mv);
+      bytes_to_f16(mhi[j], mv + 2);
+      const uint32_t dmb = dbits[j] >> 16;
+      wj[j] = (dmb & 0x7FFFu) >= 0x6400u && (dmb & 0x7C00u) != 0x7C00u;
+      wide |= wj[j];
+      // -dmin, times 2^-10 for a wide column (its exponent field is >= 25)
+      const h2 nd = __builtin_bit_cast(h2, ((wj[j] ? dmb - 0x2800u : dmb) ^ 0x8000u) * 0x10001u);
+      uint32_t dv[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const h2 m2 = __builtin_bit_cast(h2, mv[i]);
+        const h2 hi = m2 * nd;
+        const h2 lo = __builtin_elementwise_fma(m2, nd, -hi);
+        dv[i] = __builtin_bit_cast(uint32_t, lane < 32 ? hi : lo);
+      }
+      bmin[j] = __builtin_bit_cast(h8, u32x4{dv[0], dv[1], dv[2], dv[3]});
       // opaque: kept as f32 values, not folded into v_fma_mix_f32 (slower here)
-      dd[j] = __uint_as_float(opaque(__float_as_uint(f16_to_f32(dbits[j] & 0xFFFFu))));
-      dm[j] = __uint_as_float(opaque(__float_as_uint(f16_to_f32(dbits[j] >> 16))));
+      const float d = __uint_as_float(opaque(__float_as_uint(f16_to_f32(dbits[j] & 0xFFFFu))));
+      ds[j] = wj[j] ? d * 0x1p-10f : d;
+    }
+    const bool any_wide = __builtin_amdgcn_ballot_w64(wide) != 0;
+    if (any_wide) {
+#pragma unroll
+      for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int j = 0; j < NT; j++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) tot[mt][j][i] *= wj[j] ? 0x1p-10f : 1.0f;
     }
     const h8* sums = &xsl[b & 1][0];
 #pragma unroll
@@ -530,13 +562,21 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void gemm_q4k_mfma(GEMM_MATS
       const f4 rs = xel[b & 1][mt * 4 + c];  // 2^-sh of rows 4c .. 4c+3
 #pragma unroll
       for (int j = 0; j < NT; j++) {
-        const f4 qm = __builtin_amdgcn_mfma_f32_16x16x32_f16(amin, bmin[j], f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        f4 dp;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const float v = __builtin_fmaf(dd[j], acc[mt][j][i], -dm[j] * qm[i]);
-          tot[mt][j][i] = __builtin_fmaf(v, rs[i], tot[mt][j][i]);
-        }
+        for (int i = 0; i < 4; i++) dp[i] = ds[j] * acc[mt][j][i];
+        const f4 v = __builtin_amdgcn_mfma_f32_16x16x32_f16(amin, bmin[j], dp, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) tot[mt][j][i] = __builtin_fmaf(v[i], rs[i], tot[mt][j][i]);
       }
+    }
+    if (any_wide) {
+#pragma unroll
+      for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int j = 0; j < NT; j++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) tot[mt][j][i] *= wj[j] ? 1024.0f : 1.0f;
     }
   }
   // the last stage's loads (clamped repeats) land before the workgroup's LDS is released

@@ -142,6 +142,31 @@ def test_gemm_huge_and_nonfinite_rows(name, N, K):
         assert np.array_equal(y[r][fin].view(np.uint32), ref[r][fin].view(np.uint32)), f"row {r} not bit-exact"
 
 
+def test_gemm_wide_dmin():
+    """Super-blocks whose |dmin| is 1024 or more (|dmin * m| beyond fp16's
+    largest finite value) in some columns, beside ordinary columns of the same
+    waves: the matrix-core min term of those columns runs scaled by 2^-10 and
+    meets the same bar against the reference's serial fp32 chain."""
+    M, N, K = 192, 512, 2048
+    g = np.random.default_rng(4711)
+    w = synth.quant_weights(ssdq.Q4_K, N, K, 4712)
+    blk = w.reshape(N, K // 256, 144)
+    for n in g.choice(N, 40, replace=False):
+        sbs = g.choice(K // 256, 3, replace=False)
+        v = g.uniform(1024.0, 60000.0, 3) * g.choice([-1.0, 1.0], 3)
+        blk[n, sbs, 2:4] = v.astype(np.float16).view(np.uint8).reshape(-1, 2)
+    blk[7, 0, 2:4] = np.float16(1024.0).reshape(1).view(np.uint8)  # the boundary itself
+    blk[8, 1, 2:4] = np.float16(1023.5).reshape(1).view(np.uint8)  # just below it
+    xb = synth.f32_to_bf16_bits(synth.normal_f32((M, K), 4713))
+    announce("gemm wide dmin", M, N, K)
+    y, rc = gemm(w, xb, M, N, K)
+    assert rc == 0
+    ref = o.gemm_q4k_bf16(w, xb, M, N, K, threads=8)
+    exact = o.gemm_q4k_bf16(w, xb, M, N, K, threads=8, exact=True)
+    assert np.all(np.isfinite(ref))
+    assert_close_attributed(y, ref, exact, "gemm wide dmin")
+
+
 @pytest.mark.parametrize("M,N,K", [(1, 16, 256), (7, 33, 512), (100, 64, 1024), (513, 40, 256)])
 def test_gemm_ragged(M, N, K):
     w = synth.quant_weights(ssdq.Q4_K, N, K, M + N)

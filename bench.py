@@ -432,9 +432,9 @@ def decode_layer_case(torch, ssdq, synth, timer, ctx=4096):
     return {"us": round(per * 1e6, 2), "GB/s": round(nbytes / per / 1e9, 1),
             "pct_hbm_peak": round(100 * nbytes / per / 1e9 / HBM_PEAK_GBS, 2), "bytes": nbytes,
             "layers_rotated": n, "context": ctx, "hidden_finite": ok,
-            "note": "ssdq_decode_layer_dev: 9 steps in 8 kernel launches (the two RMSNorms folded into the QKV and "
-                    "SwiGLU launches, the residual add into the down projection's slice reduction), one HIP graph "
-                    "replay per 50 layers"}
+            "note": "ssdq_decode_layer_dev: 9 steps in 7 kernel launches (the two RMSNorms folded into the QKV and "
+                    "SwiGLU launches, the token's INT8 append into the attention launch, the residual add into "
+                    "the down projection's slice reduction), one HIP graph replay per 50 layers"}
 
 
 def attention_case(torch, ssdq, synth, codes, scales):

@@ -415,7 +415,10 @@ size_t ssdq_decode_layer_scratch_bytes(const ssdq_layer_config* cfg, size_t* off
  * attention above for one sequence (block_table: max_blocks_per_seq entries;
  * slot_mapping and ctx_len: one int32 each, in device memory). scratch: NULL
  * for the library's per-stream workspace, or a 256-byte aligned buffer of
- * ssdq_decode_layer_scratch_bytes(cfg) bytes. Shapes of every tensor are
+ * ssdq_decode_layer_scratch_bytes(cfg) bytes; it holds the step outputs
+ * listed above. The attention's split partials and the down projection's
+ * K-slice partials still come from the per-stream workspace (see
+ * ssdq_reserve_workspace), as in the separate entry points. Shapes of every tensor are
  * checked before anything is launched. Status: the worst of the steps
  * (SSDQ_WARN_UNSUPPORTED_ZEROED when a projection's type is unsupported and
  * its output was zero-filled, as the reference's matvec does). */

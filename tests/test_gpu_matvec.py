@@ -286,15 +286,20 @@ def test_batch1_long_rows(dtype, out_dim, in_dim):
 
 
 K_SLICED = [  # K-sliced rows: slice partials in the workspace, summed in slice order
-    (Q4_K, 28672, 8192),   # row streams, 2 slices
-    (Q4_K, 4096, 14336),   # row streams, 4 slices, partial last slice
-    (Q6_K, 4096, 14336),   # batch-1 kernel, 7 slices
+    (Q4_K, 28672, 8192),   # LDS row streams, 2 slices of 2304 bytes (too long for a row slot)
+    (Q4_K, 4096, 14336),   # LDS row slots, 4 slices of 14 blocks, 64-row runs (12 row waves)
+    (Q6_K, 4096, 14336),   # LDS row slots, 7 slices of 8 blocks, 113-row runs (8 row waves, two slots)
     (Q8_0, 4096, 28672),   # batch-1 kernel, 7 slices, interleaved row streams
     (Q4_0, 2000, 28800),   # 8 slices, partial last slice
     (Q6_K, 33, 14336),     # fewer rows than row streams
     (Q6_K, 128256, 4096),  # output-head shape: whole-row LDS streams (128 units per row), no slices
-    (Q6_K, 20000, 8192),   # LDS row streams, 4 slices of 8 blocks (Q6_K head of an 8192-wide model)
-    (Q4_K, 40000, 8704),   # LDS row streams, 3 slices of 12, 12 and 10 blocks (short last slice)
+    (Q6_K, 20000, 8192),   # LDS row slots, 4 slices of 8 blocks (Q6_K head of an 8192-wide model)
+    (Q4_K, 40000, 8704),   # LDS row slots, 3 slices of 12, 12 and 10 blocks (short last slice)
+    # the row-slot K slices around their wave layouts (256 CUs, 4 slices: 64 runs)
+    (Q4_K, 1030, 14336),   # 16-17 rows per run (ragged shares), two slots per wave
+    (Q4_K, 5000, 14336),   # 78-79 rows per run, 12 row waves with one slot
+    (Q4_K, 5200, 14336),   # 81-82 rows per run, 8 row waves with two slots
+    (Q6_K, 9000, 14336),   # 250 rows per run (7 slices, 36 runs), clamped repeats after the last row
 ]
 
 

@@ -167,7 +167,8 @@ def test_gemm_wide_dmin():
     assert_close_attributed(y, ref, exact, "gemm wide dmin")
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 16, 256), (7, 33, 512), (100, 64, 1024), (513, 40, 256)])
+@pytest.mark.parametrize("M,N,K", [(1, 16, 256), (7, 33, 512), (100, 64, 1024), (513, 40, 256),
+                                   (512, 1024, 5376)])  # 8 K splits of 2-3 super-blocks (odd and even)
 def test_gemm_ragged(M, N, K):
     w = synth.quant_weights(ssdq.Q4_K, N, K, M + N)
     xb = synth.f32_to_bf16_bits(synth.normal_f32((M, K), K))

@@ -392,6 +392,14 @@ __host__ __device__ constexpr size_t ext_lds_bytes(int G) {
   return (size_t)B * G * (kGS + 2) * sizeof(float) + tab_bytes<F>;
 }
 
+// Types whose groups are requested two at a time per lane (see mv_ext).
+// Measured at 14336 x 4096, batch 1, 8 workgroups per CU: IQ2_XXS 15.3 -> 14.7
+// us, IQ2_XS 16.6 -> 15.8, IQ3_XXS 16.0 -> 14.8, IQ3_S 17.3 -> 16.6, IQ4_NL 12.7
+// -> 12.3, F16 23.8 -> 22.4; IQ4_XS (12.4 -> 14.6) and BF16 (21.8 -> 22.4) keep
+// one group at a time.
+template <int F>
+constexpr bool kPairGroups = F != kIQ4_XS && F != kBF16;
+
 template <int F, int B, int R>
 __global__ __launch_bounds__(256) void mv_ext(const uint8_t* __restrict__ w, const float* __restrict__ x,
                                               float* __restrict__ y, int out_dim, int in_dim, int G,
@@ -430,30 +438,72 @@ __global__ __launch_bounds__(256) void mv_ext(const uint8_t* __restrict__ w, con
     for (int rr = 0; rr < R; rr++)
 #pragma unroll
       for (int b = 0; b < B; b++) acc[rr][b] = 0.f;
-    for (int g = lane; g < G; g += 64) {
-      uint32_t raw[R][NW];
+    // (the two forms below are written out separately: sharing the group body
+    // through a lambda cost the paired form 14-18 VGPRs and a wave per SIMD)
+    if constexpr (kPairGroups<F>) {
+      // groups g and g + 64 of every row are requested together before either
+      // is decoded (the second clamped to the row's last group, and not summed,
+      // past the end), so a wave keeps twice the loads in flight
+      for (int g0 = lane; g0 < G; g0 += 128) {
+        uint32_t raw[2][R][NW];
 #pragma unroll
-      for (int rr = 0; rr < R; rr++) {
-        const int row = min(r0 + rr, r_end - 1);
-        load_group<F>(w + (size_t)row * row_bytes, g, raw[rr]);
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+          for (int rr = 0; rr < R; rr++) {
+            const int row = min(r0 + rr, r_end - 1);
+            load_group<F>(w + (size_t)row * row_bytes, min(g0 + 64 * h, G - 1), raw[h][rr]);
+          }
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          const int g = min(g0 + 64 * h, G - 1);
+          const bool live = g0 + 64 * h < G;
+#pragma unroll
+          for (int rr = 0; rr < R; rr++) {
+            float u[32], S[2], O[2];
+            decode_group<F>(raw[h][rr], g, u, S, O, tab);
+#pragma unroll
+            for (int b = 0; b < B; b++) {
+              const float* xg = xs + ((size_t)b * G + g) * kGS;
+              float pa = 0.f, pb = 0.f;
+#pragma unroll
+              for (int e = 0; e < 16; e++) pa = fmaf(u[e], xg[e], pa);
+#pragma unroll
+              for (int e = 16; e < 32; e++) pb = fmaf(u[e], xg[e], pb);
+              const float* sg = xsum + ((size_t)b * G + g) * 2;
+              float a = fmaf(-O[0], sg[0], acc[rr][b]);
+              a = fmaf(-O[1], sg[1], a);
+              a = fmaf(S[0], pa, a);
+              acc[rr][b] = live ? fmaf(S[1], pb, a) : acc[rr][b];
+            }
+          }
+        }
       }
+    } else {
+      for (int g = lane; g < G; g += 64) {
+        uint32_t raw[R][NW];
 #pragma unroll
-      for (int rr = 0; rr < R; rr++) {
-        float u[32], S[2], O[2];
-        decode_group<F>(raw[rr], g, u, S, O, tab);
+        for (int rr = 0; rr < R; rr++) {
+          const int row = min(r0 + rr, r_end - 1);
+          load_group<F>(w + (size_t)row * row_bytes, g, raw[rr]);
+        }
 #pragma unroll
-        for (int b = 0; b < B; b++) {
-          const float* xg = xs + ((size_t)b * G + g) * kGS;
-          float pa = 0.f, pb = 0.f;
+        for (int rr = 0; rr < R; rr++) {
+          float u[32], S[2], O[2];
+          decode_group<F>(raw[rr], g, u, S, O, tab);
 #pragma unroll
-          for (int e = 0; e < 16; e++) pa = fmaf(u[e], xg[e], pa);
+          for (int b = 0; b < B; b++) {
+            const float* xg = xs + ((size_t)b * G + g) * kGS;
+            float pa = 0.f, pb = 0.f;
 #pragma unroll
-          for (int e = 16; e < 32; e++) pb = fmaf(u[e], xg[e], pb);
-          const float* sg = xsum + ((size_t)b * G + g) * 2;
-          float a = fmaf(-O[0], sg[0], acc[rr][b]);
-          a = fmaf(-O[1], sg[1], a);
-          a = fmaf(S[0], pa, a);
-          acc[rr][b] = fmaf(S[1], pb, a);
+            for (int e = 0; e < 16; e++) pa = fmaf(u[e], xg[e], pa);
+#pragma unroll
+            for (int e = 16; e < 32; e++) pb = fmaf(u[e], xg[e], pb);
+            const float* sg = xsum + ((size_t)b * G + g) * 2;
+            float a = fmaf(-O[0], sg[0], acc[rr][b]);
+            a = fmaf(-O[1], sg[1], a);
+            a = fmaf(S[0], pa, a);
+            acc[rr][b] = fmaf(S[1], pb, a);
+          }
         }
       }
     }
@@ -602,8 +652,12 @@ hipError_t run_ext(const uint8_t* w, const float* x, float* y, int out_dim, int 
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
   }
-  // about two workgroups per CU, rows in multiples of 4R
-  const int target = 2 * device_cu_count();
+  // about eight workgroups per CU, rows in multiples of 4R.  Each wave walks
+  // its groups one load-and-decode at a time, so the waves in flight carry the
+  // latency: with two workgroups per CU (and four rows per wave at batch 1)
+  // 14336 x 4096 took IQ4_NL 15.4 -> 12.7 us, IQ4_XS 15.3 -> 12.3, BF16 25.2 ->
+  // 21.7, IQ2_XXS 17.4 -> 15.2, IQ3_S 18.9 -> 17.2, F16 24.7 -> 23.8.
+  const int target = 8 * device_cu_count();
   const int q = 4 * R;
   int n = std::max(1, std::min((out_dim + q - 1) / q, target));
   int rows = (out_dim + n - 1) / n;
@@ -634,7 +688,7 @@ hipError_t ext_fast(const uint8_t* w, const float* x, float* y, int out_dim, int
       case 8: e = run_ext<F, 8, 1>(w, xb, yb, out_dim, in_dim, G, row_bytes, ext_lds_bytes<F, 8>(G), s); break;
       case 4: e = run_ext<F, 4, 1>(w, xb, yb, out_dim, in_dim, G, row_bytes, ext_lds_bytes<F, 4>(G), s); break;
       case 2: e = run_ext<F, 2, 2>(w, xb, yb, out_dim, in_dim, G, row_bytes, ext_lds_bytes<F, 2>(G), s); break;
-      default: e = run_ext<F, 1, 4>(w, xb, yb, out_dim, in_dim, G, row_bytes, ext_lds_bytes<F, 1>(G), s); break;
+      default: e = run_ext<F, 1, 2>(w, xb, yb, out_dim, in_dim, G, row_bytes, ext_lds_bytes<F, 1>(G), s); break;
     }
     if (e != hipSuccess) return e;
     b0 += take;

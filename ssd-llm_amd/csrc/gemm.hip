@@ -435,6 +435,9 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void gemm_q4k_mfma(GEMM_MATS
     WRegs hdr, cd0, cd1;
   };
   WSet wa, wb;  // ping-pong: super-block b computes from one set and loads b + 1 into the other
+  // fetch_first issues exactly two 16-byte loads per column (2 NT) and
+  // fetch_second one (NT): the stage waits publish_stage<NT> and <2 NT> below
+  // count them, so a change here must change those waits
   auto wptr = [&](int j, int b) { return wrow[j] + (size_t)(b_begin + min(b, nb - 1)) * 144; };
   auto fetch_first = [&](int b, WSet& w) {
 #pragma unroll

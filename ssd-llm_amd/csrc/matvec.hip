@@ -1941,6 +1941,10 @@ hipError_t run_b1r(const uint8_t* w, const float* x, float* y, int out_dim, int 
 template <int F>
 constexpr bool kSliceSlots = F == kQ6_K || F == kQ4_K;
 
+template <int F, int NCR>
+hipError_t run_b1r_sliced_ncr(const uint8_t* w, const float* x, double* part, int out_dim, int row_bpr,
+                              int slice_bpr, int slices, hipStream_t s);
+
 // mv_b1r over K slices of slice_bpr blocks (partials as doubles in part,
 // [slice][row], for slice_reduce_kernel): one workgroup per CU and slice, each
 // owning a run of rows of its slice, 2 KB slots (slices start 16-byte aligned
@@ -1952,7 +1956,16 @@ hipError_t run_b1r_sliced(const uint8_t* w, const float* x, double* part, int ou
   if constexpr (!kSliceSlots<F>) {
     return hipErrorNotSupported;
   } else {
-    constexpr int NCR = 2;
+    const size_t slice_bytes = (size_t)slice_bpr * Geom<F>::bb;
+    if (slice_bytes > 2048) return run_b1r_sliced_ncr<F, 3>(w, x, part, out_dim, row_bpr, slice_bpr, slices, s);
+    return run_b1r_sliced_ncr<F, 2>(w, x, part, out_dim, row_bpr, slice_bpr, slices, s);
+  }
+}
+
+template <int F, int NCR>
+hipError_t run_b1r_sliced_ncr(const uint8_t* w, const float* x, double* part, int out_dim, int row_bpr,
+                              int slice_bpr, int slices, hipStream_t s) {
+  {
     const int keff = slice_bpr * Geom<F>::bs, U = keff / FastUnit<F>::E;
     const size_t slice_bytes = (size_t)slice_bpr * Geom<F>::bb, row_bytes = (size_t)row_bpr * Geom<F>::bb;
     if (slices < 2 || U > 64 || keff > 4096 || slice_bytes > (size_t)1024 * NCR) return hipErrorNotSupported;

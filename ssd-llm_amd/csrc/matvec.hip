@@ -1947,8 +1947,10 @@ hipError_t run_b1r_sliced_ncr(const uint8_t* w, const float* x, double* part, in
 
 // mv_b1r over K slices of slice_bpr blocks (partials as doubles in part,
 // [slice][row], for slice_reduce_kernel): one workgroup per CU and slice, each
-// owning a run of rows of its slice, 2 KB slots (slices start 16-byte aligned
-// in memory).  Rows per workgroup decide the wave layout as in run_b1r.
+// owning a run of rows of its slice, 2 KB slots, or 3 KB for slices of up to
+// 3 KB (slices start 16-byte aligned in memory; 28672 x 8192 Q4_K, two slices
+// of 2304 bytes: 27.6 us on the LDS row streams of mv_b1s_lds, 26.9 us here).
+// Rows per workgroup decide the wave layout as in run_b1r.
 // hipErrorNotSupported when the shape does not qualify.
 template <int F>
 hipError_t run_b1r_sliced(const uint8_t* w, const float* x, double* part, int out_dim, int row_bpr, int slice_bpr,

@@ -286,7 +286,7 @@ def test_batch1_long_rows(dtype, out_dim, in_dim):
 
 
 K_SLICED = [  # K-sliced rows: slice partials in the workspace, summed in slice order
-    (Q4_K, 28672, 8192),   # LDS row streams, 2 slices of 2304 bytes (too long for a row slot)
+    (Q4_K, 28672, 8192),   # LDS row slots of 3 KB, 2 slices of 2304 bytes
     (Q4_K, 4096, 14336),   # LDS row slots, 4 slices of 14 blocks, 64-row runs (12 row waves)
     (Q6_K, 4096, 14336),   # LDS row slots, 7 slices of 8 blocks, 113-row runs (8 row waves, two slots)
     (Q8_0, 4096, 28672),   # batch-1 kernel, 7 slices, interleaved row streams

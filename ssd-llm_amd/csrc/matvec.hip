@@ -716,13 +716,12 @@ template <int RMAX> constexpr int kB1Depth = RMAX < 2 ? RMAX : 2;
 
 // RMSNorm of the staged x (the norm-fused decode-layer launches): h = x (+ the
 // residual), x' = h * inv_rms * w with inv_rms = 1 / sqrt(mean(h^2) + eps),
-// the sum of squares reduced over the workgroup (each workgroup computes the
-// same value: the same data in the same order).  Workgroup 0 writes h and x'.
+// the sum of squares reduced over the staging threads (each workgroup computes
+// the same value: the same data in the same order).  Workgroup 0 writes h and
+// x'.  norm_sumsq forms h in place and returns the thread's sum of squares;
+// norm_apply scales by inv_rms and the norm weights.
 template <int SIT, bool RES>
-__device__ __forceinline__ void stage_norm(XChunks<SIT>& st, const XChunks<SIT>& st_r, const XChunks<SIT>& st_w,
-                                           int keff, const MatvecFuse& fu) {
-  __shared__ float part[16];
-  const int nchunk = keff >> 3;
+__device__ __forceinline__ float norm_sumsq(XChunks<SIT>& st, const XChunks<SIT>& st_r) {
   float q = 0.f;
 #pragma unroll
   for (int it = 0; it < SIT; it++)
@@ -731,16 +730,16 @@ __device__ __forceinline__ void stage_norm(XChunks<SIT>& st, const XChunks<SIT>&
       if (RES) st.v[it][j] = st.v[it][j] + st_r.v[it][j];
       q = fmaf(st.v[it][j], st.v[it][j], q);  // chunks past the end are zeros
     }
-  q = wave_sum(q);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  if (lane == 0) part[wave] = q;
-  __syncthreads();
-  float t = 0.f;
-  for (int i = 0; i < nw; i++) t += part[i];
-  const float inv = 1.0f / sqrtf(t / (float)keff + fu.norm_eps);
+  return q;
+}
+
+template <int SIT>
+__device__ __forceinline__ void norm_apply(XChunks<SIT>& st, const XChunks<SIT>& st_w, float inv, int keff,
+                                           int nthreads, const MatvecFuse& fu) {
+  const int nchunk = keff >> 3;
 #pragma unroll
   for (int it = 0; it < SIT; it++) {
-    const int c = it * (int)blockDim.x + (int)threadIdx.x;
+    const int c = it * nthreads + (int)threadIdx.x;
     const bool live = c < nchunk;
     float h[8];
 #pragma unroll
@@ -760,6 +759,20 @@ __device__ __forceinline__ void stage_norm(XChunks<SIT>& st, const XChunks<SIT>&
       }
     }
   }
+}
+
+// The norm over every thread of the workgroup (mv_b1: all waves stage x).
+template <int SIT, bool RES>
+__device__ __forceinline__ void stage_norm(XChunks<SIT>& st, const XChunks<SIT>& st_r, const XChunks<SIT>& st_w,
+                                           int keff, const MatvecFuse& fu) {
+  __shared__ float part[16];
+  const float q = wave_sum(norm_sumsq<SIT, RES>(st, st_r));
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  if (lane == 0) part[wave] = q;
+  __syncthreads();
+  float t = 0.f;
+  for (int i = 0; i < nw; i++) t += part[i];
+  norm_apply<SIT>(st, st_w, 1.0f / sqrtf(t / (float)keff + fu.norm_eps), keff, (int)blockDim.x, fu);
 }
 
 // Decode-layer fusion of the batch-1 kernel (FUSE = true).  Up to three
@@ -783,6 +796,30 @@ __device__ __forceinline__ int fuse_seg(const MatvecFuse& f, int v, int& r) {
   const int sg = (v >= f.start1 ? 1 : 0) + (v >= f.start2 ? 1 : 0);
   r = v - (sg == 0 ? 0 : sg == 1 ? f.start1 : f.start2);
   return sg;
+}
+
+// Epilogue of the row pair at virtual rows v, v + 1 with dot products a0, a1:
+// silu(gate) * up, or the two outputs, rotated when their segment is in
+// rope_mask (rows r, r + 1 are pair i of a head).
+__device__ __forceinline__ void fuse_store_pair(const MatvecFuse& fu, int v, float a0, float a1) {
+  int r;
+  const int sg = fuse_seg(fu, v, r);
+  if (fu.swiglu) {
+    fu.y0[r] = (a0 / (1.0f + expf(-a0))) * a1;
+    return;
+  }
+  float o0 = a0, o1 = a1;
+  if ((fu.rope_mask >> sg) & 1u) {
+    const int i = (r % fu.head_dim) >> 1;
+    const float ang = (float)fu.position * fu.freq.f[i];
+    // sin / cos of the fp32 angle, rounded once from double
+    const float sn = (float)sin((double)ang), cs = (float)cos((double)ang);
+    o0 = a0 * cs - a1 * sn;
+    o1 = a0 * sn + a1 * cs;
+  }
+  float* yo = sg == 0 ? fu.y0 : sg == 1 ? fu.y1 : fu.y2;
+  yo[r] = o0;
+  yo[r + 1] = o1;
 }
 
 // Every lane keeps the digit planes of its units in registers.  KS waves split
@@ -936,29 +973,8 @@ __global__ __launch_bounds__(768) void mv_b1(const uint8_t* __restrict__ w,
   if constexpr (FUSE >= 2) {
     if (lane == 63) {
 #pragma unroll
-      for (int rr = 0; rr < RMAX; rr += 2) {
-        if (rr < n_rows) {
-          const float a0 = (float)acc[rr], a1 = (float)acc[rr + 1];
-          int r;
-          const int sg = fuse_seg(fu, r_begin + rr, r);
-          if (fu.swiglu) {
-            fu.y0[r] = (a0 / (1.0f + expf(-a0))) * a1;  // silu(gate) * up
-          } else {
-            float o0 = a0, o1 = a1;
-            if ((fu.rope_mask >> sg) & 1u) {  // rows r, r+1: pair i of a head
-              const int i = (r % fu.head_dim) >> 1;
-              const float ang = (float)fu.position * fu.freq.f[i];
-              // sin / cos of the fp32 angle, rounded once from double
-              const float sn = (float)sin((double)ang), cs = (float)cos((double)ang);
-              o0 = a0 * cs - a1 * sn;
-              o1 = a0 * sn + a1 * cs;
-            }
-            float* yo = sg == 0 ? fu.y0 : sg == 1 ? fu.y1 : fu.y2;
-            yo[r] = o0;
-            yo[r + 1] = o1;
-          }
-        }
-      }
+      for (int rr = 0; rr < RMAX; rr += 2)
+        if (rr < n_rows) fuse_store_pair(fu, r_begin + rr, (float)acc[rr], (float)acc[rr + 1]);
     }
     return;
   }
@@ -1217,18 +1233,23 @@ __global__ __launch_bounds__(768) void mv_b1s_lds(const uint8_t* __restrict__ w,
 //      the copies of row r + D as soon as the slot's LDS reads are done.  Row
 //      sums go to LDS and are stored after the loop.
 // Measured (kernel alone, graph replays): 14336 x 4096 Q4_K 8.45 -> 7.99 us
-// (D 1, 12 row waves), 28672 x 4096 14.3 -> 12.5 us and 4096 x 4096 4.81 ->
-// 4.56 us (D 2, 8 row waves); 1024 rows (4 per CU) stay on mv_b1 (3.6 against
-// 3.9 us).  Slots of one whole row each beat a contiguous 1 KB ring of the
+// (D 1, 12 row waves), 4096 x 4096 4.81 -> 4.56 us (D 2, 8 row waves); 1024
+// rows (4 per CU) stay on mv_b1 (3.6 against 3.9 us).  Slots of one whole row each beat a contiguous 1 KB ring of the
 // wave's run (8.2-8.8 us) and requesting every row of the run at the start
 // (10.4 us: the copies stall at issue and the stream slows).
 constexpr int kB1rXW = 4;
 
-template <int F, int NCR, int D, int NRW>
-__global__ __launch_bounds__(64 * (kB1rXW + NRW)) void mv_b1r(const uint8_t* __restrict__ w,
-                                                              const float* __restrict__ x, float* __restrict__ y,
-                                                              int out_dim, int row_bpr, int slice_bpr, int q, int rem,
-                                                              int rows_cap) {
+// The body of mv_b1r and of its decode-layer fusion mv_b1r_fused (FUSE as in
+// mv_b1: 2 row pairs with the RoPE / SwiGLU epilogue, 3 and 4 the same with an
+// RMSNorm of x, 4 of x + a residual).  Fused, the workgroup's units are row
+// pairs (out_dim virtual rows, q and rem count pairs): row wave v takes pairs
+// v, v + NRW, ... and copies both rows of each, so it holds both dot products
+// of its pairs for the epilogue.  With the norm, the x waves also load the
+// residual and the norm weights before the first barrier.
+template <int F, int NCR, int D, int NRW, int FUSE>
+__device__ __forceinline__ void b1r_body(const uint8_t* __restrict__ w, const float* __restrict__ x,
+                                         float* __restrict__ y, int out_dim, int row_bpr, int slice_bpr, int q,
+                                         int rem, int rows_cap, const FuseArg<FUSE>& fu) {
   constexpr int US = Dig<F>::US, NW = FastUnit<F>::NW, SLOT = 1024 * NCR, SIT = 2;
   static_assert(NCR * (D - 1) < 64, "vmcnt range");
   extern __shared__ uint4 lds4[];
@@ -1247,10 +1268,73 @@ __global__ __launch_bounds__(64 * (kB1rXW + NRW)) void mv_b1r(const uint8_t* __r
   const size_t row_bytes = (size_t)row_bpr * Geom<F>::bb;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  uint8_t* const slots = reinterpret_cast<uint8_t*>(lds4) + (size_t)U * US * sizeof(uint32_t);
+  double* const red_all = reinterpret_cast<double*>(slots + (size_t)NRW * D * SLOT);
+  // norm-fused: the x waves' sums of squares and staging exponents, after the
+  // row sums of every row wave
+  [[maybe_unused]] float* const part = reinterpret_cast<float*>(red_all + (size_t)NRW * rows_cap);
   if (wave < kB1rXW) {
     XChunks<SIT> st;
     stage_load<SIT>(x, keff, st, 64 * kB1rXW);
+    [[maybe_unused]] XChunks<SIT> st_r, st_w;
+    if constexpr (FUSE >= 3) {
+      if constexpr (FUSE == 4) stage_load<SIT>(fu.norm_res, keff, st_r, 64 * kB1rXW);
+      stage_load<SIT>(fu.norm_w, keff, st_w, 64 * kB1rXW);
+    }
     __builtin_amdgcn_s_barrier();  // 1.
+    if constexpr (FUSE >= 3) {
+      // Every output is linear in x' = h inv_rms w, so the x waves stage h w
+      // at once and the row waves multiply their dot products by inv_rms,
+      // which needs the sums of squares of all x waves only after the loop.
+      // Where a product of finite h and w overflows fp32 (for x' itself finite
+      // or, the sum of squares overflowing, zero), the wave stages h w 2^-k
+      // instead (k from its largest product, rounded once from double), and
+      // the row waves scale the partial sums of its units by 2^k.
+      const float qs = wave_sum(norm_sumsq<SIT, FUSE == 4>(st, st_r));  // st is h from here
+      XChunks<SIT> hw;
+      bool ovf = false;
+#pragma unroll
+      for (int it = 0; it < SIT; it++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          const float h = st.v[it][j], g = st_w.v[it][j];
+          hw.v[it][j] = h * g;
+          ovf |= isinf(hw.v[it][j]) && isfinite(h) && isfinite(g);
+        }
+      int k = 0;
+      if (__any(ovf)) {
+        float e = -1000.f;  // bound on the exponent of every finite product
+#pragma unroll
+        for (int it = 0; it < SIT; it++)
+#pragma unroll
+          for (int j = 0; j < 8; j++) {
+            const float h = st.v[it][j], g = st_w.v[it][j];
+            if (isfinite(h) && isfinite(g) && h != 0.f && g != 0.f) e = fmaxf(e, (float)(ilogbf(h) + ilogbf(g) + 2));
+          }
+        k = max(0, (int)wave_max(e) - 127);
+        const double sc = ldexp(1.0, -k);
+#pragma unroll
+        for (int it = 0; it < SIT; it++)
+#pragma unroll
+          for (int j = 0; j < 8; j++) {
+            const float h = st.v[it][j], g = st_w.v[it][j];
+            if (isfinite(h) && isfinite(g)) hw.v[it][j] = (float)((double)h * (double)g * sc);
+          }
+      }
+      if (lane == 0) {
+        part[wave] = qs;
+        reinterpret_cast<int*>(part)[kB1rXW + wave] = k;
+      }
+      stage_store<F, SIT>(hw, keff, lds, 64 * kB1rXW);
+      lds_barrier();  // 2.
+      if (blockIdx.x == 0) {  // h and x' to the step outputs
+        float t = 0.f;
+#pragma unroll
+        for (int i = 0; i < kB1rXW; i++) t += part[i];
+        norm_apply<SIT>(st, st_w, 1.0f / sqrtf(t / (float)keff + fu.norm_eps), keff, 64 * kB1rXW, fu);
+      }
+      return;
+    }
     stage_store<F, SIT>(st, keff, lds, 64 * kB1rXW);
     lds_barrier();  // 2.
     return;
@@ -1258,16 +1342,34 @@ __global__ __launch_bounds__(64 * (kB1rXW + NRW)) void mv_b1r(const uint8_t* __r
   __builtin_amdgcn_s_barrier();  // 1.
   const int rw = wave - kB1rXW;
   const int b = (int)blockIdx.x;
-  const int wg_begin = b * q + min(b, rem), wg_rows = q + (b < rem ? 1 : 0);
-  const int nr = wg_rows > rw ? (wg_rows - 1 - rw) / NRW + 1 : 0;  // <= rows_cap
-  uint8_t* wl = reinterpret_cast<uint8_t*>(lds4) + (size_t)U * US * sizeof(uint32_t) + (size_t)rw * D * SLOT;
-  double* red = reinterpret_cast<double*>(reinterpret_cast<uint8_t*>(lds4) + (size_t)U * US * sizeof(uint32_t) +
-                                          (size_t)NRW * D * SLOT) +
-                (size_t)rw * rows_cap;
+  constexpr int UR = FUSE != 0 ? 2 : 1;  // rows per unit of work
+  const int wg_begin = b * q + min(b, rem), wg_units = q + (b < rem ? 1 : 0);
+  const int nu = wg_units > rw ? (wg_units - 1 - rw) / NRW + 1 : 0;
+  const int nr = UR * nu;  // <= rows_cap
+  uint8_t* wl = slots + (size_t)rw * D * SLOT;
+  double* red = red_all + (size_t)rw * rows_cap;
   const uint32_t wl_off = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)wl;
+  // The segments' weight pointers as a base and two offsets (scalar
+  // arithmetic per row, as in mv_b1).
+  [[maybe_unused]] const uint8_t* fw0 = nullptr;
+  [[maybe_unused]] ptrdiff_t fd1 = 0, fd2 = 0;
+  if constexpr (FUSE != 0) {
+    fw0 = fu.w0;
+    fd1 = fu.w1 - fu.w0;
+    fd2 = fu.w2 - fu.w0;
+  }
   auto copy_row = [&](int k, int sl) {
-    const int row = min(wg_begin + rw + min(k, max(nr, 1) - 1) * NRW, out_dim - 1);
-    const uint8_t* rp = w + (size_t)row * row_bytes;
+    const int kk = min(k, max(nr, 1) - 1);
+    const uint8_t* rp;
+    if constexpr (FUSE != 0) {
+      const int pair = min(wg_begin + rw + (kk >> 1) * NRW, out_dim / 2 - 1);
+      int r;
+      const int sg = fuse_seg(fu, __builtin_amdgcn_readfirstlane(2 * pair + (kk & 1)), r);
+      rp = fw0 + (sg == 0 ? 0 : sg == 1 ? fd1 : fd2) + (size_t)r * row_bytes;
+    } else {
+      const int row = min(wg_begin + rw + kk * NRW, out_dim - 1);
+      rp = w + (size_t)row * row_bytes;
+    }
 #pragma unroll
     for (int c = 0; c < NCR; c++) {
       const int o = 1024 * c + 16 * lane;
@@ -1283,6 +1385,13 @@ __global__ __launch_bounds__(64 * (kB1rXW + NRW)) void mv_b1r(const uint8_t* __r
   for (int t = 0; t < US; t += 4) {
     const uint4 v = lds4[(size_t)u * (US / 4) + t / 4];
     pr[t] = v.x; pr[t + 1] = v.y; pr[t + 2] = v.z; pr[t + 3] = v.w;
+  }
+  // norm-fused: 2^k of the x wave that staged unit u (its 8-element chunks
+  // c went to thread c mod 64 kB1rXW)
+  [[maybe_unused]] double unit_sc = 1.0;
+  if constexpr (FUSE >= 3) {
+    const int c0 = (FastUnit<F>::E / 8) * u;
+    unit_sc = ldexp(1.0, reinterpret_cast<const int*>(part)[kB1rXW + (c0 % (64 * kB1rXW)) / 64]);
   }
   for (int r0 = 0; r0 < nr; r0 += D) {  // 3.
 #pragma unroll
@@ -1309,16 +1418,44 @@ __global__ __launch_bounds__(64 * (kB1rXW + NRW)) void mv_b1r(const uint8_t* __r
       if (r0 + i + D < nr) copy_row(r0 + i + D, i);
       double a = 0.0;
       accumulate_dig<F>(raw, u, [&](int t) { return pr[t]; }, a);
+      if constexpr (FUSE >= 3) a *= unit_sc;
       a = wave_sum_l63_d(lane < U ? a : 0.0);
       if (lane == 63 && r0 + i < nr) red[r0 + i] = a;
     }
   }
   wait_vmcnt<0>();  // the last copies land before the workgroup's LDS is released
+  if constexpr (FUSE != 0) {
+    double inv = 1.0;
+    if constexpr (FUSE >= 3) {
+      float t = 0.f;
+#pragma unroll
+      for (int i = 0; i < kB1rXW; i++) t += part[i];
+      inv = (double)(1.0f / sqrtf(t / (float)keff + fu.norm_eps));
+    }
+    for (int k = lane; k < nu; k += 64)
+      fuse_store_pair(fu, 2 * (wg_begin + rw + k * NRW), (float)(red[2 * k] * inv), (float)(red[2 * k + 1] * inv));
+    return;
+  }
   double* yp = reinterpret_cast<double*>(y) + (size_t)blockIdx.y * out_dim;
   for (int r = lane; r < nr; r += 64) {
     if (sliced) yp[wg_begin + rw + r * NRW] = red[r];
     else y[wg_begin + rw + r * NRW] = (float)red[r];
   }
+}
+
+template <int F, int NCR, int D, int NRW>
+__global__ __launch_bounds__(64 * (kB1rXW + NRW)) void mv_b1r(const uint8_t* __restrict__ w,
+                                                              const float* __restrict__ x, float* __restrict__ y,
+                                                              int out_dim, int row_bpr, int slice_bpr, int q, int rem,
+                                                              int rows_cap) {
+  b1r_body<F, NCR, D, NRW, 0>(w, x, y, out_dim, row_bpr, slice_bpr, q, rem, rows_cap, NoFuse{});
+}
+
+// Whole rows only (one K slice); vrows virtual rows, q and rem in row pairs.
+template <int F, int NCR, int D, int NRW, int FUSE>
+__global__ __launch_bounds__(64 * (kB1rXW + NRW)) void mv_b1r_fused(const float* __restrict__ x, int vrows, int bpr,
+                                                                    int q, int rem, int rows_cap, MatvecFuse fu) {
+  b1r_body<F, NCR, D, NRW, FUSE>(nullptr, x, nullptr, vrows, bpr, bpr, q, rem, rows_cap, fu);
 }
 
 // Sums the K-slice partials (doubles, [slices][n]) in slice order and rounds
@@ -1902,9 +2039,11 @@ constexpr bool kRowSlots = F == kQ4_K || F == kQ4_0 || F == kQ8_0;
 // mv_b1r launch: whole rows of 3584-4096 elements (3 KB slots for Q4_K and
 // Q4_0, 5 KB for Q8_0), 16-byte aligned, from 8 rows per CU up to one round of
 // mv_b1 workgroups (10 rows per wave).  One row in flight per wave with 12 row
-// waves for 24-80 rows per CU, else two with 8 row waves (measured on 256
-// CUs: 4096, 14336 and 28672 rows).  hipErrorNotSupported when the shape does
-// not qualify.
+// waves from 24 rows per CU, else two with 8 row waves (measured on 256 CUs:
+// 4096, 14336 and 28672 rows; at 28672 x 4096 Q4_K, 112 rows per CU, 12 waves
+// 14.02-14.14 us against 14.18-14.20 us with 8; at 28672 x 8192 in two K
+// slices, 224 rows per CU, 26.87-27.10 against 27.93-27.94 us).
+// hipErrorNotSupported when the shape does not qualify.
 template <int F>
 hipError_t run_b1r(const uint8_t* w, const float* x, float* y, int out_dim, int bpr, hipStream_t s) {
   if constexpr (!kRowSlots<F>) {
@@ -1918,7 +2057,7 @@ hipError_t run_b1r(const uint8_t* w, const float* x, float* y, int out_dim, int 
     if (((uintptr_t)w % 16) != 0 || row_bytes % 16 != 0) return hipErrorNotSupported;
     const int cu = device_cu_count();
     if ((long)out_dim < 8L * cu || (long)out_dim > 10L * 12 * cu) return hipErrorNotSupported;
-    const bool one = (long)out_dim >= 24L * cu && (long)out_dim <= 80L * cu;
+    const bool one = (long)out_dim >= 24L * cu;
     const int nrw = one ? 12 : 8, d = one ? 1 : 2;
     const int n_wg = cu, q = out_dim / n_wg, rem = out_dim % n_wg;
     const int slice_bpr = bpr;
@@ -1934,6 +2073,49 @@ hipError_t run_b1r(const uint8_t* w, const float* x, float* y, int out_dim, int 
       return hipGetLastError();
     };
     return one ? go(mv_b1r<F, NCR, 1, 12>, 64 * (kB1rXW + 12)) : go(mv_b1r<F, NCR, 2, 8>, 64 * (kB1rXW + 8));
+  }
+}
+
+// Fused decode-layer launch on the LDS row slots (mv_b1r_fused): whole rows as
+// run_b1r takes them, every segment 16-byte aligned, at least one row pair per
+// CU.  hipErrorNotSupported when the shape does not qualify.
+template <int F, int MODE>
+hipError_t run_b1r_fused(const MatvecFuse& f, const float* x, int vrows, int bpr, hipStream_t s) {
+  if constexpr (!kRowSlots<F>) {
+    return hipErrorNotSupported;
+  } else {
+    constexpr int NCR = F == kQ8_0 ? 5 : 3;
+    const int keff = bpr * Geom<F>::bs, U = keff / FastUnit<F>::E;
+    const size_t row_bytes = (size_t)bpr * Geom<F>::bb;
+    if (U > 64 || keff > 4096 || row_bytes <= (size_t)1024 * (NCR - 1) || row_bytes > (size_t)1024 * NCR)
+      return hipErrorNotSupported;
+    for (const uint8_t* w : {f.w0, f.w1, f.w2})
+      if (w && (uintptr_t)w % 16 != 0) return hipErrorNotSupported;
+    if (row_bytes % 16 != 0) return hipErrorNotSupported;
+    const int cu = device_cu_count();
+    const int pairs = vrows / 2;
+    if (pairs < cu) return hipErrorNotSupported;
+    const int q = pairs / cu, rem = pairs % cu;
+    // Row waves and rows in flight per wave, measured (kernel in a HIP graph,
+    // Q4_K rows of 4096; (row waves, rows in flight) = (8, 2) / (12, 2) /
+    // (8, 1) / (12, 1)): QKV + RoPE 6144 rows, 24 per CU, 6.81 / 8.09 / 7.34 /
+    // 7.63 us; SwiGLU 2 x 14336 rows, 112 per CU, 14.83 / 13.94 / 16.02 /
+    // 13.82 us.  mv_b1 took 8.00 and 16.47 us.
+    const bool many = q >= 24;  // at least 48 rows per workgroup
+    const int nrw = many ? 12 : 8, d = many ? 1 : 2;
+    const int rows_cap = 2 * ((q + (rem ? 1 : 0) + nrw - 1) / nrw);
+    const size_t lds = (size_t)U * Dig<F>::US * sizeof(uint32_t) + (size_t)nrw * d * 1024 * NCR +
+                       (size_t)nrw * rows_cap * sizeof(double) + 2 * kB1rXW * sizeof(float);
+    if (lds > (size_t)lds_limit()) return hipErrorNotSupported;
+    auto go = [&](auto kern, int threads) {
+      hipError_t e = set_lds_attr(kern, lds);
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL(kern, dim3((unsigned)cu), dim3((unsigned)threads), lds, s, x, vrows, bpr, q, rem, rows_cap,
+                         f);
+      return hipGetLastError();
+    };
+    return many ? go(mv_b1r_fused<F, NCR, 1, 12, MODE>, 64 * (kB1rXW + 12))
+                : go(mv_b1r_fused<F, NCR, 2, 8, MODE>, 64 * (kB1rXW + 8));
   }
 }
 
@@ -1975,7 +2157,7 @@ hipError_t run_b1r_sliced_ncr(const uint8_t* w, const float* x, double* part, in
     const int cu = device_cu_count();
     const int n_wg = std::max(1, cu / slices), q = out_dim / n_wg, rem = out_dim % n_wg;
     if (q < 8) return hipErrorNotSupported;
-    const bool one = q >= 24 && q <= 80;
+    const bool one = q >= 24;
     const int nrw = one ? 12 : 8, d = one ? 1 : 2;
     const int rows_cap = (q + (rem ? 1 : 0) + nrw - 1) / nrw;
     const size_t lds = (size_t)U * Dig<F>::US * sizeof(uint32_t) + (size_t)nrw * d * 1024 * NCR +
@@ -2179,6 +2361,15 @@ hipError_t fused_dispatch(const MatvecFuse& f, int vrows, const float* x, int in
   if (U == 0 || (U != 64 && U != 128)) return hipSuccess;  // whole units per lane, one slice
   for (const uint8_t* w : {f.w0, f.w1, f.w2})
     if (w && !fast_aligned<F>(w, x, in_dim, bpr)) return hipSuccess;
+  {  // whole Q4_K / Q4_0 / Q8_0 rows of 3584-4096 elements: the LDS row slots
+    hipError_t e = !f.norm_w   ? run_b1r_fused<F, 2>(f, x, vrows, bpr, s)
+                   : f.norm_res ? run_b1r_fused<F, 4>(f, x, vrows, bpr, s)
+                                : run_b1r_fused<F, 3>(f, x, vrows, bpr, s);
+    if (e != hipErrorNotSupported) {
+      *used = e == hipSuccess;
+      return e;
+    }
+  }
   if (f.norm_w) {
     // the norm-fused forms: the row counts of the Llama-3-8B-sized layers (QKV
     // 6144 rows: 2 per wave; SwiGLU 2 x 14336: 10), one unit per lane; other

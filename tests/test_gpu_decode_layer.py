@@ -38,7 +38,7 @@ from ssdq import synth
 
 pytestmark = pytest.mark.gpu
 
-Q4_K, Q6_K, Q8_0, Q5_K, F32, F16 = ssdq.Q4_K, ssdq.Q6_K, ssdq.Q8_0, ssdq.Q5_K, ssdq.F32, ssdq.F16
+Q4_K, Q6_K, Q8_0, Q4_0, Q5_K, F32, F16 = ssdq.Q4_K, ssdq.Q6_K, ssdq.Q8_0, ssdq.Q4_0, ssdq.Q5_K, ssdq.F32, ssdq.F16
 EPS = 1e-5
 BLOCK = 16
 E2E_RTOL = 1e-4  # end-to-end bar, relative to the outputs' term scale
@@ -243,6 +243,10 @@ CASES = [
     # without the norm the hidden state feeds the projections as it is
     ("small_no_attn_norm_hd64", dict(SMALL, n_head=16, n_kv=4, hd=64, n_ff=2048), Q4KM, F32, ("attn_norm",), 33,
      10000.0, 1.0),
+    # the norm-fused kernels with Q8_0 q/k/v (2688 row pairs: 10 or 11 per CU
+    # on 256 CUs) and Q4_0 gate/up, a 3840-wide attention output
+    ("q8_0_qkv_30_heads_q4_0_ffn", dict(LLAMA, n_head=30, n_kv=6, n_ff=11008),
+     dict(Q4KM, attn_q=Q8_0, attn_k=Q8_0, attn_v=Q8_0, ffn_gate=Q4_0, ffn_up=Q4_0), F32, (), 130, 500000.0, 1.0),
 ]
 
 
@@ -294,6 +298,44 @@ def test_decode_layer_from_resident_weights(cid, shape, types, norm_type, drop, 
                 spread = effective_positions(L, st["q"], ref_pool, pos)
                 print(f"{cid} token {tok}: attention over {pos + 1} positions, effective {spread:.1f}")
                 assert spread > 1.5 or pos < 8, "one-hot attention: the case would not test the weighting"
+    finally:
+        store.close()
+        torch.cuda.synchronize()
+
+
+def test_decode_layer_hidden_near_fp32_max():
+    """Hidden values near FLT_MAX.  The norms' fp32 sums of squares overflow, so
+    the reference's inv_rms is 0 and its normalised vectors are 0: q, k, v and
+    the FFN are zero, and the layer output is hidden + the attention output.
+    The norm-fused kernels stage h * w and scale the dot products by inv_rms;
+    here some of those products overflow fp32 (|h| 3e38, w > 1.2), which they
+    stage scaled by a power of two, so the outputs are those zeros, not NaN."""
+    shape = dict(n_embd=4096, n_head=8, n_kv=2, hd=128, n_ff=2048)  # fused: 768 and 2048 row pairs
+    L = Layer(shape["n_embd"], shape["n_head"], shape["n_kv"], shape["hd"], shape["n_ff"], Q4KM, 4500)
+    kv_dim, theta, pos, layer = L.n_kv * L.hd, 500000.0, 40, 2
+    cfg = ssdq.layer_config(L.n_embd, L.n_head, L.n_kv, L.hd, L.n_ff, theta, EPS)
+    nbytes, offs = ssdq.decode_layer_scratch(cfg)
+    scratch = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+    hidden = synth.rng(4501).standard_normal(L.n_embd).astype(np.float32)
+    big = np.flatnonzero((L.norm("attn_norm") > 1.2) & (L.norm("ffn_norm") > 1.2))[:8]
+    assert big.size == 8
+    hidden[big] = np.where(np.arange(8) % 2, 3.0e38, -3.0e38).astype(np.float32)
+    pool = Pool(kv_dim, pos, 8, 16, (1.0, 1.0), 4502).upload()
+    ref_pool = Pool(kv_dim, pos, 8, 16, (1.0, 1.0), 4502)
+    store = ssdq.WeightStore()
+    try:
+        L.upload(store, layer)
+        announce("decode layer near FLT_MAX", "position", pos)
+        before = pool.from_device()
+        out, got = run_gpu_layer(store, layer, cfg, hidden, pos, pool, scratch, offs, step_sizes(L))
+        assert np.all(np.isfinite(out))
+        for name in ("attn_in", "q", "k", "v", "ffn_in", "ffn_h", "ffn_out"):
+            assert not np.any(got[name]), f"{name}: not all zero"
+        check_steps(L, hidden, pos, pool, before, pool.from_device(), got, out, theta, "near FLT_MAX")
+        ref, st = oracle_layer(L, hidden, pos, ref_pool, theta)
+        assert not np.any(st["q"]) and not np.any(st["ffn_h"])
+        err = np.abs(out.astype(np.float64) - ref)
+        assert np.all(err <= ATOL + E2E_RTOL * term_scale(L, hidden, st))
     finally:
         store.close()
         torch.cuda.synchronize()

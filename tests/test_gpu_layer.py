@@ -6,7 +6,7 @@ residual + RMSNorm (fused_post_attn_norm_f32_cpu, compute.rs:536-555), each
 with the projections through matvec_quantized_cpu.  Shapes are Llama-3-8B's
 (n_embd 4096, 32 query / 8 KV heads of 128, n_ff 14336, vocab 128256) plus
 cases that take the unfused path (mixed or extra types, rows of 80 units, odd
-row counts).
+row counts) and other head counts and FFN widths for the fused launches.
 
 Tolerance: the projections are held to |gpu - ref| <= 1e-4 + 1e-3 |ref| (with
 the exact-sum substitution of helpers.assert_close_attributed).  RoPE and
@@ -34,25 +34,33 @@ Q4_K, Q6_K, Q8_0, Q4_0, Q5_K = ssdq.Q4_K, ssdq.Q6_K, ssdq.Q8_0, ssdq.Q4_0, ssdq.
 
 
 QKV = [
-    # dtypes (q, k, v), n_embd, head_dim, position, theta
-    ((Q4_K, Q4_K, Q4_K), 4096, 128, 4000, 500000.0),   # fused
-    ((Q6_K, Q6_K, Q6_K), 4096, 128, 31999, 500000.0),  # fused, two units per lane
-    ((Q8_0, Q8_0, Q8_0), 4096, 128, 1, 10000.0),       # fused
-    ((Q4_K, Q4_K, Q6_K), 4096, 128, 77, 500000.0),     # mixed types: separate launches
-    ((Q5_K, Q5_K, Q5_K), 4096, 128, 12345, 500000.0),  # an extra type: separate launches
-    ((Q4_K, Q4_K, Q4_K), 4096, 0, 5, 10000.0),         # no rotation (fused_qkv_f32)
-    ((Q4_K, Q4_K, Q4_K), 5120, 128, 5, 10000.0),       # 80 units per row: separate launches
+    # dtypes (q, k, v), n_embd, head_dim, position, theta, query heads, KV heads
+    ((Q4_K, Q4_K, Q4_K), 4096, 128, 4000, 500000.0, 32, 8),   # fused
+    ((Q6_K, Q6_K, Q6_K), 4096, 128, 31999, 500000.0, 32, 8),  # fused, two units per lane
+    ((Q8_0, Q8_0, Q8_0), 4096, 128, 1, 10000.0, 32, 8),       # fused
+    ((Q4_K, Q4_K, Q6_K), 4096, 128, 77, 500000.0, 32, 8),     # mixed types: separate launches
+    ((Q5_K, Q5_K, Q5_K), 4096, 128, 12345, 500000.0, 32, 8),  # an extra type: separate launches
+    ((Q4_K, Q4_K, Q4_K), 4096, 0, 5, 10000.0, 32, 8),         # no rotation (fused_qkv_f32)
+    ((Q4_K, Q4_K, Q4_K), 5120, 128, 5, 10000.0, 32, 8),       # 80 units per row: separate launches
+    # fused, other head counts: (30, 6) is 2688 row pairs (10 or 11 per CU on
+    # 256 CUs), (10, 2) 896 pairs (3 or 4), (2, 1) 256 pairs (1 per CU), (1, 1)
+    # 128 pairs (fewer than the CUs: the kernel of register rows)
+    ((Q4_K, Q4_K, Q4_K), 4096, 128, 1210, 500000.0, 30, 6),
+    ((Q8_0, Q8_0, Q8_0), 4096, 128, 1210, 500000.0, 30, 6),
+    ((Q4_0, Q4_0, Q4_0), 4096, 128, 1070, 500000.0, 10, 2),
+    ((Q4_K, Q4_K, Q4_K), 4096, 128, 1014, 500000.0, 2, 1),
+    ((Q4_K, Q4_K, Q4_K), 4096, 128, 1007, 500000.0, 1, 1),
 ]
 
 
-@pytest.mark.parametrize("dts,n_embd,head_dim,position,theta", QKV)
-def test_qkv_rope(dts, n_embd, head_dim, position, theta):
-    q_dim, kv_dim = 32 * 128, 8 * 128
+@pytest.mark.parametrize("dts,n_embd,head_dim,position,theta,nh,nkv", QKV)
+def test_qkv_rope(dts, n_embd, head_dim, position, theta, nh, nkv):
+    q_dim, kv_dim = nh * 128, nkv * 128
     ws = [synth.quant_weights(dt, rows, n_embd, 700 + i) for i, (dt, rows) in
           enumerate(zip(dts, (q_dim, kv_dim, kv_dim)))]
     x = synth.normal_f32(n_embd, 701)
     q, k, v = empty_dev(q_dim, torch.float32), empty_dev(kv_dim, torch.float32), empty_dev(kv_dim, torch.float32)
-    announce("qkv rope", [ssdq.TYPE_NAMES[d] for d in dts], n_embd, head_dim, position)
+    announce("qkv rope", [ssdq.TYPE_NAMES[d] for d in dts], n_embd, head_dim, position, nh, nkv)
     rc = ssdq.qkv_rope(dts, [to_dev(w) for w in ws], to_dev(x), q, k, v, q_dim, kv_dim, n_embd, head_dim,
                        position, theta)
     assert rc == 0
@@ -70,17 +78,19 @@ def test_qkv_rope(dts, n_embd, head_dim, position, theta):
             assert_close_attributed(from_dev(got), ref, ex, f"{name} {ssdq.TYPE_NAMES[dt]}")
 
 
-SWIGLU = [(Q4_K, 4096), (Q6_K, 4096), (Q4_0, 4096), (Q5_K, 4096), (Q4_K, 5120)]
+# n_ff 14336 is 56 row pairs per CU on 256 CUs; 14000 is 54 or 55, 300 is 1
+# or 2, 200 fewer than the CUs (the kernel of register rows)
+SWIGLU = [(Q4_K, 4096, 14336), (Q6_K, 4096, 14336), (Q4_0, 4096, 14336), (Q8_0, 4096, 14336),
+          (Q5_K, 4096, 14336), (Q4_K, 5120, 14336), (Q4_K, 4096, 14000), (Q4_0, 4096, 300), (Q4_K, 4096, 200)]
 
 
-@pytest.mark.parametrize("dtype,n_embd", SWIGLU)
-def test_swiglu(dtype, n_embd):
-    n_ff = 14336
+@pytest.mark.parametrize("dtype,n_embd,n_ff", SWIGLU)
+def test_swiglu(dtype, n_embd, n_ff):
     wg = synth.quant_weights(dtype, n_ff, n_embd, 800)
     wu = synth.quant_weights(dtype, n_ff, n_embd, 801)
     x = synth.normal_f32(n_embd, 802)
     h = empty_dev(n_ff, torch.float32)
-    announce("swiglu", ssdq.TYPE_NAMES[dtype], n_embd)
+    announce("swiglu", ssdq.TYPE_NAMES[dtype], n_embd, n_ff)
     assert ssdq.swiglu(dtype, to_dev(wg), to_dev(wu), to_dev(x), h, n_ff, n_embd) == 0
     ref = o.swiglu(dtype, wg, wu, x, n_ff, n_embd)
     g = o.matvec_exact(dtype, wg, x, n_ff, n_embd)

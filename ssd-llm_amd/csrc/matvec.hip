@@ -368,6 +368,19 @@ __device__ __forceinline__ uint32_t plane_bytes(uint32_t a, uint32_t b, uint32_t
   return lo | hi;
 }
 
+// byte d of a, b, c, e to bytes 0-3 of out[d] (plane_bytes for d = 0..3 as one
+// 4 x 4 byte transpose: eight byte permutes)
+__device__ __forceinline__ void planes4(uint32_t a, uint32_t b, uint32_t c, uint32_t e, uint32_t out[4]) {
+  const uint32_t ab_lo = __builtin_amdgcn_perm(b, a, 0x05010400u);  // a0 b0 a1 b1
+  const uint32_t ab_hi = __builtin_amdgcn_perm(b, a, 0x07030602u);  // a2 b2 a3 b3
+  const uint32_t ce_lo = __builtin_amdgcn_perm(e, c, 0x05010400u);
+  const uint32_t ce_hi = __builtin_amdgcn_perm(e, c, 0x07030602u);
+  out[0] = __builtin_amdgcn_perm(ce_lo, ab_lo, 0x05040100u);  // a0 b0 c0 e0
+  out[1] = __builtin_amdgcn_perm(ce_lo, ab_lo, 0x07060302u);
+  out[2] = __builtin_amdgcn_perm(ce_hi, ab_hi, 0x05040100u);
+  out[3] = __builtin_amdgcn_perm(ce_hi, ab_hi, 0x07060302u);
+}
+
 // Staging of x in two phases so the x loads can be issued before the weight
 // prefetch: vector loads return in order, so x fetched after the weights would
 // wait for them.  One thread per 8 elements (the four threads of a 32-element
@@ -416,15 +429,16 @@ __device__ __forceinline__ void stage_store(const XChunks<SIT>& st, int keff, ui
     const bool live = c0 < total;
     const int r = rows > 1 ? c0 / nchunk : 0, c = c0 - r * nchunk;
     const float* v = st.v[it];
-    float m = 0.f;
-    bool bad = false;
+    float m = 0.f, z = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; j++) {
       m = fmaxf(m, fabsf(v[j]));
-      bad |= !(fabsf(v[j]) < INFINITY);  // NaN or infinity
+      z = fmaf(v[j], 0.f, z);  // NaN when an element is NaN or infinite
     }
     m = fmaxf(m, dpp_mov<0xB1>(m));
     m = fmaxf(m, dpp_mov<0x4E>(m));
+    z += dpp_mov<0xB1>(z);  // the group's four chunks
+    z += dpp_mov<0x4E>(z);
     const int k = c & 3;
     int e = 0;
     if (m > 0.f) (void)frexpf(m, &e);  // m < 2^e
@@ -444,9 +458,7 @@ __device__ __forceinline__ void stage_store(const XChunks<SIT>& st, int keff, ui
     }
     const double s_half = s + dpp_mov_d<0xB1>(s);  // sum over this 16-element half of the group
     s = s_half + dpp_mov_d<0x4E>(s_half);
-    bool gbad = bad;
-    gbad |= __shfl_xor(gbad ? 1 : 0, 1, 64) != 0;
-    gbad |= __shfl_xor(gbad ? 1 : 0, 2, 64) != 0;
+    const bool gbad = z != z;
     if (live) {
       const int g = c >> 2;
       uint32_t* rec = lds + (size_t)r * lds_stride + (size_t)(g / D::NG) * D::US + (g % D::NG) * D::GW;
@@ -461,15 +473,20 @@ __device__ __forceinline__ void stage_store(const XChunks<SIT>& st, int keff, ui
           for (int d = 0; d < kDigits; d++)
             pb[2 * (kDigits * ph + d)] =
                 (uint16_t)__builtin_amdgcn_perm(u[4 + ph], u[ph], (uint32_t)d | ((uint32_t)(4 + d) << 8) | 0x0C0C0000u);
-      } else
-#pragma unroll
-      for (int d = 0; d < kDigits; d++) {
+      } else {
+        static_assert(kDigits == 4, "one 4 x 4 byte transpose per half chunk");
+        uint32_t p0[4], p1[4];
         if (D::contig) {
-          pl[d] = plane_bytes(u[0], u[1], u[2], u[3], d);
-          pl[kDigits + d] = plane_bytes(u[4], u[5], u[6], u[7], d);
+          planes4(u[0], u[1], u[2], u[3], p0);
+          planes4(u[4], u[5], u[6], u[7], p1);
         } else {
-          pl[d] = plane_bytes(u[0], u[2], u[4], u[6], d);
-          pl[kDigits + d] = plane_bytes(u[1], u[3], u[5], u[7], d);
+          planes4(u[0], u[2], u[4], u[6], p0);
+          planes4(u[1], u[3], u[5], u[7], p1);
+        }
+#pragma unroll
+        for (int d = 0; d < kDigits; d++) {
+          pl[d] = p0[d];
+          pl[kDigits + d] = p1[d];
         }
       }
       constexpr bool halves = D::GW == 40;  // two 16-element sums per record

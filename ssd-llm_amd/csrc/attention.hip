@@ -856,8 +856,11 @@ hipError_t run_paged_mfma(const PagedAttnArgs& a, float* part, hipStream_t s) {
   };
   hipError_t e0;
   if constexpr (HD < 256) {  // head_dim 256 fits one wave per SIMD only: 4 waves
-    e0 = a.n_head_kv % 8 == 0 ? go(std::integral_constant<int, 8>{}, true)
-                              : go(std::integral_constant<int, 4>{}, a.n_head_kv % 4 == 0);
+    // 8 KV heads per workgroup, unless that leaves CUs without a workgroup
+    const long wg8 = (long)n_splits * (a.n_head_kv / 8) * n_hchunks * a.n_seq;
+    e0 = a.n_head_kv % 8 == 0 && wg8 >= device_cu_count()
+             ? go(std::integral_constant<int, 8>{}, true)
+             : go(std::integral_constant<int, 4>{}, a.n_head_kv % 4 == 0);
   } else {
     e0 = go(std::integral_constant<int, 4>{}, a.n_head_kv % 4 == 0);
   }

@@ -135,9 +135,13 @@ int api_fail(int code, const char* fmt, ...) {
 }
 int api_hip_fail(hipError_t e, const char* what) { return hip_fail(e, what); }
 int api_ok() { return ok(); }
-void api_rope_freqs(RopeFreq* r, int head_dim, float theta) {
-  for (int i = 0; i < 128; i++)
-    r->f[i] = i < head_dim / 2 ? 1.0f / powf(theta, 2.0f * (float)i / (float)head_dim) : 0.0f;
+void api_rope_table(RopeTable* r, int head_dim, float theta, int position) {
+  for (int i = 0; i < 128; i++) {
+    const float freq = i < head_dim / 2 ? 1.0f / powf(theta, 2.0f * (float)i / (float)head_dim) : 0.0f;
+    const float ang = (float)position * freq;
+    r->sn[i] = (float)sin((double)ang);
+    r->cs[i] = (float)cos((double)ang);
+  }
 }
 hipError_t api_workspace(size_t bytes, hipStream_t stream, void** out, int slot) {
   return workspace_get(bytes, stream, out, slot);
@@ -469,7 +473,9 @@ int ssdq_kv_swap_in_dev(const void* slots, const int32_t* block_ids, size_t n_bl
 namespace {
 // 1 / theta^(2i/head_dim) with the C library's powf, the call the reference's
 // rope_f32_multi_head makes (compute.rs:494)
-void rope_freqs(ssdq::RopeFreq* r, int head_dim, float theta) { ssdq::api_rope_freqs(r, head_dim, theta); }
+void rope_table(ssdq::RopeTable* r, int head_dim, float theta, int position) {
+  ssdq::api_rope_table(r, head_dim, theta, position);
+}
 }  // namespace
 
 int ssdq_rmsnorm_dev(const float* x, const float* residual, const float* weight, float eps,
@@ -494,8 +500,8 @@ int ssdq_qkv_rope_dev(int dtype_q, const void* wq, int dtype_k, const void* wk, 
   if (head_dim && ((head_dim & 1) || head_dim > 256 || q_dim % head_dim || kv_dim % head_dim))
     return fail(SSDQ_ERR_INVALID_ARG, "%s: head_dim must be even, at most 256 and divide q_dim and kv_dim", fn);
   hipStream_t s = (hipStream_t)stream;
-  ssdq::RopeFreq freq;
-  rope_freqs(&freq, head_dim ? (int)head_dim : 2, theta_base);
+  ssdq::RopeTable rope;
+  rope_table(&rope, head_dim ? (int)head_dim : 2, theta_base, (int)position);
   if (dtype_q == dtype_k && dtype_k == dtype_v && supported_quant(dtype_q)) {
     ssdq::MatvecFuse f{};
     f.w0 = (const uint8_t*)wq; f.w1 = (const uint8_t*)wk; f.w2 = (const uint8_t*)wv;
@@ -504,8 +510,7 @@ int ssdq_qkv_rope_dev(int dtype_q, const void* wq, int dtype_k, const void* wk, 
     f.start2 = (int)(q_dim + kv_dim);
     f.rope_mask = head_dim ? 3u : 0u;
     f.head_dim = head_dim ? (int)head_dim : 2;
-    f.position = (int)position;
-    f.freq = freq;
+    f.rope = rope;
     bool used = false;
     hipError_t e = ssdq::launch_matvec_fused(dtype_q, f, (int)(q_dim + 2 * kv_dim), x, n_embd, s, &used);
     if (e != hipSuccess) return hip_fail(e, fn);
@@ -523,8 +528,8 @@ int ssdq_qkv_rope_dev(int dtype_q, const void* wq, int dtype_k, const void* wk, 
     if (rc > worst) worst = rc;
   }
   if (head_dim) {
-    hipError_t e = ssdq::launch_rope(q, (int)q_dim, (int)head_dim, (int)position, freq, s);
-    if (e == hipSuccess) e = ssdq::launch_rope(k, (int)kv_dim, (int)head_dim, (int)position, freq, s);
+    hipError_t e = ssdq::launch_rope(q, (int)q_dim, (int)head_dim, rope, s);
+    if (e == hipSuccess) e = ssdq::launch_rope(k, (int)kv_dim, (int)head_dim, rope, s);
     if (e != hipSuccess) return hip_fail(e, fn);
   }
   if (worst != SSDQ_OK) {

@@ -44,11 +44,14 @@ hipError_t launch_matvec_ext(int dtype, const uint8_t* w, const float* x, float*
 // the rows of gate (w0) and up (w1) alternate and silu(g) * u goes to y0),
 // and RoPE on the output pairs of the segments in rope_mask.  Every segment
 // has an even row count.
-// RoPE frequencies theta^(-2i/head_dim), i < head_dim / 2, computed on the
-// host with the C library's powf (what the reference's f32::powf calls), so
-// the fp32 angle position * freq matches the reference bit for bit.
-struct RopeFreq {
-  float f[128];
+// RoPE of one position: sn[i], cs[i] = sin, cos of the fp32 angle position *
+// freq_i, freq_i = theta^(-2i/head_dim) for i < head_dim / 2, all on the host:
+// the frequency with the C library's powf (what the reference's f32::powf
+// calls), so the angle matches the reference bit for bit, and sin / cos in
+// double, rounded once to fp32.  The kernels only read the table.
+struct RopeTable {
+  float sn[128];
+  float cs[128];
 };
 
 struct MatvecFuse {
@@ -61,8 +64,8 @@ struct MatvecFuse {
   int start1, start2;  // first virtual row of segments 1 and 2 (INT_MAX: absent)
   int swiglu;
   unsigned rope_mask;
-  int head_dim, position;
-  RopeFreq freq;
+  int head_dim;
+  RopeTable rope;
   // RMSNorm of x in the kernel's staging (the norm-fused variants): x' = (x +
   // norm_res) * inv_rms * norm_w, inv_rms = 1 / sqrt(mean((x + norm_res)^2) +
   // norm_eps); workgroup 0 writes x + norm_res to hidden_out and x' to xn_out
@@ -88,7 +91,7 @@ hipError_t launch_matvec_fused(int dtype, const MatvecFuse& f, int total_rows, c
                                size_t in_dim, hipStream_t stream, bool* used);
 // Pieces of the unfused decode layer.
 // RoPE on n values (heads of head_dim), pairs (2i, 2i+1): rope_f32_multi_head.
-hipError_t launch_rope(float* v, int n, int head_dim, int position, const RopeFreq& freq, hipStream_t stream);
+hipError_t launch_rope(float* v, int n, int head_dim, const RopeTable& rope, hipStream_t stream);
 // h = silu(g) * u
 hipError_t launch_swiglu(const float* g, const float* u, float* h, int n, hipStream_t stream);
 // h += a (n floats)
@@ -197,6 +200,6 @@ int api_paged_attention_append(const float* q, int8_t* k_codes, float* k_scales,
                                size_t n_head_kv, size_t head_dim, size_t block_size, size_t max_blocks_per_seq,
                                size_t max_ctx, hipStream_t stream);
 // theta^(-2i/head_dim) with the C library's powf, as the reference computes them
-void api_rope_freqs(RopeFreq* r, int head_dim, float theta);
+void api_rope_table(RopeTable* r, int head_dim, float theta, int position);
 
 }  // namespace ssdq

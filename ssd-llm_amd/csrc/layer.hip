@@ -10,14 +10,12 @@
 namespace ssdq {
 namespace {
 
-__global__ __launch_bounds__(256) void rope_kernel(float* __restrict__ v, int n, int head_dim, int position,
-                                                   RopeFreq freq) {
+__global__ __launch_bounds__(256) void rope_kernel(float* __restrict__ v, int n, int head_dim, RopeTable rope) {
   const int p = blockIdx.x * blockDim.x + threadIdx.x;  // pair index
   const int r = 2 * p;
   if (r + 1 >= n) return;  // the reference's idx1 < len guard
   const int i = (r % head_dim) >> 1;
-  const float ang = (float)position * freq.f[i];  // freq from the host's powf
-  const float sn = (float)sin((double)ang), cs = (float)cos((double)ang);
+  const float sn = rope.sn[i], cs = rope.cs[i];
   const float x0 = v[r], x1 = v[r + 1];
   v[r] = x0 * cs - x1 * sn;
   v[r + 1] = x0 * sn + x1 * cs;
@@ -91,11 +89,10 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* x, const flo
 
 }  // namespace
 
-hipError_t launch_rope(float* v, int n, int head_dim, int position, const RopeFreq& freq, hipStream_t s) {
+hipError_t launch_rope(float* v, int n, int head_dim, const RopeTable& rope, hipStream_t s) {
   if (n <= 1) return hipSuccess;
   const int pairs = n / 2;
-  hipLaunchKernelGGL(rope_kernel, dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0, s, v, n, head_dim, position,
-                     freq);
+  hipLaunchKernelGGL(rope_kernel, dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0, s, v, n, head_dim, rope);
   return hipGetLastError();
 }
 

@@ -828,9 +828,7 @@ __device__ __forceinline__ void fuse_store_pair(const MatvecFuse& fu, int v, flo
   float o0 = a0, o1 = a1;
   if ((fu.rope_mask >> sg) & 1u) {
     const int i = (r % fu.head_dim) >> 1;
-    const float ang = (float)fu.position * fu.freq.f[i];
-    // sin / cos of the fp32 angle, rounded once from double
-    const float sn = (float)sin((double)ang), cs = (float)cos((double)ang);
+    const float sn = fu.rope.sn[i], cs = fu.rope.cs[i];
     o0 = a0 * cs - a1 * sn;
     o1 = a0 * sn + a1 * cs;
   }

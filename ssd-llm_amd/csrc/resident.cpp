@@ -382,8 +382,7 @@ int ssdq_decode_layer_dev(const ssdq_weights* w, uint32_t layer, const ssdq_laye
     f.start2 = (int)(q_dim + kv_dim);
     f.rope_mask = 3u;
     f.head_dim = (int)cfg->head_dim;
-    f.position = (int)position;
-    ssdq::api_rope_freqs(&f.freq, (int)cfg->head_dim, cfg->rope_theta);
+    ssdq::api_rope_table(&f.rope, (int)cfg->head_dim, cfg->rope_theta, (int)position);
     f.norm_w = g_attn;
     f.norm_eps = cfg->norm_eps;
     f.xn_out = xn;

@@ -149,6 +149,19 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+// Bytes d of a, b, c, e to bytes 0-3 of out[d], d = 0..3: a 4 x 4 byte
+// transpose in eight byte permutes (the digit planes of four 32-bit integers).
+__device__ __forceinline__ void planes4(uint32_t a, uint32_t b, uint32_t c, uint32_t e, uint32_t out[4]) {
+  const uint32_t ab_lo = __builtin_amdgcn_perm(b, a, 0x05010400u);  // a0 b0 a1 b1
+  const uint32_t ab_hi = __builtin_amdgcn_perm(b, a, 0x07030602u);  // a2 b2 a3 b3
+  const uint32_t ce_lo = __builtin_amdgcn_perm(e, c, 0x05010400u);
+  const uint32_t ce_hi = __builtin_amdgcn_perm(e, c, 0x07030602u);
+  out[0] = __builtin_amdgcn_perm(ce_lo, ab_lo, 0x05040100u);  // a0 b0 c0 e0
+  out[1] = __builtin_amdgcn_perm(ce_lo, ab_lo, 0x07060302u);
+  out[2] = __builtin_amdgcn_perm(ce_hi, ab_hi, 0x05040100u);
+  out[3] = __builtin_amdgcn_perm(ce_hi, ab_hi, 0x07060302u);
+}
+
 // INT8 code of one KV element (quantize_vectors_int8, src/ssd/block_swap.rs:36-60
 // = QuantizedVec::quantize, src/inference/quantized_kv_cache.rs:23-41):
 // clamp(round_half_away(v * inv), -127, 127), NaN -> 0 (Rust `as i8`), as a

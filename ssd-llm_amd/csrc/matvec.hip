@@ -361,26 +361,6 @@ __device__ __forceinline__ void pair_store(uint32_t* p, double d) {
   p[1] = (uint32_t)(b >> 32);
 }
 
-__device__ __forceinline__ uint32_t plane_bytes(uint32_t a, uint32_t b, uint32_t c, uint32_t e, int d) {
-  // byte d of a, b, c, e -> bytes 0, 1, 2, 3
-  const uint32_t lo = __builtin_amdgcn_perm(b, a, (uint32_t)d | ((uint32_t)(4 + d) << 8) | 0x0C0C0000u);
-  const uint32_t hi = __builtin_amdgcn_perm(e, c, 0x00000C0Cu | ((uint32_t)d << 16) | ((uint32_t)(4 + d) << 24));
-  return lo | hi;
-}
-
-// byte d of a, b, c, e to bytes 0-3 of out[d] (plane_bytes for d = 0..3 as one
-// 4 x 4 byte transpose: eight byte permutes)
-__device__ __forceinline__ void planes4(uint32_t a, uint32_t b, uint32_t c, uint32_t e, uint32_t out[4]) {
-  const uint32_t ab_lo = __builtin_amdgcn_perm(b, a, 0x05010400u);  // a0 b0 a1 b1
-  const uint32_t ab_hi = __builtin_amdgcn_perm(b, a, 0x07030602u);  // a2 b2 a3 b3
-  const uint32_t ce_lo = __builtin_amdgcn_perm(e, c, 0x05010400u);
-  const uint32_t ce_hi = __builtin_amdgcn_perm(e, c, 0x07030602u);
-  out[0] = __builtin_amdgcn_perm(ce_lo, ab_lo, 0x05040100u);  // a0 b0 c0 e0
-  out[1] = __builtin_amdgcn_perm(ce_lo, ab_lo, 0x07060302u);
-  out[2] = __builtin_amdgcn_perm(ce_hi, ab_hi, 0x05040100u);
-  out[3] = __builtin_amdgcn_perm(ce_hi, ab_hi, 0x07060302u);
-}
-
 // Staging of x in two phases so the x loads can be issued before the weight
 // prefetch: vector loads return in order, so x fetched after the weights would
 // wait for them.  One thread per 8 elements (the four threads of a 32-element

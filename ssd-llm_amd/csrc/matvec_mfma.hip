@@ -46,13 +46,6 @@ constexpr int kGRows = 16;  // weight rows per group (the MFMA's 16 columns)
 constexpr int kRq = 4;      // K quarters per group
 constexpr int kRgpw = 3;    // groups per workgroup
 
-// byte d of a, b, c, e -> bytes 0, 1, 2, 3
-__device__ __forceinline__ uint32_t gather_byte(uint32_t a, uint32_t b, uint32_t c, uint32_t e, int d) {
-  const uint32_t lo = __builtin_amdgcn_perm(b, a, (uint32_t)d | ((uint32_t)(4 + d) << 8) | 0x0C0C0000u);
-  const uint32_t hi = __builtin_amdgcn_perm(e, c, 0x00000C0Cu | ((uint32_t)d << 16) | ((uint32_t)(4 + d) << 24));
-  return lo | hi;
-}
-
 template <int NB, int NBLK>
 struct Q8R {
   static constexpr int NM = (NB + 3) / 4;
@@ -160,19 +153,17 @@ __global__ __launch_bounds__(768, 1) void mv_q8r(const uint8_t* __restrict__ w, 
     const int b = c / (NBLK * 4), j = (c >> 2) % NBLK, q = c & 3;
     const float v[8] = {xv[k][0].x, xv[k][0].y, xv[k][0].z, xv[k][0].w,
                         xv[k][1].x, xv[k][1].y, xv[k][1].z, xv[k][1].w};
-    float m = 0.f;
-    bool bad = false;
+    float m = 0.f, z = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       m = fmaxf(m, fabsf(v[i]));
-      bad |= !(fabsf(v[i]) < INFINITY);
+      z = fmaf(v[i], 0.f, z);  // NaN when an element is NaN or infinite
     }
     // the four chunks of a block are the lanes of one DPP quad
     m = fmaxf(m, dpp_mov<0xB1>(m));
     m = fmaxf(m, dpp_mov<0x4E>(m));
-    float badf = bad ? 1.f : 0.f;
-    badf = fmaxf(badf, dpp_mov<0xB1>(badf));
-    badf = fmaxf(badf, dpp_mov<0x4E>(badf));
+    z += dpp_mov<0xB1>(z);
+    z += dpp_mov<0x4E>(z);
     int e = 0;
     if (m > 0.f) (void)frexpf(m, &e);  // m < 2^e
     const int sh = min(30 - e, 149);  // 2^-sh stays a (subnormal) fp32 value
@@ -181,14 +172,15 @@ __global__ __launch_bounds__(768, 1) void mv_q8r(const uint8_t* __restrict__ w, 
     // digits
     uint32_t u[8];
 #pragma unroll
-    for (int i = 0; i < 8; i++) u[i] = (uint32_t)(int)rintf(ldexpf(v[i], sh)) + 0x80808080u;
+    for (int i = 0; i < 8; i++) u[i] = ((uint32_t)(int)rintf(ldexpf(v[i], sh)) + 0x80808080u) ^ 0x80808080u;
     if (c0 < chunks) {
       uint2* f = reinterpret_cast<uint2*>(frag + (size_t)j * P::FS + (b >> 2) * 512) + 16 * q + 4 * (b & 3);
+      uint32_t p0[4], p1[4];
+      planes4(u[0], u[1], u[2], u[3], p0);
+      planes4(u[4], u[5], u[6], u[7], p1);
 #pragma unroll
-      for (int d = 0; d < 4; d++)
-        f[d] = make_uint2(gather_byte(u[0], u[1], u[2], u[3], d) ^ 0x80808080u,
-                          gather_byte(u[4], u[5], u[6], u[7], d) ^ 0x80808080u);
-      if (q == 0) scl[j * NB + b] = badf != 0.f ? __builtin_nanf("") : ldexpf(1.0f, -sh);
+      for (int d = 0; d < 4; d++) f[d] = make_uint2(p0[d], p1[d]);
+      if (q == 0) scl[j * NB + b] = z != z ? __builtin_nanf("") : ldexpf(1.0f, -sh);
     }
   }
   __syncthreads();

@@ -1285,17 +1285,25 @@ __device__ __forceinline__ void b1r_body(const uint8_t* __restrict__ w, const fl
       // or, the sum of squares overflowing, zero), the wave stages h w 2^-k
       // instead (k from its largest product, rounded once from double), and
       // the row waves scale the partial sums of its units by 2^k.
-      const float qs = wave_sum(norm_sumsq<SIT, FUSE == 4>(st, st_r));  // st is h from here
+      // st is h from here; the wave's sum of squares is valid in lane 63
+      const float qs = wave_sum_l63(norm_sumsq<SIT, FUSE == 4>(st, st_r));
       XChunks<SIT> hw;
-      bool ovf = false;
+      float zz = 0.f;  // NaN when a product is infinite or NaN (rare: then the test below)
 #pragma unroll
       for (int it = 0; it < SIT; it++)
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-          const float h = st.v[it][j], g = st_w.v[it][j];
-          hw.v[it][j] = h * g;
-          ovf |= isinf(hw.v[it][j]) && isfinite(h) && isfinite(g);
+          hw.v[it][j] = st.v[it][j] * st_w.v[it][j];
+          zz = fmaf(hw.v[it][j], 0.f, zz);
         }
+      bool ovf = false;
+      if (__any(zz != zz)) {
+#pragma unroll
+        for (int it = 0; it < SIT; it++)
+#pragma unroll
+          for (int j = 0; j < 8; j++)
+            ovf |= isinf(hw.v[it][j]) && isfinite(st.v[it][j]) && isfinite(st_w.v[it][j]);
+      }
       int k = 0;
       if (__any(ovf)) {
         float e = -1000.f;  // bound on the exponent of every finite product
@@ -1316,7 +1324,7 @@ __device__ __forceinline__ void b1r_body(const uint8_t* __restrict__ w, const fl
             if (isfinite(h) && isfinite(g)) hw.v[it][j] = (float)((double)h * (double)g * sc);
           }
       }
-      if (lane == 0) {
+      if (lane == 63) {
         part[wave] = qs;
         reinterpret_cast<int*>(part)[kB1rXW + wave] = k;
       }

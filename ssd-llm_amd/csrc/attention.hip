@@ -304,6 +304,24 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v + dpp_f<0x128>(v);
 }
 
+// Sums and maxima over the same lane of the four 16-lane rows (lanes l, l ^ 16,
+// l ^ 32, l ^ 48), in every lane: the rows are exchanged by v_permlane16_swap
+// and v_permlane32_swap of a register with itself (VALU, no LDS), and the
+// operands of each step are those of x + shfl_xor(x, 16), then 32, so the
+// results are bit for bit the same.
+__device__ __forceinline__ float rows4_sum(float x) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
+__device__ __forceinline__ float rows4_max(float x) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+}
+
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
@@ -411,11 +429,8 @@ __global__ __launch_bounds__(64 * NWV, HD == 256 ? 1 : 8 / NWV) void paged_attn_
         m = fmaxf(m, fabsf(qv[mi][i]));
         bad |= !(fabsf(qv[mi][i]) < INFINITY);
       }
-    m = fmaxf(m, __shfl_xor(m, 16, 64));  // same head, the other dims
-    m = fmaxf(m, __shfl_xor(m, 32, 64));
-    int badi = bad ? 1 : 0;
-    badi |= __shfl_xor(badi, 16, 64);
-    badi |= __shfl_xor(badi, 32, 64);
+    m = rows4_max(m);  // same head, the other dims
+    const int badi = rows4_max(bad ? 1.f : 0.f) != 0.f;
     int e = 0;
     if (m > 0.f) (void)frexpf(m, &e);  // m < 2^e
     // the values are scaled (2^(30 - e) itself overflows below 2^-97); the
@@ -633,10 +648,7 @@ __global__ __launch_bounds__(64 * NWV, HD == 256 ? 1 : 8 / NWV) void paged_attn_
   for (int h = 0; h < 4; h++)
 #pragma unroll
     for (int d = 0; d < VD; d++) {
-      float a = acc[h][d];
-      a += __shfl_xor(a, 16, 64);
-      a += __shfl_xor(a, 32, 64);
-      acc[h][d] = a;
+      acc[h][d] = rows4_sum(acc[h][d]);
     }
   if (tg == 0) {
 #pragma unroll

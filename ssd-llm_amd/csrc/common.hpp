@@ -149,6 +149,29 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+// Sum / maximum over each 32-lane half of a wavefront, in every lane, with
+// the pairings of the steps x op shfl_xor(x, o), o = 1, 2, 4, 8, 16 (so a sum
+// is bit for bit the one those steps give): DPP quad_perm for o = 1, 2; after
+// them the four lanes of a quad agree, so row_half_mirror (lane i of 8 to
+// 7 - i) pairs the same quads as o = 4, and row_mirror the same halves of a
+// row as o = 8; v_permlane16_swap of a register with itself for o = 16.
+__device__ __forceinline__ float half_wave_sum(float v) {
+  v += dpp_mov<0xB1>(v);
+  v += dpp_mov<0x4E>(v);
+  v += dpp_mov<0x141>(v);  // row_half_mirror
+  v += dpp_mov<0x140>(v);  // row_mirror
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ float half_wave_max(float v) {
+  v = fmaxf(v, dpp_mov<0xB1>(v));
+  v = fmaxf(v, dpp_mov<0x4E>(v));
+  v = fmaxf(v, dpp_mov<0x141>(v));
+  v = fmaxf(v, dpp_mov<0x140>(v));
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+
 // Bytes d of a, b, c, e to bytes 0-3 of out[d], d = 0..3: a 4 x 4 byte
 // transpose in eight byte permutes (the digit planes of four 32-bit integers).
 __device__ __forceinline__ void planes4(uint32_t a, uint32_t b, uint32_t c, uint32_t e, uint32_t out[4]) {

@@ -112,8 +112,7 @@ __global__ __launch_bounds__(512) void gemm_prep_x(const uint16_t* __restrict__ 
     bad |= !(fabsf(a[i]) < INFINITY);
   }
   // the 32 threads of a row are one half of a wave
-#pragma unroll
-  for (int o = 1; o < 32; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  mx = half_wave_max(mx);
   int e = 10;
   if (mx > 0.f && mx < INFINITY) (void)frexpf(mx, &e);  // mx < 2^e
   const int sh = 10 - e;
@@ -127,18 +126,15 @@ __global__ __launch_bounds__(512) void gemm_prep_x(const uint16_t* __restrict__ 
     lost += fabsf(ldexpf(xs - (float)hv, -sh));  // the difference is exact in fp32
     sum += xs;
   }
-#pragma unroll
-  for (int o = 1; o < 32; o <<= 1) {
-    lost += __shfl_xor(lost, o, 64);
-    bad |= __shfl_xor(bad ? 1 : 0, o, 64) != 0;
-  }
+  lost = half_wave_sum(lost);
+  bad = half_wave_max(bad ? 1.f : 0.f) != 0.f;
   const bool flag = bad || mx > 65504.0f || !(lost <= kLossLimit);
   const int t = 4 * (sb >> 2) + q, c = sb & 3;
   tile[t * 64 + 16 * c + r] = h;
   // lanes 4i .. 4i+3 hold one sub-block; a + b is commutative, so all four
   // lanes end with the same sum
-  sum += __shfl_xor(sum, 1);
-  sum += __shfl_xor(sum, 2);
+  sum += dpp_mov<0xB1>(sum);  // the pairings of shfl_xor 1, 2
+  sum += dpp_mov<0x4E>(sum);
   const _Float16 hi = (_Float16)sum;
   const _Float16 lo = (_Float16)(sum - (float)hi);
   _Float16* o = xsp + ((size_t)m16 * nblk + blk) * 256;

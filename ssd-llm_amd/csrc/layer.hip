@@ -64,9 +64,9 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* x, const flo
     const float h = res ? x[i] + res[i] : x[i];
     q = fmaf(h, h, q);
   }
-  q = wave_sum(q);
+  q = wave_sum_l63(q);  // valid in lane 63
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (lane == 0) part[wave] = q;
+  if (lane == 63) part[wave] = q;
   __syncthreads();
   float t = 0.f;
   for (int i = 0; i < (int)(blockDim.x >> 6); i++) t += part[i];

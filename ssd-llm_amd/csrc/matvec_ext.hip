@@ -423,7 +423,7 @@ __global__ __launch_bounds__(256) void mv_ext(const uint8_t* __restrict__ w, con
     *reinterpret_cast<float4*>(dst) = v0;
     *reinterpret_cast<float4*>(dst + 4) = v1;
     float s = ((v0.x + v0.y) + (v0.z + v0.w)) + ((v1.x + v1.y) + (v1.z + v1.w));
-    s += __shfl_xor(s, 1, 64);
+    s += dpp_mov<0xB1>(s);  // lane i ^ 1, as shfl_xor(s, 1)
     if ((part & 1) == 0) xsum[((size_t)b * G + g) * 2 + (part >> 1)] = s;
   }
   __syncthreads();

@@ -1234,6 +1234,18 @@ __global__ __launch_bounds__(768) void mv_b1s_lds(const uint8_t* __restrict__ w,
 // (10.4 us: the copies stall at issue and the stream slows).
 constexpr int kB1rXW = 4;
 
+// Waits until at most pend rows of NCR copies each are pending (pend <= P,
+// wave-uniform; vmcnt takes an immediate, so one branch per count).
+template <int NCR, int P>
+__device__ __forceinline__ void wait_rows(int pend) {
+  if constexpr (P == 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (pend >= P) wait_vmcnt<NCR * P>();
+    else wait_rows<NCR, P - 1>(pend);
+  }
+}
+
 // The body of mv_b1r and of its decode-layer fusion mv_b1r_fused (FUSE as in
 // mv_b1: 2 row pairs with the RoPE / SwiGLU epilogue, 3 and 4 the same with an
 // RMSNorm of x, 4 of x + a residual).  Fused, the workgroup's units are row
@@ -1400,12 +1412,11 @@ __device__ __forceinline__ void b1r_body(const uint8_t* __restrict__ w, const fl
 #pragma unroll
     for (int i = 0; i < D; i++) {
       // Row r0 + i has landed once only the copies issued after it are
-      // pending: those of row r0 + i + 1 (D = 2), unless that row is past the
-      // run and past the first D (refills past the run are not issued; the
-      // first D rows are, clamped).
+      // pending: those of rows r0 + i + 1 .. r0 + i + D - 1 that were issued
+      // (the first D rows always are, clamped; refills past the run are not),
+      // that is min(D - 1, max(D, nr) - 1 - (r0 + i)) rows.
       __builtin_amdgcn_sched_barrier(0);
-      if (D == 1 || r0 + i + 1 >= max(D, nr)) wait_vmcnt<0>();
-      else wait_vmcnt<NCR * (D - 1)>();
+      wait_rows<NCR, D - 1>(min(D - 1, max(D, nr) - 1 - (r0 + i)));
       __builtin_amdgcn_sched_barrier(0);
       uint32_t raw[NW];
       load_unit<F>(wl + i * SLOT, u, raw);

@@ -1214,11 +1214,16 @@ __global__ __launch_bounds__(768) void mv_b1s_lds(const uint8_t* __restrict__ w,
 // (clamped repeats, not stored); later rows past the run are not.
 //
 // Schedule (per-wave wall-clock timelines on MI355X, 14336 x 4096 Q4_K):
-//   1. The x waves request x, then every wave meets at a barrier: every x load
-//      is queued in the CU before any weight copy (x lands at ~0.55 us from the
-//      first wave's start instead of ~1 us).
+//   1. The x waves request x; the row waves sleep a few hundred cycles first,
+//      so the x loads are queued in the CU ahead of the weight copies (x lands
+//      at ~0.55 us from the first wave's start instead of ~1 us).  A barrier
+//      there instead made the x waves wait for the last row wave to launch
+//      before converting (measured: 14336 x 4096 Q4_K 8.10 -> 8.07 us, 4096 x
+//      4096 Q4_0 4.50 -> 4.47, 11008 x 4096 Q8_0 9.20 -> 9.11, and with the
+//      longer sleep of the norm-fused launches, whose x waves also request the
+//      residual and the norm weights, the decode layer 55.5 -> 54.9 us).
 //   2. The row waves copy their first D rows.  The x waves wait for x, write
-//      the digit planes and meet the row waves at a second (LDS-only) barrier.
+//      the digit planes and meet the row waves at an LDS-only barrier.
 //      x is fetched by waves that issue no copies, so the compiler's wait for
 //      x, which cannot count the copies (inline assembly), drains nothing of
 //      the weight stream; staging x (~0.8 us) hides under the first rows'
@@ -1252,7 +1257,8 @@ __device__ __forceinline__ void wait_rows(int pend) {
 // pairs (out_dim virtual rows, q and rem count pairs): row wave v takes pairs
 // v, v + NRW, ... and copies both rows of each, so it holds both dot products
 // of its pairs for the epilogue.  With the norm, the x waves also load the
-// residual and the norm weights before the first barrier.
+// residual and the norm weights, and the row waves sleep longer before their
+// first copies.
 template <int F, int NCR, int D, int NRW, int FUSE>
 __device__ __forceinline__ void b1r_body(const uint8_t* __restrict__ w, const float* __restrict__ x,
                                          float* __restrict__ y, int out_dim, int row_bpr, int slice_bpr, int q,
@@ -1288,7 +1294,6 @@ __device__ __forceinline__ void b1r_body(const uint8_t* __restrict__ w, const fl
       if constexpr (FUSE == 4) stage_load<SIT>(fu.norm_res, keff, st_r, 64 * kB1rXW);
       stage_load<SIT>(fu.norm_w, keff, st_w, 64 * kB1rXW);
     }
-    __builtin_amdgcn_s_barrier();  // 1.
     if constexpr (FUSE >= 3) {
       // Every output is linear in x' = h inv_rms w, so the x waves stage h w
       // at once and the row waves multiply their dot products by inv_rms,
@@ -1354,7 +1359,7 @@ __device__ __forceinline__ void b1r_body(const uint8_t* __restrict__ w, const fl
     lds_barrier();  // 2.
     return;
   }
-  __builtin_amdgcn_s_barrier();  // 1.
+  __builtin_amdgcn_s_sleep(FUSE >= 3 ? 6 : 2);  // 1. (64 cycles per unit)
   const int rw = wave - kB1rXW;
   const int b = (int)blockIdx.x;
   constexpr int UR = FUSE != 0 ? 2 : 1;  // rows per unit of work

@@ -25,6 +25,17 @@ hipError_t launch_matvec(int dtype, const uint8_t* w, const float* x, float* y, 
 hipError_t launch_matvec_acc(int dtype, const uint8_t* w, const float* x, float* acc, float* y, size_t out_dim,
                              size_t in_dim, hipStream_t s, void* workspace, size_t workspace_bytes,
                              const float* acc_in = nullptr);
+// While one is alive on a host thread, batch-1 matvecs launched from that
+// thread treat x as just written by the previous kernel (not resident in this
+// XCD's L2) and pick the form that requests it from more waves.  A hint for
+// kernel selection only: results are the same bit for bit.
+struct FreshX {
+  FreshX();
+  ~FreshX();
+  FreshX(const FreshX&) = delete;
+  FreshX& operator=(const FreshX&) = delete;
+};
+bool fresh_x();
 // Device workspace launch_matvec uses for these operands (batch-1 K slices).
 size_t matvec_workspace_bytes(int dtype, const void* w, const float* x, size_t out_dim,
                               size_t in_dim, size_t batch);

@@ -1204,9 +1204,10 @@ __global__ __launch_bounds__(768) void mv_b1s_lds(const uint8_t* __restrict__ w,
 }
 
 // Batch-1 matvec of whole rows (at most 64 units) with the rows copied into
-// LDS and x staged by waves of its own.  One workgroup per CU of kB1rXW "x
-// waves" and NRW "row waves".  The workgroup owns a contiguous range of rows;
-// row wave v takes rows v, v + NRW, v + 2 NRW, ... of it, so the workgroup's
+// LDS and x staged by waves of its own.  One workgroup per CU of XW "x waves"
+// (kB1rXW, or kB1rXWCold where x is cold) and NRW "row waves".  The
+// workgroup owns a contiguous range of rows; row wave v takes rows v, v + NRW,
+// v + 2 NRW, ... of it, so the workgroup's
 // copies in flight cover consecutive rows.  Each row wave keeps D row slots of
 // NCR KB and copies a row into a slot with NCR contiguous 1 KB nontemporal
 // copies (lanes past the row masked off; lane 0 always issues, so every row
@@ -1238,6 +1239,13 @@ __global__ __launch_bounds__(768) void mv_b1s_lds(const uint8_t* __restrict__ w,
 // wave's run (8.2-8.8 us) and requesting every row of the run at the start
 // (10.4 us: the copies stall at issue and the stream slows).
 constexpr int kB1rXW = 4;
+// x waves where x is cold: the fused decode-layer launches with 8 row waves
+// (their x is the layer input, just written) and plain launches under FreshX.
+// With x resident in L2 (a matvec repeated on one x) four x waves are faster:
+// 4096 x 4096 Q4_0 4.49 against 4.56 us with eight; where x was just written
+// by the previous kernel, eight request it sooner: the decode layer's output
+// projection and QKV + RoPE launches, 54.9 -> 54.0 us per layer (A/B, two runs).
+constexpr int kB1rXWCold = 8;
 
 // Waits until at most pend rows of NCR copies each are pending (pend <= P,
 // wave-uniform; vmcnt takes an immediate, so one branch per count).
@@ -1259,11 +1267,11 @@ __device__ __forceinline__ void wait_rows(int pend) {
 // of its pairs for the epilogue.  With the norm, the x waves also load the
 // residual and the norm weights, and the row waves sleep longer before their
 // first copies.
-template <int F, int NCR, int D, int NRW, int FUSE>
+template <int F, int NCR, int D, int NRW, int FUSE, int XW = kB1rXW>
 __device__ __forceinline__ void b1r_body(const uint8_t* __restrict__ w, const float* __restrict__ x,
                                          float* __restrict__ y, int out_dim, int row_bpr, int slice_bpr, int q,
                                          int rem, int rows_cap, const FuseArg<FUSE>& fu) {
-  constexpr int US = Dig<F>::US, NW = FastUnit<F>::NW, SLOT = 1024 * NCR, SIT = 2;
+  constexpr int US = Dig<F>::US, NW = FastUnit<F>::NW, SLOT = 1024 * NCR, SIT = 8 / XW;
   static_assert(NCR * (D - 1) < 64, "vmcnt range");
   extern __shared__ uint4 lds4[];
   uint32_t* lds = reinterpret_cast<uint32_t*>(lds4);
@@ -1286,13 +1294,13 @@ __device__ __forceinline__ void b1r_body(const uint8_t* __restrict__ w, const fl
   // norm-fused: the x waves' sums of squares and staging exponents, after the
   // row sums of every row wave
   [[maybe_unused]] float* const part = reinterpret_cast<float*>(red_all + (size_t)NRW * rows_cap);
-  if (wave < kB1rXW) {
+  if (wave < XW) {
     XChunks<SIT> st;
-    stage_load<SIT>(x, keff, st, 64 * kB1rXW);
+    stage_load<SIT>(x, keff, st, 64 * XW);
     [[maybe_unused]] XChunks<SIT> st_r, st_w;
     if constexpr (FUSE >= 3) {
-      if constexpr (FUSE == 4) stage_load<SIT>(fu.norm_res, keff, st_r, 64 * kB1rXW);
-      stage_load<SIT>(fu.norm_w, keff, st_w, 64 * kB1rXW);
+      if constexpr (FUSE == 4) stage_load<SIT>(fu.norm_res, keff, st_r, 64 * XW);
+      stage_load<SIT>(fu.norm_w, keff, st_w, 64 * XW);
     }
     if constexpr (FUSE >= 3) {
       // Every output is linear in x' = h inv_rms w, so the x waves stage h w
@@ -1343,24 +1351,24 @@ __device__ __forceinline__ void b1r_body(const uint8_t* __restrict__ w, const fl
       }
       if (lane == 63) {
         part[wave] = qs;
-        reinterpret_cast<int*>(part)[kB1rXW + wave] = k;
+        reinterpret_cast<int*>(part)[XW + wave] = k;
       }
-      stage_store<F, SIT>(hw, keff, lds, 64 * kB1rXW);
+      stage_store<F, SIT>(hw, keff, lds, 64 * XW);
       lds_barrier();  // 2.
       if (blockIdx.x == 0) {  // h and x' to the step outputs
         float t = 0.f;
 #pragma unroll
-        for (int i = 0; i < kB1rXW; i++) t += part[i];
-        norm_apply<SIT>(st, st_w, 1.0f / sqrtf(t / (float)keff + fu.norm_eps), keff, 64 * kB1rXW, fu);
+        for (int i = 0; i < XW; i++) t += part[i];
+        norm_apply<SIT>(st, st_w, 1.0f / sqrtf(t / (float)keff + fu.norm_eps), keff, 64 * XW, fu);
       }
       return;
     }
-    stage_store<F, SIT>(st, keff, lds, 64 * kB1rXW);
+    stage_store<F, SIT>(st, keff, lds, 64 * XW);
     lds_barrier();  // 2.
     return;
   }
   __builtin_amdgcn_s_sleep(FUSE >= 3 ? 6 : 2);  // 1. (64 cycles per unit)
-  const int rw = wave - kB1rXW;
+  const int rw = wave - XW;
   const int b = (int)blockIdx.x;
   constexpr int UR = FUSE != 0 ? 2 : 1;  // rows per unit of work
   const int wg_begin = b * q + min(b, rem), wg_units = q + (b < rem ? 1 : 0);
@@ -1407,11 +1415,11 @@ __device__ __forceinline__ void b1r_body(const uint8_t* __restrict__ w, const fl
     pr[t] = v.x; pr[t + 1] = v.y; pr[t + 2] = v.z; pr[t + 3] = v.w;
   }
   // norm-fused: 2^k of the x wave that staged unit u (its 8-element chunks
-  // c went to thread c mod 64 kB1rXW)
+  // c went to thread c mod 64 XW)
   [[maybe_unused]] double unit_sc = 1.0;
   if constexpr (FUSE >= 3) {
     const int c0 = (FastUnit<F>::E / 8) * u;
-    unit_sc = ldexp(1.0, reinterpret_cast<const int*>(part)[kB1rXW + (c0 % (64 * kB1rXW)) / 64]);
+    unit_sc = ldexp(1.0, reinterpret_cast<const int*>(part)[XW + (c0 % (64 * XW)) / 64]);
   }
   for (int r0 = 0; r0 < nr; r0 += D) {  // 3.
 #pragma unroll
@@ -1448,7 +1456,7 @@ __device__ __forceinline__ void b1r_body(const uint8_t* __restrict__ w, const fl
     if constexpr (FUSE >= 3) {
       float t = 0.f;
 #pragma unroll
-      for (int i = 0; i < kB1rXW; i++) t += part[i];
+      for (int i = 0; i < XW; i++) t += part[i];
       inv = (double)(1.0f / sqrtf(t / (float)keff + fu.norm_eps));
     }
     for (int k = lane; k < nu; k += 64)
@@ -1462,19 +1470,19 @@ __device__ __forceinline__ void b1r_body(const uint8_t* __restrict__ w, const fl
   }
 }
 
-template <int F, int NCR, int D, int NRW>
-__global__ __launch_bounds__(64 * (kB1rXW + NRW)) void mv_b1r(const uint8_t* __restrict__ w,
+template <int F, int NCR, int D, int NRW, int XW = kB1rXW>
+__global__ __launch_bounds__(64 * (XW + NRW)) void mv_b1r(const uint8_t* __restrict__ w,
                                                               const float* __restrict__ x, float* __restrict__ y,
                                                               int out_dim, int row_bpr, int slice_bpr, int q, int rem,
                                                               int rows_cap) {
-  b1r_body<F, NCR, D, NRW, 0>(w, x, y, out_dim, row_bpr, slice_bpr, q, rem, rows_cap, NoFuse{});
+  b1r_body<F, NCR, D, NRW, 0, XW>(w, x, y, out_dim, row_bpr, slice_bpr, q, rem, rows_cap, NoFuse{});
 }
 
 // Whole rows only (one K slice); vrows virtual rows, q and rem in row pairs.
-template <int F, int NCR, int D, int NRW, int FUSE>
-__global__ __launch_bounds__(64 * (kB1rXW + NRW)) void mv_b1r_fused(const float* __restrict__ x, int vrows, int bpr,
+template <int F, int NCR, int D, int NRW, int FUSE, int XW = kB1rXW>
+__global__ __launch_bounds__(64 * (XW + NRW)) void mv_b1r_fused(const float* __restrict__ x, int vrows, int bpr,
                                                                     int q, int rem, int rows_cap, MatvecFuse fu) {
-  b1r_body<F, NCR, D, NRW, FUSE>(nullptr, x, nullptr, vrows, bpr, bpr, q, rem, rows_cap, fu);
+  b1r_body<F, NCR, D, NRW, FUSE, XW>(nullptr, x, nullptr, vrows, bpr, bpr, q, rem, rows_cap, fu);
 }
 
 // Sums the K-slice partials (doubles, [slices][n]) in slice order and rounds
@@ -2051,6 +2059,16 @@ hipError_t run_b1s_lds_rows(const uint8_t* w, const float* x, float* y, int out_
   }
 }
 
+thread_local int g_fresh_x = 0;
+
+}  // namespace
+
+FreshX::FreshX() { ++g_fresh_x; }
+FreshX::~FreshX() { --g_fresh_x; }
+bool fresh_x() { return g_fresh_x > 0; }
+
+namespace {
+
 // Types whose whole rows of 4096 elements take mv_b1r (LDS row slots).
 template <int F>
 constexpr bool kRowSlots = F == kQ4_K || F == kQ4_0 || F == kQ8_0;
@@ -2091,6 +2109,7 @@ hipError_t run_b1r(const uint8_t* w, const float* x, float* y, int out_dim, int 
                          q, rem, rows_cap);
       return hipGetLastError();
     };
+    if (!one && fresh_x()) return go(mv_b1r<F, NCR, 2, 8, kB1rXWCold>, 64 * (kB1rXWCold + 8));
     return one ? go(mv_b1r<F, NCR, 1, 12>, 64 * (kB1rXW + 12)) : go(mv_b1r<F, NCR, 2, 8>, 64 * (kB1rXW + 8));
   }
 }
@@ -2124,7 +2143,7 @@ hipError_t run_b1r_fused(const MatvecFuse& f, const float* x, int vrows, int bpr
     const int nrw = many ? 12 : 8, d = many ? 1 : 2;
     const int rows_cap = 2 * ((q + (rem ? 1 : 0) + nrw - 1) / nrw);
     const size_t lds = (size_t)U * Dig<F>::US * sizeof(uint32_t) + (size_t)nrw * d * 1024 * NCR +
-                       (size_t)nrw * rows_cap * sizeof(double) + 2 * kB1rXW * sizeof(float);
+                       (size_t)nrw * rows_cap * sizeof(double) + 2 * kB1rXWCold * sizeof(float);
     if (lds > (size_t)lds_limit()) return hipErrorNotSupported;
     auto go = [&](auto kern, int threads) {
       hipError_t e = set_lds_attr(kern, lds);
@@ -2134,7 +2153,7 @@ hipError_t run_b1r_fused(const MatvecFuse& f, const float* x, int vrows, int bpr
       return hipGetLastError();
     };
     return many ? go(mv_b1r_fused<F, NCR, 1, 12, MODE>, 64 * (kB1rXW + 12))
-                : go(mv_b1r_fused<F, NCR, 2, 8, MODE>, 64 * (kB1rXW + 8));
+                : go(mv_b1r_fused<F, NCR, 2, 8, MODE, kB1rXWCold>, 64 * (kB1rXWCold + 8));
   }
 }
 

@@ -415,7 +415,10 @@ int ssdq_decode_layer_dev(const ssdq_weights* w, uint32_t layer, const ssdq_laye
                                       slot_mapping, att, 1, cfg->n_head, cfg->n_head_kv, cfg->head_dim, block_size,
                                       max_blocks_per_seq, max_ctx, s)))
     return worst;
-  if (take(ssdq_matvec_dev(t_o->dtype, t_o->dev, att, ao, n_embd, q_dim, 1, stream))) return worst;
+  {
+    const ssdq::FreshX fresh;  // att was just written by the attention combine
+    if (take(ssdq_matvec_dev(t_o->dtype, t_o->dev, att, ao, n_embd, q_dim, 1, stream))) return worst;
+  }
 
   // 6. hidden += attn_output, ffn_input = rms_norm(hidden, ffn_norm)
   // (fused_post_attn_norm_f32, transformer.rs:346-359); without ffn_norm the

@@ -338,18 +338,28 @@ __device__ __forceinline__ void stage_x(const float* __restrict__ x, int in_dim,
 // the same rounded x as the codes' term.
 constexpr int kDigits = 4;
 constexpr int kDigScale = 8 * kDigits, kDigSum = kDigScale + 1;
+// A unit's record holds NG group records of GW dwords; records of consecutive
+// units are US dwords apart, 4 more than NG GW: every lane reads its own
+// unit's record with 16-byte LDS loads, and a stride of 72 or 40 dwords (8 mod
+// 32) put lanes l and l + 4 on the same banks, a 2-way conflict over the ~18
+// KB each row wave reads before its first row.  Strides of 76, 44 and 84
+// dwords (12, 12 and 20 mod 32) give any 8 consecutive lanes distinct banks
+// (the readers load the 4 padding dwords too: trimming them measured no
+// faster).  Measured (row-slot kernels, A/B, two runs): 14336 x 4096 Q4_K 8.16-8.25 ->
+// 7.71-7.89 us, 4096 x 4096 Q4_0 4.46 -> 4.38 us, 4096 x 14336 Q4_K 10.67 ->
+// 10.35 us, the decode layer 54.0 -> 52.9 us.
 template <int F> struct Dig;
-template <> struct Dig<kQ4_K> { static constexpr int NG = 2, GW = 36, US = 72; static constexpr bool contig = false; };
-template <> struct Dig<kQ4_0> { static constexpr int NG = 2, GW = 36, US = 72; static constexpr bool contig = false; };
-template <> struct Dig<kQ5_K> { static constexpr int NG = 2, GW = 36, US = 72; static constexpr bool contig = false; };
-template <> struct Dig<kQ8_0> { static constexpr int NG = 2, GW = 36, US = 72; static constexpr bool contig = true; };
-template <> struct Dig<kQ8_K> { static constexpr int NG = 2, GW = 36, US = 72; static constexpr bool contig = true; };
-template <> struct Dig<kQ6_K> { static constexpr int NG = 1, GW = 40, US = 40; static constexpr bool contig = false; };
+template <> struct Dig<kQ4_K> { static constexpr int NG = 2, GW = 36, US = 76; static constexpr bool contig = false; };
+template <> struct Dig<kQ4_0> { static constexpr int NG = 2, GW = 36, US = 76; static constexpr bool contig = false; };
+template <> struct Dig<kQ5_K> { static constexpr int NG = 2, GW = 36, US = 76; static constexpr bool contig = false; };
+template <> struct Dig<kQ8_0> { static constexpr int NG = 2, GW = 36, US = 76; static constexpr bool contig = true; };
+template <> struct Dig<kQ8_K> { static constexpr int NG = 2, GW = 36, US = 76; static constexpr bool contig = true; };
+template <> struct Dig<kQ6_K> { static constexpr int NG = 1, GW = 40, US = 44; static constexpr bool contig = false; };
 // Q2_K: a group record holds two 16-element sub-blocks, each as 4 phase planes
 // (elements p, p+4, p+8, p+12: the bytes a code dword yields for shift 2p) x 4
 // digits, then the scale and the two sub-block sums as for Q6_K.
-template <> struct Dig<kQ2_K> { static constexpr int NG = 2, GW = 40, US = 80; static constexpr bool contig = false; };
-template <> struct Dig<kQ3_K> { static constexpr int NG = 2, GW = 40, US = 80; static constexpr bool contig = false; };
+template <> struct Dig<kQ2_K> { static constexpr int NG = 2, GW = 40, US = 84; static constexpr bool contig = false; };
+template <> struct Dig<kQ3_K> { static constexpr int NG = 2, GW = 40, US = 84; static constexpr bool contig = false; };
 
 // A double kept in two dwords of a group record.
 __device__ __forceinline__ double pair_value(uint32_t lo, uint32_t hi) {
@@ -1938,7 +1948,7 @@ bool fast_aligned(const uint8_t* w, const float* x, int in_dim, int bpr) {
 // (144-160 VGPRs) spill, and scratch accesses would also break the exact wait
 // counts of the kernels that stream rows through LDS.
 template <int F>
-constexpr bool kTwoUnits = Dig<F>::US <= 40;
+constexpr bool kTwoUnits = Dig<F>::NG == 1;
 
 // Row geometry of the batch-1 kernel: rows of up to 128 units run whole (one
 // wave per row stream); longer rows are cut into slices of at most 64 units.
